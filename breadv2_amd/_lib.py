@@ -1,0 +1,139 @@
+"""ctypes binding of libbread_moe.so (the C ABI declared in include/bread_moe.h).
+
+The library is the product: every compute call goes to the HIP kernels in it.
+There is no CPU fallback; if the shared object is missing, importing this
+module raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_uint16, c_uint64, c_void_p
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libbread_moe.so")
+
+QTYPE_F32 = 0
+QTYPE_F16 = 1
+QTYPE_Q8_0 = 8
+QTYPE_Q4_K = 12
+QTYPE_Q6_K = 14
+
+QK_K = 256
+Q4K_BLOCK_BYTES = 144
+Q6K_BLOCK_BYTES = 210
+Q8_0_BLOCK_ELEMS = 32
+Q8_0_BLOCK_BYTES = 34
+
+OK = 0
+ERR_ARG = -1
+ERR_QTYPE = -2
+ERR_SHAPE = -3
+ERR_ALIGN = -4
+ERR_HIP = -5
+ERR_NOMEM = -6
+ERR_CAPACITY = -7
+ERR_DEVICE = -8
+
+
+class BreadError(RuntimeError):
+    def __init__(self, status: int, where: str):
+        self.status = status
+        super().__init__(f"{where}: {status_str(status)} ({status})")
+
+
+class MoeShape(ctypes.Structure):
+    _fields_ = [
+        ("hidden", c_int),
+        ("expert_inter", c_int),
+        ("shared_inter", c_int),
+        ("n_experts", c_int),
+        ("top_k", c_int),
+        ("rms_eps", c_float),
+    ]
+
+
+class MoeLayer(ctypes.Structure):
+    _fields_ = [
+        ("gate_exps", c_void_p),
+        ("up_exps", c_void_p),
+        ("down_exps", c_void_p),
+        ("gate_expert_bytes", c_uint64),
+        ("up_expert_bytes", c_uint64),
+        ("down_expert_bytes", c_uint64),
+        ("gate_type", c_int),
+        ("up_type", c_int),
+        ("down_type", c_int),
+        ("gate_shexp", c_void_p),
+        ("up_shexp", c_void_p),
+        ("down_shexp", c_void_p),
+        ("gate_shexp_type", c_int),
+        ("up_shexp_type", c_int),
+        ("down_shexp_type", c_int),
+        ("router", c_void_p),
+        ("shexp_gate", c_void_p),
+    ]
+
+
+# name -> (restype, argtypes); mirrors include/bread_moe.h one to one.
+SIGNATURES = {
+    "bread_status_str": (c_char_p, [c_int]),
+    "bread_set_exit_on_error": (None, [c_int]),
+    "bread_matvec": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "bread_matvec_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "bread_dequant_rows": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "bread_moe_shape_default": (None, [POINTER(MoeShape)]),
+    "bread_moe_ctx_create": (c_int, [POINTER(MoeShape), c_int, POINTER(c_void_p)]),
+    "bread_moe_ctx_destroy": (c_int, [c_void_p]),
+    "bread_moe_ctx_check": (c_int, [c_void_p, POINTER(c_int)]),
+    "bread_route": (c_int, [c_void_p, POINTER(MoeLayer), c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "bread_route_layer": (
+        c_int,
+        [c_void_p, POINTER(MoeLayer), c_void_p, POINTER(c_int32), POINTER(c_float), POINTER(c_float), c_void_p],
+    ),
+    "bread_moe_forward": (
+        c_int,
+        [c_void_p, POINTER(MoeLayer), c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p],
+    ),
+    "bread_rmsnorm_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_void_p]),
+    "bread_arena_create": (c_int, [POINTER(MoeShape), c_int, POINTER(c_void_p)]),
+    "bread_arena_destroy": (c_int, [c_void_p]),
+    "bread_arena_layer": (c_int, [c_void_p, c_int, POINTER(MoeLayer)]),
+    "bread_arena_layer_bytes": (c_uint64, [c_void_p]),
+    "bread_synth_q4k": (c_int, [c_void_p, c_uint64, c_uint64, c_void_p]),
+    "bread_synth_q6k": (c_int, [c_void_p, c_uint64, c_uint64, c_void_p]),
+    "bread_synth_normal_f32": (c_int, [c_void_p, c_uint64, c_uint64, c_float, c_float, c_void_p]),
+    "bread_synth_normal_f16": (c_int, [c_void_p, c_uint64, c_uint64, c_float, c_float, c_void_p]),
+}
+
+
+def _load() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()'). "
+            "There is no CPU fallback for the MoE path."
+        )
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def status_str(status: int) -> str:
+    return lib.bread_status_str(int(status)).decode()
+
+
+def check(status: int, where: str) -> None:
+    if status != OK:
+        raise BreadError(int(status), where)
+
+
+def default_shape() -> MoeShape:
+    s = MoeShape()
+    lib.bread_moe_shape_default(ctypes.byref(s))
+    return s

@@ -1,0 +1,280 @@
+"""Python host layer over the C ABI: device memory and streams come from
+PyTorch (plumbing); every computation is a call into libbread_moe.so.
+
+Names mirror the reference's interface for this path (kernels.cu:289
+bread_matvec, one_layer.cu:937 route_layer, the MoE block of
+one_layer_forward one_layer.cu:1800-1986), with the reference's exit(1)
+replaced by a raised BreadError carrying the status code.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import MoeLayer, MoeShape, check, lib
+
+QTYPE_Q8_0 = _lib.QTYPE_Q8_0
+QTYPE_Q4_K = _lib.QTYPE_Q4_K
+QTYPE_Q6_K = _lib.QTYPE_Q6_K
+
+
+def _p(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _s(stream) -> ctypes.c_void_p:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def row_bytes(qtype: int, cols: int) -> int:
+    if qtype == QTYPE_Q4_K:
+        return cols // 256 * 144
+    if qtype == QTYPE_Q6_K:
+        return cols // 256 * 210
+    if qtype == QTYPE_Q8_0:
+        return cols // 32 * 34
+    raise ValueError(f"qtype {qtype}")
+
+
+# ---------------------------------------------------------------- matvec
+
+
+def bread_matvec(w, x, y, rows: int, cols: int, qtype: int, stream=None) -> None:
+    """fp16 in / fp16 out (kernels.cu:289). x, y: torch.float16 device tensors."""
+    check(lib.bread_matvec(_p(w), _p(x), _p(y), rows, cols, qtype, _s(stream)), "bread_matvec")
+
+
+def bread_matvec_f32(w, x, y, rows: int, cols: int, qtype: int, stream=None) -> None:
+    check(lib.bread_matvec_f32(_p(w), _p(x), _p(y), rows, cols, qtype, _s(stream)), "bread_matvec_f32")
+
+
+def bread_dequant_rows(w, qtype: int, rows: int, cols: int, out=None, stream=None) -> torch.Tensor:
+    if out is None:
+        out = torch.empty(rows * cols, dtype=torch.float32, device=w.device)
+    check(lib.bread_dequant_rows(_p(w), qtype, rows, cols, _p(out), _s(stream)), "bread_dequant_rows")
+    return out
+
+
+def bread_rmsnorm_f32(x, w, out, n: int, n_tokens: int, eps: float, stream=None) -> None:
+    check(lib.bread_rmsnorm_f32(_p(x), _p(w), _p(out), n, n_tokens, eps, _s(stream)), "bread_rmsnorm_f32")
+
+
+# ---------------------------------------------------------------- synth
+
+
+def synth_q4k(dst, n_blocks: int, seed: int, stream=None) -> None:
+    check(lib.bread_synth_q4k(_p(dst), n_blocks, seed, _s(stream)), "bread_synth_q4k")
+
+
+def synth_q6k(dst, n_blocks: int, seed: int, stream=None) -> None:
+    check(lib.bread_synth_q6k(_p(dst), n_blocks, seed, _s(stream)), "bread_synth_q6k")
+
+
+def synth_normal_f32(dst, n: int, seed: int, mean: float, std: float, stream=None) -> None:
+    check(lib.bread_synth_normal_f32(_p(dst), n, seed, mean, std, _s(stream)), "bread_synth_normal_f32")
+
+
+def synth_normal_f16(dst, n: int, seed: int, mean: float, std: float, stream=None) -> None:
+    check(lib.bread_synth_normal_f16(_p(dst), n, seed, mean, std, _s(stream)), "bread_synth_normal_f16")
+
+
+# ---------------------------------------------------------------- shape / layers
+
+
+def shape(hidden=2048, expert_inter=512, shared_inter=512, n_experts=256, top_k=8, rms_eps=1e-6) -> MoeShape:
+    return MoeShape(hidden, expert_inter, shared_inter, n_experts, top_k, rms_eps)
+
+
+def shape_bytes(s: MoeShape) -> dict:
+    """Byte sizes of one layer's tensors (native GGUF layout)."""
+    H, I, Ish, E = s.hidden, s.expert_inter, s.shared_inter, s.n_experts
+    return {
+        "gate_expert": I * (H // 256) * 144,
+        "up_expert": I * (H // 256) * 144,
+        "down_expert": H * (I // 256) * 210,
+        "gate_sh": Ish * (H // 256) * 144,
+        "up_sh": Ish * (H // 256) * 144,
+        "down_sh": H * (Ish // 256) * 210,
+        "router": E * H * 4,
+        "shgate": H * 2,
+    }
+
+
+@dataclass
+class LayerTensors:
+    """One layer's weights as device tensors (keeps them alive)."""
+
+    shape: MoeShape
+    gate_exps: torch.Tensor
+    up_exps: torch.Tensor
+    down_exps: torch.Tensor
+    gate_sh: torch.Tensor
+    up_sh: torch.Tensor
+    down_sh: torch.Tensor
+    router: torch.Tensor
+    shgate: torch.Tensor | None
+
+    def desc(self) -> MoeLayer:
+        b = shape_bytes(self.shape)
+        return MoeLayer(
+            self.gate_exps.data_ptr(), self.up_exps.data_ptr(), self.down_exps.data_ptr(),
+            b["gate_expert"], b["up_expert"], b["down_expert"],
+            QTYPE_Q4_K, QTYPE_Q4_K, QTYPE_Q6_K,
+            self.gate_sh.data_ptr(), self.up_sh.data_ptr(), self.down_sh.data_ptr(),
+            QTYPE_Q4_K, QTYPE_Q4_K, QTYPE_Q6_K,
+            self.router.data_ptr(),
+            self.shgate.data_ptr() if self.shgate is not None else None,
+        )
+
+
+def layer_seeds(seed: int, layer: int) -> dict:
+    base = (seed * 1_000_003 + layer * 101) & ((1 << 63) - 1)
+    names = ["gate_exps", "up_exps", "down_exps", "gate_sh", "up_sh", "down_sh", "router", "shgate"]
+    return {n: base + i for i, n in enumerate(names)}
+
+
+def synth_layer_tensors(s: MoeShape, seed: int, layer: int = 0, router_std: float = 0.02,
+                        shgate_std: float = 0.02, device="cuda", stream=None) -> LayerTensors:
+    """Allocate one layer with torch and fill it with the device generator."""
+    b = shape_bytes(s)
+    E = s.n_experts
+    sd = layer_seeds(seed, layer)
+    u8 = dict(dtype=torch.uint8, device=device)
+    t = LayerTensors(
+        s,
+        torch.empty(E * b["gate_expert"], **u8),
+        torch.empty(E * b["up_expert"], **u8),
+        torch.empty(E * b["down_expert"], **u8),
+        torch.empty(b["gate_sh"], **u8),
+        torch.empty(b["up_sh"], **u8),
+        torch.empty(b["down_sh"], **u8),
+        torch.empty(E * s.hidden, dtype=torch.float32, device=device),
+        torch.empty(s.hidden, dtype=torch.float16, device=device),
+    )
+    synth_q4k(t.gate_exps, E * b["gate_expert"] // 144, sd["gate_exps"], stream)
+    synth_q4k(t.up_exps, E * b["up_expert"] // 144, sd["up_exps"], stream)
+    synth_q6k(t.down_exps, E * b["down_expert"] // 210, sd["down_exps"], stream)
+    synth_q4k(t.gate_sh, b["gate_sh"] // 144, sd["gate_sh"], stream)
+    synth_q4k(t.up_sh, b["up_sh"] // 144, sd["up_sh"], stream)
+    synth_q6k(t.down_sh, b["down_sh"] // 210, sd["down_sh"], stream)
+    synth_normal_f32(t.router, E * s.hidden, sd["router"], 0.0, router_std, stream)
+    synth_normal_f16(t.shgate, s.hidden, sd["shgate"], 0.0, shgate_std, stream)
+    return t
+
+
+class Arena:
+    """All experts of n_layers layers resident in HBM (bread_arena_*)."""
+
+    def __init__(self, s: MoeShape, n_layers: int):
+        self.shape = s
+        self.n_layers = n_layers
+        self._h = ctypes.c_void_p()
+        check(lib.bread_arena_create(ctypes.byref(s), n_layers, ctypes.byref(self._h)), "bread_arena_create")
+
+    @property
+    def layer_bytes(self) -> int:
+        return int(lib.bread_arena_layer_bytes(self._h))
+
+    def layer(self, l: int) -> MoeLayer:
+        d = MoeLayer()
+        check(lib.bread_arena_layer(self._h, l, ctypes.byref(d)), "bread_arena_layer")
+        return d
+
+    def synth_layer(self, l: int, seed: int, router_std=0.02, shgate_std=0.02, stream=None) -> None:
+        d = self.layer(l)
+        s = self.shape
+        b = shape_bytes(s)
+        E = s.n_experts
+        sd = layer_seeds(seed, l)
+        st = _s(stream)
+
+        def q(fn, ptr, nb, sv):
+            check(fn(ctypes.c_void_p(ptr), nb, sv, st), fn.__name__)
+
+        q(lib.bread_synth_q4k, d.gate_exps, E * b["gate_expert"] // 144, sd["gate_exps"])
+        q(lib.bread_synth_q4k, d.up_exps, E * b["up_expert"] // 144, sd["up_exps"])
+        q(lib.bread_synth_q6k, d.down_exps, E * b["down_expert"] // 210, sd["down_exps"])
+        q(lib.bread_synth_q4k, d.gate_shexp, b["gate_sh"] // 144, sd["gate_sh"])
+        q(lib.bread_synth_q4k, d.up_shexp, b["up_sh"] // 144, sd["up_sh"])
+        q(lib.bread_synth_q6k, d.down_shexp, b["down_sh"] // 210, sd["down_sh"])
+        check(lib.bread_synth_normal_f32(ctypes.c_void_p(d.router), E * s.hidden, sd["router"], 0.0, router_std, st),
+              "bread_synth_normal_f32")
+        check(lib.bread_synth_normal_f16(ctypes.c_void_p(d.shexp_gate), s.hidden, sd["shgate"], 0.0, shgate_std, st),
+              "bread_synth_normal_f16")
+
+    def close(self) -> None:
+        if self._h:
+            lib.bread_arena_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class MoeContext:
+    """bread_moe_ctx_t: scratch for MoE calls on one stream."""
+
+    def __init__(self, s: MoeShape, max_tokens: int = 1):
+        self.shape = s
+        self.max_tokens = max_tokens
+        self._h = ctypes.c_void_p()
+        check(lib.bread_moe_ctx_create(ctypes.byref(s), max_tokens, ctypes.byref(self._h)), "bread_moe_ctx_create")
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    def route(self, layer: MoeLayer, x: torch.Tensor, n_tokens: int, stream=None):
+        K = self.shape.top_k
+        idx = torch.empty((n_tokens, K), dtype=torch.int32, device=x.device)
+        w = torch.empty((n_tokens, K), dtype=torch.float32, device=x.device)
+        gsh = torch.empty((n_tokens,), dtype=torch.float32, device=x.device)
+        check(lib.bread_route(self._h, ctypes.byref(layer), _p(x), n_tokens, _p(idx), _p(w), _p(gsh), _s(stream)),
+              "bread_route")
+        return idx, w, gsh
+
+    def route_layer(self, layer: MoeLayer, x: torch.Tensor, stream=None):
+        """route_layer shim (one_layer.cu:937): host lists and the raw gate logit."""
+        K = self.shape.top_k
+        idx = (ctypes.c_int32 * K)()
+        w = (ctypes.c_float * K)()
+        g = ctypes.c_float()
+        check(lib.bread_route_layer(self._h, ctypes.byref(layer), _p(x), idx, w, ctypes.byref(g), _s(stream)),
+              "bread_route_layer")
+        return list(idx), list(w), g.value
+
+    def forward(self, layer: MoeLayer, x: torch.Tensor, hidden: torch.Tensor, n_tokens: int,
+                want_routing: bool = False, stream=None):
+        K = self.shape.top_k
+        idx = w = gsh = None
+        if want_routing:
+            idx = torch.empty((n_tokens, K), dtype=torch.int32, device=x.device)
+            w = torch.empty((n_tokens, K), dtype=torch.float32, device=x.device)
+            gsh = torch.empty((n_tokens,), dtype=torch.float32, device=x.device)
+        check(lib.bread_moe_forward(self._h, ctypes.byref(layer), _p(x), _p(hidden), n_tokens, _p(idx), _p(w),
+                                    _p(gsh), _s(stream)), "bread_moe_forward")
+        return idx, w, gsh
+
+    def check_device(self) -> int:
+        e = ctypes.c_int(0)
+        check(lib.bread_moe_ctx_check(self._h, ctypes.byref(e)), "bread_moe_ctx_check")
+        return e.value
+
+    def close(self) -> None:
+        if self._h:
+            lib.bread_moe_ctx_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

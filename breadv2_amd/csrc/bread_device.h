@@ -1,0 +1,172 @@
+// bread_device.h — device helpers shared by the gfx950 kernels of the MoE
+// feed-forward path: fp16 decode, K-quant field unpacking, alignment-tolerant
+// loads and wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define QK 256
+#define Q4K_BYTES 144
+#define Q6K_BYTES 210
+#define Q80_BYTES 34
+#define Q80_ELEMS 32
+#define WAVE 64
+
+// ---------------------------------------------------------------------------
+// fp16 decode
+// ---------------------------------------------------------------------------
+
+// Bitwise restatement of bread_h2f (bread_utils.h:27-47): subnormals become
+// mantissa * 2^-24, Inf/NaN keep their payload bits.  Used where results must
+// match the reference bit for bit (the dequant export).
+__device__ __forceinline__ float h2f_exact(uint32_t h)
+{
+    h &= 0xFFFFu;
+    const uint32_t sign = (h >> 15) << 31;
+    const uint32_t exponent = (h >> 10) & 0x1Fu;
+    const uint32_t mantissa = h & 0x3FFu;
+    if (exponent == 0) {
+        const float val = (float)mantissa * (1.0f / 16777216.0f);
+        return (h >> 15) ? -val : val;
+    }
+    const uint32_t bits = exponent == 31 ? (sign | 0x7F800000u | (mantissa << 13))
+                                         : (sign | ((exponent + 112u) << 23) | (mantissa << 13));
+    return __builtin_bit_cast(float, bits);
+}
+
+// Hardware conversion (v_cvt_f32_f16): identical to h2f_exact for every
+// finite value including subnormals; only quiets signalling NaNs.  Used in
+// the matvec paths, whose contract is a tolerance.
+__device__ __forceinline__ float h2f(uint32_t h)
+{
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
+}
+
+__device__ __forceinline__ uint16_t f2h(float f)
+{
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// ---------------------------------------------------------------------------
+// K-quant fields
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, uint32_t k)
+{
+    return (w >> (8u * k)) & 0xFFu;
+}
+
+// Byte k (0..11) of the Q4_K packed scales held as three dwords.
+__device__ __forceinline__ uint32_t scale_byte(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t k)
+{
+    const uint32_t w = k < 4 ? s0 : (k < 8 ? s1 : s2);
+    return byte_of(w, k & 3u);
+}
+
+// 6-bit (scale, min) pair j (0..7) of a Q4_K superblock, the unpacking of
+// get_scale_min_k4 (dequant_q4k_cpu.c:70-79).
+__device__ __forceinline__ void scale_min_k4(uint32_t j, uint32_t s0, uint32_t s1, uint32_t s2,
+                                             uint32_t &sc, uint32_t &m)
+{
+    if (j < 4) {
+        sc = scale_byte(s0, s1, s2, j) & 63u;
+        m = scale_byte(s0, s1, s2, j + 4) & 63u;
+    } else {
+        sc = (scale_byte(s0, s1, s2, j + 4) & 0x0Fu) | ((scale_byte(s0, s1, s2, j - 4) >> 6) << 4);
+        m = (scale_byte(s0, s1, s2, j + 4) >> 4) | ((scale_byte(s0, s1, s2, j) >> 6) << 4);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Loads
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ uint4 ld_b128(const uint8_t *p)
+{
+    return *reinterpret_cast<const uint4 *>(p);
+}
+
+__device__ __forceinline__ uint32_t ld_b32(const uint8_t *p)
+{
+    return *reinterpret_cast<const uint32_t *>(p);
+}
+
+// 8 bytes starting at a 2-byte aligned address, from aligned dword loads.
+// Every dword loaded holds at least one wanted byte (for p = 4m the third
+// load repeats the second), so nothing outside the object's aligned dwords
+// is read.  Q6_K and Q8_0 blocks (210 and 34 bytes) are only 2-byte aligned.
+__device__ __forceinline__ uint2 ld8_a2(const uint8_t *p)
+{
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint8_t *b = reinterpret_cast<const uint8_t *>(a & ~(uintptr_t)3);
+    const uint32_t sh = (uint32_t)(a & 3u);
+    const uint32_t w0 = ld_b32(b);
+    const uint32_t w1 = ld_b32(b + 4);
+    const uint32_t w2 = ld_b32(reinterpret_cast<const uint8_t *>((a + 7) & ~(uintptr_t)3));
+    uint2 r;
+    r.x = __builtin_amdgcn_alignbyte(w1, w0, sh);
+    r.y = __builtin_amdgcn_alignbyte(w2, w1, sh);
+    return r;
+}
+
+// 16-bit value at a 2-byte aligned address.
+__device__ __forceinline__ uint32_t ld16_a2(const uint8_t *p)
+{
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t w = ld_b32(reinterpret_cast<const uint8_t *>(a & ~(uintptr_t)3));
+    return (w >> (8u * (uint32_t)(a & 3u))) & 0xFFFFu;
+}
+
+// ---------------------------------------------------------------------------
+// wave64 reductions (DPP inside 16-lane rows, cross-row by permute)
+// ---------------------------------------------------------------------------
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                 0xF, 0xF, true));
+}
+
+// Sum over aligned groups of 8 lanes; the result is in every lane of the group.
+__device__ __forceinline__ float sum8(float v)
+{
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    return v;
+}
+
+__device__ __forceinline__ float sum16(float v)
+{
+    v = sum8(v);
+    v += dpp_f<0x140>(v);  // row_mirror
+    return v;
+}
+
+__device__ __forceinline__ float sum32(float v)
+{
+    v = sum16(v);
+    v += __shfl_xor(v, 16);
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+    v = sum32(v);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ __forceinline__ int lane_id()
+{
+    return (int)(threadIdx.x & (WAVE - 1));
+}

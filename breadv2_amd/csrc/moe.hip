@@ -1,0 +1,394 @@
+// moe.hip — MoE context, routing, the multi-token path, RMSNorm and the
+// C-ABI entry points of the MoE block.
+//
+// Multi-token path (any n_tokens, and the fallback for shapes the
+// single-launch decode kernel is not built for): four stream-ordered kernels
+//   router logits  -> softmax/top-k (one wave per token)
+//   -> gate/up + SwiGLU (one wave per (token, slot, row))
+//   -> down + combine (one wave per (token, row), slots in reference order).
+// Slot 0 is the shared expert, slots 1..K the routed experts by rank.
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "bread_internal.h"
+#include "quant_dot.h"
+#include "route_dev.h"
+
+static int g_exit_on_error = 0;
+
+extern "C" void bread_set_exit_on_error(int enable)
+{
+    g_exit_on_error = enable;
+}
+
+int bread_fail(int status, const char *where, const char *detail)
+{
+    if (g_exit_on_error) {
+        fprintf(stderr, "bread: %s: %s (%s)\n", where, bread_status_str(status), detail ? detail : "");
+        exit(1);
+    }
+    return status;
+}
+
+extern "C" const char *bread_status_str(int status)
+{
+    switch (status) {
+    case BREAD_OK: return "ok";
+    case BREAD_ERR_ARG: return "invalid argument";
+    case BREAD_ERR_QTYPE: return "unsupported qtype";
+    case BREAD_ERR_SHAPE: return "unsupported shape";
+    case BREAD_ERR_ALIGN: return "misaligned pointer";
+    case BREAD_ERR_HIP: return "HIP runtime error";
+    case BREAD_ERR_NOMEM: return "out of memory";
+    case BREAD_ERR_CAPACITY: return "more tokens than the context holds";
+    case BREAD_ERR_DEVICE: return "device-side fault flagged by a kernel";
+    }
+    return "unknown status";
+}
+
+extern "C" void bread_moe_shape_default(bread_moe_shape_t *s)
+{
+    if (!s) return;
+    s->hidden = 2048;       // bread.h: hidden_dim
+    s->expert_inter = 512;  // bread.h: expert_inter
+    s->shared_inter = 512;  // bread.h: shared_inter
+    s->n_experts = 256;     // bread.h: num_experts
+    s->top_k = 8;           // bread.h: top_k
+    s->rms_eps = 1e-6f;     // bread.h:68
+}
+
+static int validate_shape(const bread_moe_shape_t *s)
+{
+    BREAD_REQUIRE(s, BREAD_ERR_ARG, "NULL shape");
+    BREAD_REQUIRE(s->hidden > 0 && s->expert_inter > 0 && s->shared_inter > 0 && s->n_experts > 0 &&
+                      s->top_k > 0,
+                  BREAD_ERR_ARG, "shape fields must be positive");
+    BREAD_REQUIRE(s->top_k <= s->n_experts, BREAD_ERR_ARG, "top_k > n_experts");
+    BREAD_REQUIRE(s->hidden % QK == 0 && s->expert_inter % QK == 0 && s->shared_inter % QK == 0,
+                  BREAD_ERR_SHAPE, "hidden and intermediate sizes must be multiples of 256");
+    BREAD_REQUIRE(s->n_experts <= 1024, BREAD_ERR_SHAPE, "n_experts > 1024");
+    BREAD_REQUIRE(s->top_k <= 32, BREAD_ERR_SHAPE, "top_k > 32");
+    return BREAD_OK;
+}
+
+int bread_validate_layer(const bread_moe_shape_t *s, const bread_moe_layer_t *L)
+{
+    BREAD_REQUIRE(L, BREAD_ERR_ARG, "NULL layer");
+    BREAD_REQUIRE(L->gate_exps && L->up_exps && L->down_exps && L->gate_shexp && L->up_shexp &&
+                      L->down_shexp && L->router,
+                  BREAD_ERR_ARG, "NULL weight pointer in layer");
+    BREAD_REQUIRE(L->gate_type == BREAD_QTYPE_Q4_K && L->up_type == BREAD_QTYPE_Q4_K &&
+                      L->down_type == BREAD_QTYPE_Q6_K && L->gate_shexp_type == BREAD_QTYPE_Q4_K &&
+                      L->up_shexp_type == BREAD_QTYPE_Q4_K && L->down_shexp_type == BREAD_QTYPE_Q6_K,
+                  BREAD_ERR_QTYPE, "device MoE path takes Q4_K gate/up and Q6_K down");
+    const uint64_t gb = (uint64_t)s->expert_inter * (s->hidden / QK) * Q4K_BYTES;
+    const uint64_t db = (uint64_t)s->hidden * (s->expert_inter / QK) * Q6K_BYTES;
+    BREAD_REQUIRE(L->gate_expert_bytes >= gb && L->up_expert_bytes >= gb && L->down_expert_bytes >= db,
+                  BREAD_ERR_SHAPE, "expert stride smaller than one expert");
+    const uintptr_t a16 = (uintptr_t)L->gate_exps | (uintptr_t)L->up_exps | (uintptr_t)L->gate_shexp |
+                          (uintptr_t)L->up_shexp | (uintptr_t)L->router | L->gate_expert_bytes |
+                          L->up_expert_bytes;
+    BREAD_REQUIRE((a16 & 15) == 0, BREAD_ERR_ALIGN, "Q4_K experts and router must be 16-byte aligned");
+    const uintptr_t a4 = (uintptr_t)L->down_exps | (uintptr_t)L->down_shexp | L->down_expert_bytes |
+                         (uintptr_t)L->shexp_gate;
+    BREAD_REQUIRE((a4 & 3) == 0, BREAD_ERR_ALIGN, "Q6_K experts must be 4-byte aligned");
+    BREAD_REQUIRE(((uintptr_t)L->shexp_gate & 7) == 0, BREAD_ERR_ALIGN, "shexp_gate must be 8-byte aligned");
+    return BREAD_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Context
+// ---------------------------------------------------------------------------
+
+extern "C" int bread_moe_ctx_create(const bread_moe_shape_t *shape, int max_tokens, bread_moe_ctx_t **out)
+{
+    int rc = validate_shape(shape);
+    if (rc) return rc;
+    BREAD_REQUIRE(out && max_tokens > 0, BREAD_ERR_ARG, "out must be non-NULL and max_tokens > 0");
+    *out = nullptr;
+    bread_moe_ctx_t *c = (bread_moe_ctx_t *)calloc(1, sizeof(bread_moe_ctx_t));
+    BREAD_REQUIRE(c, BREAD_ERR_NOMEM, "host allocation");
+    c->shape = *shape;
+    c->max_tokens = max_tokens;
+    hipError_t e = hipGetDevice(&c->device);
+    const int E = shape->n_experts, K = shape->top_k;
+    const int Imax = shape->expert_inter > shape->shared_inter ? shape->expert_inter : shape->shared_inter;
+    const size_t T = (size_t)max_tokens;
+    if (e == hipSuccess) e = hipMalloc((void **)&c->logits, T * E * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->lbound, T * E * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->idx, T * K * sizeof(int32_t));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->w, T * K * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->gsh, T * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->h, T * (K + 1) * Imax * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->sync, sizeof(bread_sync));
+    if (e == hipSuccess) {
+        bread_sync init;
+        memset(&init, 0, sizeof(init));
+        for (int k = 0; k < 64; k++) init.route_idx[k] = -1;
+        e = hipMemcpy(c->sync, &init, sizeof(init), hipMemcpyHostToDevice);
+    }
+    if (e != hipSuccess) {
+        bread_moe_ctx_destroy(c);
+        return bread_fail(e == hipErrorOutOfMemory ? BREAD_ERR_NOMEM : BREAD_ERR_HIP, "bread_moe_ctx_create",
+                          hipGetErrorString(e));
+    }
+    *out = c;
+    return BREAD_OK;
+}
+
+extern "C" int bread_moe_ctx_destroy(bread_moe_ctx_t *c)
+{
+    if (!c) return BREAD_OK;
+    (void)hipFree(c->logits);
+    (void)hipFree(c->lbound);
+    (void)hipFree(c->idx);
+    (void)hipFree(c->w);
+    (void)hipFree(c->gsh);
+    (void)hipFree(c->h);
+    (void)hipFree(c->sync);
+    free(c);
+    return BREAD_OK;
+}
+
+extern "C" int bread_moe_ctx_check(bread_moe_ctx_t *c, int *device_error)
+{
+    BREAD_REQUIRE(c, BREAD_ERR_ARG, "NULL context");
+    BREAD_HIP(hipStreamSynchronize(c->last_stream));
+    uint32_t err = 0;
+    BREAD_HIP(hipMemcpy(&err, &c->sync->error, sizeof(err), hipMemcpyDeviceToHost));
+    if (device_error) *device_error = (int)err;
+    if (err) {
+        const uint32_t zero = 0;
+        BREAD_HIP(hipMemcpy(&c->sync->error, &zero, sizeof(zero), hipMemcpyHostToDevice));
+        return bread_fail(BREAD_ERR_DEVICE, "bread_moe_ctx_check", "a kernel flagged an error");
+    }
+    return BREAD_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Routing kernels
+// ---------------------------------------------------------------------------
+
+// One wave per router row (rows E.. hold the shared-gate dot); every token.
+__global__ __launch_bounds__(256) void k_router(const float *__restrict__ router, const uint16_t *__restrict__ shg,
+                                                const float *__restrict__ x, float *__restrict__ logits,
+                                                float *__restrict__ gsh, int H, int E, int T)
+{
+    const int v = (int)((blockIdx.x * blockDim.x + threadIdx.x) / WAVE);
+    if (v > E) return;
+    for (int t = 0; t < T; t++) {
+        const float *xt = x + (size_t)t * H;
+        if (v < E) {
+            const float s = router_row_dot(router + (size_t)v * H, xt, H);
+            if (lane_id() == 0) logits[(size_t)t * E + v] = s;
+        } else {
+            const float s = shg ? shgate_dot(shg, xt, H) : 0.f;
+            if (lane_id() == 0) gsh[t] = s;
+        }
+    }
+}
+
+template <int MAXV>
+__global__ __launch_bounds__(64) void k_topk(const float *__restrict__ logits, int E, int K,
+                                             int32_t *__restrict__ idx, float *__restrict__ w)
+{
+    const int t = blockIdx.x;
+    int ik;
+    float wk;
+    topk_wave<MAXV>(logits + (size_t)t * E, E, K, ik, wk);
+    if (lane_id() < K) {
+        idx[(size_t)t * K + lane_id()] = ik;
+        w[(size_t)t * K + lane_id()] = wk;
+    }
+}
+
+// One wave per (token, slot, row): gate and up rows, then SwiGLU.
+__global__ __launch_bounds__(256) void k_gateup(bread_moe_layer_t L, const float *__restrict__ x,
+                                                const int32_t *__restrict__ idx, float *__restrict__ h, int H,
+                                                int I, int Ish, int K, int T)
+{
+    const int Imax = I > Ish ? I : Ish;
+    const int64_t v = (int64_t)((blockIdx.x * (uint64_t)blockDim.x + threadIdx.x) / WAVE);
+    const int64_t per_tok = (int64_t)(K + 1) * Imax;
+    if (v >= per_tok * T) return;
+    const int t = (int)(v / per_tok);
+    const int slot = (int)((v % per_tok) / Imax);
+    const int r = (int)(v % Imax);
+    if (r >= (slot ? I : Ish)) return;
+    const uint64_t rb = (uint64_t)(H / QK) * Q4K_BYTES;
+    const uint8_t *g, *u;
+    if (slot == 0) {
+        g = (const uint8_t *)L.gate_shexp;
+        u = (const uint8_t *)L.up_shexp;
+    } else {
+        const int e = idx[(size_t)t * K + slot - 1];
+        g = (const uint8_t *)L.gate_exps + (uint64_t)e * L.gate_expert_bytes;
+        u = (const uint8_t *)L.up_exps + (uint64_t)e * L.up_expert_bytes;
+    }
+    const float *xt = x + (size_t)t * H;
+    const int lane = lane_id();
+    const float gv = wave_sum(q4k_row_partial(g + r * rb, H / QK, xt, lane));
+    const float uv = wave_sum(q4k_row_partial(u + r * rb, H / QK, xt, lane));
+    if (lane == 0) h[((size_t)t * (K + 1) + slot) * Imax + r] = silu_mul(gv, uv);
+}
+
+// One wave per (token, output row): down rows of every slot, combined in the
+// reference order (one_layer.cu:1447-1469).
+__global__ __launch_bounds__(256) void k_down(bread_moe_layer_t L, const int32_t *__restrict__ idx,
+                                              const float *__restrict__ w, const float *__restrict__ gsh,
+                                              const float *__restrict__ h, float *__restrict__ hidden, int H,
+                                              int I, int Ish, int K, int T)
+{
+    const int Imax = I > Ish ? I : Ish;
+    const int64_t v = (int64_t)((blockIdx.x * (uint64_t)blockDim.x + threadIdx.x) / WAVE);
+    if (v >= (int64_t)H * T) return;
+    const int t = (int)(v / H);
+    const int r = (int)(v % H);
+    const int lane = lane_id();
+    const float *ht = h + (size_t)t * (K + 1) * Imax;
+    const float sh = wave_sum(q6k_row_partial((const uint8_t *)L.down_shexp + (uint64_t)r * (Ish / QK) * Q6K_BYTES,
+                                              Ish / QK, ht, lane));
+    float acc = hidden[(size_t)t * H + r];
+    acc += sigmoidf_ref(gsh[t]) * sh;
+    const uint64_t rb = (uint64_t)(I / QK) * Q6K_BYTES;
+    for (int k = 0; k < K; k++) {
+        const int e = idx[(size_t)t * K + k];
+        const uint8_t *d = (const uint8_t *)L.down_exps + (uint64_t)e * L.down_expert_bytes + r * rb;
+        const float eo = wave_sum(q6k_row_partial(d, I / QK, ht + (size_t)(k + 1) * Imax, lane));
+        acc += w[(size_t)t * K + k] * eo;
+    }
+    if (lane == 0) hidden[(size_t)t * H + r] = acc;
+}
+
+// fp32 RMSNorm, one 256-thread block per token (layer_ops.cu:203-212).
+__global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w,
+                                                 float *__restrict__ out, int n, float eps)
+{
+    __shared__ float part[4];
+    const float *xt = x + (size_t)blockIdx.x * n;
+    float *ot = out + (size_t)blockIdx.x * n;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) ss = fmaf(xt[i], xt[i], ss);
+    ss = wave_sum(ss);
+    if (lane_id() == 0) part[threadIdx.x / WAVE] = ss;
+    __syncthreads();
+    const float tot = part[0] + part[1] + part[2] + part[3];
+    const float inv = 1.0f / sqrtf(tot / (float)n + eps);
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += blockDim.x) ot[i] = xt[i] * inv * (w ? w[i] : 1.0f);
+}
+
+// ---------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------
+
+static int launch_topk(const float *logits, int E, int K, int T, int32_t *idx, float *w, hipStream_t st)
+{
+    const int mv = (E + WAVE - 1) / WAVE;
+    if (mv <= 4)
+        hipLaunchKernelGGL(k_topk<4>, dim3(T), dim3(64), 0, st, logits, E, K, idx, w);
+    else
+        hipLaunchKernelGGL(k_topk<16>, dim3(T), dim3(64), 0, st, logits, E, K, idx, w);
+    BREAD_HIP(hipGetLastError());
+    return BREAD_OK;
+}
+
+int bread_launch_route(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, int T, int32_t *idx,
+                       float *w, float *gsh, hipStream_t st)
+{
+    const bread_moe_shape_t &s = c->shape;
+    const int waves = s.n_experts + 1;
+    hipLaunchKernelGGL(k_router, dim3((waves + 3) / 4), dim3(256), 0, st, L->router, L->shexp_gate, x, c->logits,
+                       gsh, s.hidden, s.n_experts, T);
+    BREAD_HIP(hipGetLastError());
+    return launch_topk(c->logits, s.n_experts, s.top_k, T, idx, w, st);
+}
+
+int bread_launch_moe_multi(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, float *hidden, int T,
+                           hipStream_t st)
+{
+    const bread_moe_shape_t &s = c->shape;
+    int rc = bread_launch_route(c, L, x, T, c->idx, c->w, c->gsh, st);
+    if (rc) return rc;
+    const int Imax = s.expert_inter > s.shared_inter ? s.expert_inter : s.shared_inter;
+    const uint64_t gu_waves = (uint64_t)T * (s.top_k + 1) * Imax;
+    hipLaunchKernelGGL(k_gateup, dim3((unsigned)((gu_waves + 3) / 4)), dim3(256), 0, st, *L, x, c->idx, c->h,
+                       s.hidden, s.expert_inter, s.shared_inter, s.top_k, T);
+    BREAD_HIP(hipGetLastError());
+    const uint64_t dn_waves = (uint64_t)T * s.hidden;
+    hipLaunchKernelGGL(k_down, dim3((unsigned)((dn_waves + 3) / 4)), dim3(256), 0, st, *L, c->idx, c->w, c->gsh,
+                       c->h, hidden, s.hidden, s.expert_inter, s.shared_inter, s.top_k, T);
+    BREAD_HIP(hipGetLastError());
+    return BREAD_OK;
+}
+
+// ---------------------------------------------------------------------------
+// C-ABI entry points
+// ---------------------------------------------------------------------------
+
+static int check_tokens(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, int T)
+{
+    BREAD_REQUIRE(c && x, BREAD_ERR_ARG, "NULL context or input");
+    BREAD_REQUIRE(T >= 0, BREAD_ERR_ARG, "n_tokens < 0");
+    BREAD_REQUIRE(T <= c->max_tokens, BREAD_ERR_CAPACITY, "n_tokens > max_tokens of the context");
+    BREAD_REQUIRE(((uintptr_t)x & 15) == 0, BREAD_ERR_ALIGN, "x must be 16-byte aligned");
+    return bread_validate_layer(&c->shape, L);
+}
+
+extern "C" int bread_route(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, int T,
+                           int32_t *idx, float *w, float *gsh, bread_stream_t stream)
+{
+    int rc = check_tokens(c, L, x, T);
+    if (rc) return rc;
+    BREAD_REQUIRE(idx && w && gsh, BREAD_ERR_ARG, "NULL output");
+    if (T == 0) return BREAD_OK;
+    c->last_stream = to_hip(stream);
+    return bread_launch_route(c, L, x, T, idx, w, gsh, to_hip(stream));
+}
+
+extern "C" int bread_route_layer(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x,
+                                 int *expert_indices, float *expert_weights, float *gsh_logit,
+                                 bread_stream_t stream)
+{
+    BREAD_REQUIRE(expert_indices && expert_weights && gsh_logit, BREAD_ERR_ARG, "NULL host output");
+    int rc = bread_route(c, L, x, 1, c ? c->idx : nullptr, c ? c->w : nullptr, c ? c->gsh : nullptr, stream);
+    if (rc) return rc;
+    hipStream_t st = to_hip(stream);
+    const int K = c->shape.top_k;
+    BREAD_HIP(hipMemcpyAsync(expert_indices, c->idx, K * sizeof(int32_t), hipMemcpyDeviceToHost, st));
+    BREAD_HIP(hipMemcpyAsync(expert_weights, c->w, K * sizeof(float), hipMemcpyDeviceToHost, st));
+    BREAD_HIP(hipMemcpyAsync(gsh_logit, c->gsh, sizeof(float), hipMemcpyDeviceToHost, st));
+    BREAD_HIP(hipStreamSynchronize(st));
+    return BREAD_OK;
+}
+
+extern "C" int bread_moe_forward(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, float *hidden,
+                                 int T, int32_t *idx, float *w, float *gsh, bread_stream_t stream)
+{
+    int rc = check_tokens(c, L, x, T);
+    if (rc) return rc;
+    BREAD_REQUIRE(hidden, BREAD_ERR_ARG, "NULL hidden");
+    if (T == 0) return BREAD_OK;
+    hipStream_t st = to_hip(stream);
+    c->last_stream = st;
+    rc = (T == 1) ? bread_launch_moe_decode(c, L, x, hidden, st) : BREAD_ERR_SHAPE;
+    if (rc == BREAD_ERR_SHAPE) rc = bread_launch_moe_multi(c, L, x, hidden, T, st);
+    if (rc) return rc;
+    const int K = c->shape.top_k;
+    if (idx) BREAD_HIP(hipMemcpyAsync(idx, c->idx, (size_t)T * K * sizeof(int32_t), hipMemcpyDeviceToDevice, st));
+    if (w) BREAD_HIP(hipMemcpyAsync(w, c->w, (size_t)T * K * sizeof(float), hipMemcpyDeviceToDevice, st));
+    if (gsh) BREAD_HIP(hipMemcpyAsync(gsh, c->gsh, (size_t)T * sizeof(float), hipMemcpyDeviceToDevice, st));
+    return BREAD_OK;
+}
+
+extern "C" int bread_rmsnorm_f32(const float *x, const float *w, float *out, int n, int T, float eps,
+                                 bread_stream_t stream)
+{
+    BREAD_REQUIRE(x && out, BREAD_ERR_ARG, "NULL pointer");
+    BREAD_REQUIRE(n > 0 && T >= 0, BREAD_ERR_ARG, "n must be > 0 and n_tokens >= 0");
+    if (T == 0) return BREAD_OK;
+    hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(256), 0, to_hip(stream), x, w, out, n, eps);
+    BREAD_HIP(hipGetLastError());
+    return BREAD_OK;
+}

@@ -1,0 +1,212 @@
+// quant.hip — standalone quantized matvec (bread_matvec, bread_matvec_f32)
+// and the bit-exact dequant export (bread_dequant_rows) for gfx950.
+//
+// Matvec: one wave64 per row, grid-stride over rows; 8 lanes per superblock
+// stream the row with 16-byte (Q4_K) or aligned-dword (Q6_K, Q8_0) loads,
+// fp32 accumulate, DPP wave reduction.  Replaces kernels.cu:150-308, whose
+// 256-thread blocks read one element per thread with two barriers per
+// superblock.
+#include "bread_internal.h"
+#include "quant_dot.h"
+
+namespace {
+
+template <typename T> __device__ __forceinline__ void store_y(T *y, int r, float v);
+template <> __device__ __forceinline__ void store_y<float>(float *y, int r, float v) { y[r] = v; }
+template <> __device__ __forceinline__ void store_y<uint16_t>(uint16_t *y, int r, float v)
+{
+    y[r] = f2h(v);
+}
+
+template <int QT, typename XT, typename YT>
+__global__ __launch_bounds__(256) void k_matvec(const uint8_t *__restrict__ w, const XT *__restrict__ x,
+                                                YT *__restrict__ y, int rows, int cols, uint64_t row_bytes)
+{
+    const int lane = lane_id();
+    const int wv = (int)((blockIdx.x * blockDim.x + threadIdx.x) / WAVE);
+    const int nw = (int)(gridDim.x * blockDim.x / WAVE);
+    for (int r = wv; r < rows; r += nw) {
+        const uint8_t *row = w + (size_t)r * row_bytes;
+        float p;
+        if (QT == BREAD_QTYPE_Q4_K)
+            p = q4k_row_partial(row, cols / QK, x, lane);
+        else if (QT == BREAD_QTYPE_Q6_K)
+            p = q6k_row_partial(row, cols / QK, x, lane);
+        else
+            p = q80_row_partial(row, cols / Q80_ELEMS, x, lane);
+        p = wave_sum(p);
+        if (lane == 0) store_y(y, r, p);
+    }
+}
+
+// ---- bit-exact dequant: one thread per 8 consecutive output elements.
+// Operation order and roundings of dequant_q4k_cpu.c:111-121 / :155-165;
+// contraction is off so d1*q - m1 is a multiply then a subtract.
+
+__global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t *__restrict__ w, float *__restrict__ out,
+                                                     uint64_t n_groups)
+{
+#pragma clang fp contract(off)
+    for (uint64_t g = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; g < n_groups;
+         g += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t sb = g >> 5;          // superblock (rows are packed)
+        const uint32_t e0 = (uint32_t)(g & 31) * 8;
+        const uint8_t *blk = w + sb * Q4K_BYTES;
+        const uint32_t hdr = ld_b32(blk);
+        const float d = h2f_exact(hdr);
+        const float dmin = h2f_exact(hdr >> 16);
+        const uint32_t s0 = ld_b32(blk + 4), s1 = ld_b32(blk + 8), s2 = ld_b32(blk + 12);
+        const uint32_t j = e0 >> 6, sub = (e0 >> 5) & 1, l0 = e0 & 31;
+        uint32_t sc, m;
+        scale_min_k4(2 * j + sub, s0, s1, s2, sc, m);
+        const float d1 = d * (float)sc;
+        const float m1 = dmin * (float)m;
+        const uint2 q = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + l0);
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t byte = byte_of(k < 4 ? q.x : q.y, k & 3);
+            const uint32_t nib = sub ? (byte >> 4) : (byte & 0xF);
+            v[k] = d1 * (float)nib - m1;
+        }
+        float4 *o = reinterpret_cast<float4 *>(out + sb * QK + e0);
+        o[0] = make_float4(v[0], v[1], v[2], v[3]);
+        o[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_dequant_q6k(const uint8_t *__restrict__ w, float *__restrict__ out,
+                                                     uint64_t n_groups)
+{
+#pragma clang fp contract(off)
+    for (uint64_t g = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; g < n_groups;
+         g += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t sb = g >> 5;
+        const uint32_t e0 = (uint32_t)(g & 31) * 8;
+        const uint8_t *blk = w + sb * Q6K_BYTES;
+        const float d = h2f_exact(ld16_a2(blk + 208));
+        const uint32_t n = e0 >> 7, s = (e0 >> 5) & 3, l0 = e0 & 31;
+        const uint32_t is = l0 >> 4;
+        const float scf = (float)(int8_t)blk[192 + 8 * n + is + 2 * s];
+        const uint8_t *ql = blk + 64 * n + ((s & 1) ? 32 : 0) + l0;
+        const uint8_t *qh = blk + 128 + 32 * n + l0;
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t lb = ql[k];
+            const uint32_t nib = (s & 2) ? (lb >> 4) : (lb & 0xF);
+            const uint32_t hb = ((uint32_t)qh[k] >> (2 * s)) & 3u;
+            const int q = (int)(int8_t)(nib | (hb << 4)) - 32;
+            v[k] = d * scf * (float)q;
+        }
+        float4 *o = reinterpret_cast<float4 *>(out + sb * QK + e0);
+        o[0] = make_float4(v[0], v[1], v[2], v[3]);
+        o[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_dequant_q80(const uint8_t *__restrict__ w, float *__restrict__ out,
+                                                     uint64_t n_blocks)
+{
+#pragma clang fp contract(off)
+    for (uint64_t b = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; b < n_blocks;
+         b += (uint64_t)gridDim.x * blockDim.x) {
+        const uint8_t *blk = w + b * Q80_BYTES;
+        const float d = h2f_exact(ld16_a2(blk));
+        for (int i = 0; i < Q80_ELEMS; i++) out[b * Q80_ELEMS + i] = d * (float)(int8_t)blk[2 + i];
+    }
+}
+
+int check_matvec_args(const void *w, const void *x, const void *y, int rows, int cols, int qtype)
+{
+    BREAD_REQUIRE(w && x && y, BREAD_ERR_ARG, "NULL pointer");
+    BREAD_REQUIRE(rows >= 0 && cols > 0, BREAD_ERR_ARG, "rows must be >= 0 and cols > 0");
+    BREAD_REQUIRE(qtype == BREAD_QTYPE_Q4_K || qtype == BREAD_QTYPE_Q6_K || qtype == BREAD_QTYPE_Q8_0,
+                  BREAD_ERR_QTYPE, "qtype must be 12 (Q4_K), 14 (Q6_K) or 8 (Q8_0)");
+    const int blk = qtype == BREAD_QTYPE_Q8_0 ? Q80_ELEMS : QK;
+    BREAD_REQUIRE(cols % blk == 0, BREAD_ERR_SHAPE, "cols must be a multiple of the block size");
+    BREAD_REQUIRE(((uintptr_t)w & 3) == 0, BREAD_ERR_ALIGN, "w must be 4-byte aligned");
+    BREAD_REQUIRE(((uintptr_t)x & 15) == 0, BREAD_ERR_ALIGN, "x must be 16-byte aligned");
+    return BREAD_OK;
+}
+
+uint64_t row_bytes_of(int qtype, int cols)
+{
+    switch (qtype) {
+    case BREAD_QTYPE_Q4_K: return (uint64_t)(cols / QK) * Q4K_BYTES;
+    case BREAD_QTYPE_Q6_K: return (uint64_t)(cols / QK) * Q6K_BYTES;
+    case BREAD_QTYPE_Q8_0: return (uint64_t)(cols / Q80_ELEMS) * Q80_BYTES;
+    }
+    return 0;
+}
+
+template <typename XT, typename YT>
+int launch_matvec(const void *w, const XT *x, YT *y, int rows, int cols, int qtype, hipStream_t st)
+{
+    int rc = check_matvec_args(w, x, y, rows, cols, qtype);
+    if (rc) return rc;
+    if (rows == 0) return BREAD_OK;
+    const uint64_t rb = row_bytes_of(qtype, cols);
+    const int waves_per_block = 4;
+    int blocks = (rows + waves_per_block - 1) / waves_per_block;
+    if (blocks > 65536) blocks = 65536;
+    const uint8_t *wb = (const uint8_t *)w;
+    switch (qtype) {
+    case BREAD_QTYPE_Q4_K:
+        hipLaunchKernelGGL((k_matvec<BREAD_QTYPE_Q4_K, XT, YT>), dim3(blocks), dim3(256), 0, st, wb, x, y, rows, cols, rb);
+        break;
+    case BREAD_QTYPE_Q6_K:
+        hipLaunchKernelGGL((k_matvec<BREAD_QTYPE_Q6_K, XT, YT>), dim3(blocks), dim3(256), 0, st, wb, x, y, rows, cols, rb);
+        break;
+    default:
+        hipLaunchKernelGGL((k_matvec<BREAD_QTYPE_Q8_0, XT, YT>), dim3(blocks), dim3(256), 0, st, wb, x, y, rows, cols, rb);
+        break;
+    }
+    BREAD_HIP(hipGetLastError());
+    return BREAD_OK;
+}
+
+} // namespace
+
+extern "C" int bread_matvec(const void *w, const uint16_t *x, uint16_t *y, int rows, int cols, int qtype,
+                            bread_stream_t stream)
+{
+    return launch_matvec<uint16_t, uint16_t>(w, x, y, rows, cols, qtype, to_hip(stream));
+}
+
+extern "C" int bread_matvec_f32(const void *w, const float *x, float *y, int rows, int cols, int qtype,
+                                bread_stream_t stream)
+{
+    return launch_matvec<float, float>(w, x, y, rows, cols, qtype, to_hip(stream));
+}
+
+extern "C" int bread_dequant_rows(const void *w, int qtype, int rows, int cols, float *out,
+                                  bread_stream_t stream)
+{
+    BREAD_REQUIRE(w && out, BREAD_ERR_ARG, "NULL pointer");
+    BREAD_REQUIRE(rows >= 0 && cols > 0, BREAD_ERR_ARG, "rows must be >= 0 and cols > 0");
+    BREAD_REQUIRE(qtype == BREAD_QTYPE_Q4_K || qtype == BREAD_QTYPE_Q6_K || qtype == BREAD_QTYPE_Q8_0,
+                  BREAD_ERR_QTYPE, "qtype must be 12 (Q4_K), 14 (Q6_K) or 8 (Q8_0)");
+    const int blk = qtype == BREAD_QTYPE_Q8_0 ? Q80_ELEMS : QK;
+    BREAD_REQUIRE(cols % blk == 0, BREAD_ERR_SHAPE, "cols must be a multiple of the block size");
+    BREAD_REQUIRE(((uintptr_t)w & 3) == 0, BREAD_ERR_ALIGN, "w must be 4-byte aligned");
+    BREAD_REQUIRE(((uintptr_t)out & 15) == 0, BREAD_ERR_ALIGN, "out must be 16-byte aligned");
+    if (rows == 0) return BREAD_OK;
+    hipStream_t st = to_hip(stream);
+    const uint64_t n_blocks = (uint64_t)rows * (uint64_t)(cols / blk);
+    const uint8_t *wb = (const uint8_t *)w;
+    if (qtype == BREAD_QTYPE_Q8_0) {
+        const uint64_t g = (n_blocks + 255) / 256;
+        hipLaunchKernelGGL(k_dequant_q80, dim3((unsigned)(g < 65536 ? g : 65536)), dim3(256), 0, st, wb, out, n_blocks);
+    } else {
+        const uint64_t n_groups = n_blocks * 32;
+        const uint64_t g = (n_groups + 255) / 256;
+        const dim3 grid((unsigned)(g < 65536 ? g : 65536));
+        if (qtype == BREAD_QTYPE_Q4_K)
+            hipLaunchKernelGGL(k_dequant_q4k, grid, dim3(256), 0, st, wb, out, n_groups);
+        else
+            hipLaunchKernelGGL(k_dequant_q6k, grid, dim3(256), 0, st, wb, out, n_groups);
+    }
+    BREAD_HIP(hipGetLastError());
+    return BREAD_OK;
+}

@@ -1,0 +1,213 @@
+// quant_dot.h — per-lane partial dot products of one quantized row with an
+// activation vector, for the generic (any rows/cols) matvec kernels.
+//
+// Lane layout (wave64): 8 lanes per superblock, 8 superblocks per step.
+//   Q4_K: lane chunk c = lane%8 owns qs bytes [16c, 16c+16), i.e. sub-block
+//         pair j = c/2, low nibbles -> elements 64j+16(c%2)+[0,16),
+//         high nibbles -> elements 64j+32+16(c%2)+[0,16)
+//         (element order of dequant_q4k_cpu.c:111-121).
+//   Q6_K: lane unit u = lane%8 owns half n = u/4 and l in [8t, 8t+8),
+//         t = u%4: ql bytes 64n+l and 64n+32+l, qh byte 32n+l
+//         -> elements 128n + 32s + l, s = 0..3 (dequant_q4k_cpu.c:155-170).
+// The caller reduces the lane partials over the wave.
+#pragma once
+
+#include "bread_device.h"
+
+// ---- activation loads (x must be 16-byte aligned; offsets are multiples of 8)
+
+__device__ __forceinline__ void load_x8(const float *x, int off, float (&v)[8])
+{
+    const float4 a = *reinterpret_cast<const float4 *>(x + off);
+    const float4 b = *reinterpret_cast<const float4 *>(x + off + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+__device__ __forceinline__ void load_x8(const uint16_t *x, int off, float (&v)[8])
+{
+    const uint4 a = *reinterpret_cast<const uint4 *>(x + off);
+    v[0] = h2f(a.x); v[1] = h2f(a.x >> 16); v[2] = h2f(a.y); v[3] = h2f(a.y >> 16);
+    v[4] = h2f(a.z); v[5] = h2f(a.z >> 16); v[6] = h2f(a.w); v[7] = h2f(a.w >> 16);
+}
+
+template <typename XT>
+__device__ __forceinline__ void load_x16(const XT *x, int off, float (&v)[16])
+{
+    float a[8], b[8];
+    load_x8(x, off, a);
+    load_x8(x, off + 8, b);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        v[i] = a[i];
+        v[8 + i] = b[i];
+    }
+}
+
+// ---- Q4_K: one lane's 32 weights of a superblock
+
+// hd = bytes 0..15 of the superblock (d, dmin, scales), q = its 16-byte qs
+// chunk c, j = c/2.  Returns d*sc0*sum(lo*xl) - dmin*m0*sum(xl)
+//                           + d*sc1*sum(hi*xh) - dmin*m1*sum(xh).
+__device__ __forceinline__ float q4k_chunk_dot(uint4 hd, uint4 q, uint32_t j, const float (&xl)[16],
+                                               const float (&xh)[16])
+{
+    uint32_t sc0, m0, sc1, m1;
+    scale_min_k4(2 * j, hd.y, hd.z, hd.w, sc0, m0);
+    scale_min_k4(2 * j + 1, hd.y, hd.z, hd.w, sc1, m1);
+    const float d = h2f(hd.x);
+    const float dmin = h2f(hd.x >> 16);
+    float al = 0.f, ah = 0.f, sl = 0.f, sh = 0.f;
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const uint32_t lo = qw[t] & 0x0F0F0F0Fu;
+        const uint32_t hi = (qw[t] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            al = fmaf((float)byte_of(lo, k), xl[4 * t + k], al);
+            ah = fmaf((float)byte_of(hi, k), xh[4 * t + k], ah);
+            sl += xl[4 * t + k];
+            sh += xh[4 * t + k];
+        }
+    }
+    return (d * (float)sc0) * al - (dmin * (float)m0) * sl + (d * (float)sc1) * ah -
+           (dmin * (float)m1) * sh;
+}
+
+template <typename XT>
+__device__ __forceinline__ float q4k_row_partial(const uint8_t *row, int nb, const XT *x, int lane)
+{
+    const int c = lane & 7;
+    const uint32_t j = (uint32_t)c >> 1;
+    const int hh = c & 1;
+    float acc = 0.f;
+    for (int b = lane >> 3; b < nb; b += 8) {
+        const uint8_t *blk = row + (size_t)b * Q4K_BYTES;
+        const uint4 hd = ld_b128(blk);
+        const uint4 q = ld_b128(blk + 16 + 16 * c);
+        float xl[16], xh[16];
+        const int base = b * QK + 64 * (int)j + 16 * hh;
+        load_x16(x, base, xl);
+        load_x16(x, base + 32, xh);
+        acc += q4k_chunk_dot(hd, q, j, xl, xh);
+    }
+    return acc;
+}
+
+// ---- Q6_K: one lane's 32 weights of a superblock
+
+// Bytes l..l+3 of ql (low half a, high half b) and qh -> four dwords of
+// 6-bit values, one byte per weight, for s = 0..3 (element 32s + l).
+__device__ __forceinline__ void q6k_unpack(uint32_t a, uint32_t b, uint32_t h, uint32_t (&q)[4])
+{
+    q[0] = (a & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
+    q[1] = (b & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
+    q[2] = ((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u);
+    q[3] = ((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
+}
+
+// Signed scale sc[8n + i + 2s] from the 8 scale bytes of half n.
+__device__ __forceinline__ float q6k_scale(uint2 scw, uint32_t p)
+{
+    const uint32_t w = p < 4 ? scw.x : scw.y;
+    return (float)(int8_t)byte_of(w, p & 3u);
+}
+
+// xs[s][k] = x at element 32s + l0 + k of the half.  Returns
+// d * sum_s sc_s * sum_k (q - 32) * xs[s][k].
+__device__ __forceinline__ float q6k_unit_dot(uint2 ql0, uint2 ql1, uint2 qh, uint2 scw, uint32_t i,
+                                              float d, const float (&xs)[4][8])
+{
+    float A[4] = {0.f, 0.f, 0.f, 0.f}, X[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < 2; w++) {
+        uint32_t q[4];
+        q6k_unpack(w ? ql0.y : ql0.x, w ? ql1.y : ql1.x, w ? qh.y : qh.x, q);
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                A[s] = fmaf((float)byte_of(q[s], k), xs[s][4 * w + k], A[s]);
+                X[s] += xs[s][4 * w + k];
+            }
+    }
+    float r = 0.f;
+#pragma unroll
+    for (int s = 0; s < 4; s++) r = fmaf(q6k_scale(scw, i + 2 * s), fmaf(-32.f, X[s], A[s]), r);
+    return d * r;
+}
+
+template <typename XT>
+__device__ __forceinline__ float q6k_row_partial(const uint8_t *row, int nb, const XT *x, int lane)
+{
+    const int u = lane & 7;
+    const int n = u >> 2, t = u & 3;
+    const uint32_t i = (uint32_t)t >> 1;
+    float acc = 0.f;
+    for (int b = lane >> 3; b < nb; b += 8) {
+        const uint8_t *blk = row + (size_t)b * Q6K_BYTES;
+        const uint2 ql0 = ld8_a2(blk + 64 * n + 8 * t);
+        const uint2 ql1 = ld8_a2(blk + 64 * n + 32 + 8 * t);
+        const uint2 qh = ld8_a2(blk + 128 + 32 * n + 8 * t);
+        const uint2 scw = ld8_a2(blk + 192 + 8 * n);
+        const float d = h2f(ld16_a2(blk + 208));
+        float xs[4][8];
+#pragma unroll
+        for (int s = 0; s < 4; s++) load_x8(x, b * QK + 128 * n + 32 * s + 8 * t, xs[s]);
+        acc += q6k_unit_dot(ql0, ql1, qh, scw, i, d, xs);
+    }
+    return acc;
+}
+
+// ---- Q8_0: one lane per 34-byte block of 32 weights
+
+template <typename XT>
+__device__ __forceinline__ float q80_row_partial(const uint8_t *row, int nb32, const XT *x, int lane)
+{
+    float acc = 0.f;
+    for (int b = lane; b < nb32; b += WAVE) {
+        const uint8_t *blk = row + (size_t)b * Q80_BYTES;
+        const float d = h2f(ld16_a2(blk));
+        float s = 0.f;
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const uint2 q = ld8_a2(blk + 2 + 8 * m);
+            float xv[8];
+            load_x8(x, b * Q80_ELEMS + 8 * m, xv);
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                s = fmaf((float)(int8_t)byte_of(q.x, k), xv[k], s);
+                s = fmaf((float)(int8_t)byte_of(q.y, k), xv[4 + k], s);
+            }
+        }
+        acc = fmaf(d, s, acc);
+    }
+    return acc;
+}
+
+// q4k_chunk_dot with the activation sums over the two 16-element runs
+// precomputed (they are the same for every row a lane visits).
+__device__ __forceinline__ float q4k_chunk_dot_sx(uint4 hd, uint4 q, uint32_t j, const float (&xl)[16],
+                                                  const float (&xh)[16], float sl, float sh)
+{
+    uint32_t sc0, m0, sc1, m1;
+    scale_min_k4(2 * j, hd.y, hd.z, hd.w, sc0, m0);
+    scale_min_k4(2 * j + 1, hd.y, hd.z, hd.w, sc1, m1);
+    const float d = h2f(hd.x);
+    const float dmin = h2f(hd.x >> 16);
+    float al = 0.f, ah = 0.f;
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const uint32_t lo = qw[t] & 0x0F0F0F0Fu;
+        const uint32_t hi = (qw[t] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            al = fmaf((float)byte_of(lo, k), xl[4 * t + k], al);
+            ah = fmaf((float)byte_of(hi, k), xh[4 * t + k], ah);
+        }
+    }
+    return (d * (float)sc0) * al - (dmin * (float)m0) * sl + (d * (float)sc1) * ah -
+           (dmin * (float)m1) * sh;
+}

@@ -1,0 +1,225 @@
+/* bread_moe.h — C ABI of the MI355X (gfx950) MoE feed-forward hot path.
+ *
+ * Drop-in for the reference's (arahe-dev/breadv2) MoE FFN path:
+ *   - bread_matvec            replaces kernels.cu:289 (same name, argument
+ *                             order and meaning; returns a status instead of
+ *                             exit(1), kernels.cu:303-307)
+ *   - bread_route_layer       replaces route_layer, one_layer.cu:937-992
+ *   - bread_moe_forward       replaces the MoE block of one_layer_forward,
+ *                             one_layer.cu:1800-1986 (GPU) and :1413-1471
+ *                             (fp32 host order it reproduces)
+ *   - bread_arena_*           replaces the expert residency of
+ *                             weight_cache_load_experts, loader.c:628-693
+ *
+ * Every pointer argument named d_* or documented as "device" is a device
+ * pointer; the caller owns it.  Every entry point is stream-ordered on the
+ * given HIP stream (hipStream_t; NULL is the null stream) and returns a
+ * bread_status_t.  Entry points that take a context are not reentrant for
+ * the same context: two calls that overlap on one context race on its
+ * scratch.  Use one context per stream.
+ *
+ * Weight layout is the native GGUF block layout, row-major, rows packed with
+ * no padding: row stride = (cols / block_elems) * block_bytes
+ * (gguf.c:60-95, 140-144).
+ */
+#ifndef BREAD_MOE_H
+#define BREAD_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t without the HIP headers: the same incomplete struct type. */
+typedef struct ihipStream_t *bread_stream_t;
+
+/* GGML type ids used on the path (gguf.h:31-37). */
+#define BREAD_QTYPE_F32  0
+#define BREAD_QTYPE_F16  1
+#define BREAD_QTYPE_Q8_0 8
+#define BREAD_QTYPE_Q4_K 12
+#define BREAD_QTYPE_Q6_K 14
+
+#define BREAD_QK_K            256 /* elements per K-quant superblock */
+#define BREAD_Q4K_BLOCK_BYTES 144 /* d, dmin, 12 B scales, 128 B nibbles (kernels.cu:3-7) */
+#define BREAD_Q6K_BLOCK_BYTES 210 /* 128 B ql, 64 B qh, 16 int8 sc, d (kernels.cu:9-13) */
+#define BREAD_Q8_0_BLOCK_ELEMS 32
+#define BREAD_Q8_0_BLOCK_BYTES 34 /* d, 32 int8 (kernels.cu:240-246) */
+
+typedef enum {
+    BREAD_OK = 0,
+    BREAD_ERR_ARG = -1,        /* NULL pointer, negative size, bad shape field */
+    BREAD_ERR_QTYPE = -2,      /* qtype not supported by this entry point */
+    BREAD_ERR_SHAPE = -3,      /* cols not a multiple of the block size, etc. */
+    BREAD_ERR_ALIGN = -4,      /* pointer alignment the kernels need is missing */
+    BREAD_ERR_HIP = -5,        /* a HIP runtime call failed */
+    BREAD_ERR_NOMEM = -6,      /* device or host allocation failed */
+    BREAD_ERR_CAPACITY = -7,   /* more tokens than the context was created for */
+    BREAD_ERR_DEVICE = -8      /* a kernel reported a fault (see bread_moe_ctx_check) */
+} bread_status_t;
+
+/* Text for a status code (static storage). */
+const char *bread_status_str(int status);
+
+/* When non-zero, every entry point that would return an error prints it and
+ * calls exit(1), as the reference does (bread_utils.h:14-21,
+ * kernels.cu:303-307).  Default 0. */
+void bread_set_exit_on_error(int enable);
+
+/* ------------------------------------------------------------------ */
+/* Quantized matvec and dequant                                        */
+/* ------------------------------------------------------------------ */
+
+/* y[r] = sum_c dequant(W[r,c]) * x[c] for r < rows.  x and y are fp16 bits
+ * (the reference's `half`), accumulation is fp32, y is rounded to nearest
+ * fp16.  qtype is 12 (Q4_K), 14 (Q6_K) or 8 (Q8_0); cols must be a multiple
+ * of 256 (K-quants) or 32 (Q8_0).  w must be 4-byte aligned.
+ * Replaces kernels.cu:289-308 `void bread_matvec(void *w, half *x, half *y,
+ * int rows, int cols, int qtype, cudaStream_t stream)`. */
+int bread_matvec(const void *w, const uint16_t *x, uint16_t *y, int rows, int cols,
+                 int qtype, bread_stream_t stream);
+
+/* Same product with fp32 x and y (config 1 entry; the fp32 host path's
+ * cpu_tensor_matvec, layer_ops.cu:169-189, on the device). */
+int bread_matvec_f32(const void *w, const float *x, float *y, int rows, int cols,
+                     int qtype, bread_stream_t stream);
+
+/* Bit-exact dequant: out[r*cols + c] = the reference's fp32 value of W[r,c]
+ * (dequant_q4k_cpu.c:90-172 with the subnormal-correct fp16 decode of
+ * bread_utils.h:27-47; Q8_0 value = d*q, kernels.cu:246).  Same qtypes and
+ * shape rules as bread_matvec. */
+int bread_dequant_rows(const void *w, int qtype, int rows, int cols, float *out,
+                       bread_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* MoE layer                                                           */
+/* ------------------------------------------------------------------ */
+
+/* Model shape (bread.h:16-69 defaults: 2048, 512, 512, 256, 8, 1e-6). */
+typedef struct {
+    int hidden;        /* H */
+    int expert_inter;  /* I: routed expert intermediate size */
+    int shared_inter;  /* I_sh: shared expert intermediate size */
+    int n_experts;     /* E */
+    int top_k;         /* K */
+    float rms_eps;
+} bread_moe_shape_t;
+
+void bread_moe_shape_default(bread_moe_shape_t *shape);
+
+/* One layer's MoE weights, device pointers, native GGUF layout.
+ * Routed expert e of a stacked tensor starts at base + e * expert_bytes, the
+ * GGUF layout the reference slices (loader.h:35-47, loader.c:187-190); the
+ * shared expert and router mirror wc_layer_t (loader.h:86-109) and the
+ * tensors route_layer reads (one_layer.cu:964-980).
+ * Supported types on the device path: gate/up Q4_K, down Q6_K (the qtypes the
+ * reference GPU path hardcodes, one_layer.cu:1966-1977); router F32 [E][H];
+ * shexp_gate F16 [H] or NULL (NULL means a zero logit, sigmoid 0.5, as when
+ * the reference finds no tensor, one_layer.cu:974-976). */
+typedef struct {
+    const void *gate_exps;
+    const void *up_exps;
+    const void *down_exps;
+    uint64_t gate_expert_bytes;
+    uint64_t up_expert_bytes;
+    uint64_t down_expert_bytes;
+    int gate_type, up_type, down_type;
+    const void *gate_shexp;
+    const void *up_shexp;
+    const void *down_shexp;
+    int gate_shexp_type, up_shexp_type, down_shexp_type;
+    const float *router;          /* ffn_gate_inp, fp32 [E][H] */
+    const uint16_t *shexp_gate;   /* ffn_gate_inp_shexp, fp16 [H], may be NULL */
+} bread_moe_layer_t;
+
+/* Scratch and synchronisation state for MoE calls on one stream.  Created
+ * once (all allocation happens here, none on the call path). */
+typedef struct bread_moe_ctx bread_moe_ctx_t;
+
+int bread_moe_ctx_create(const bread_moe_shape_t *shape, int max_tokens,
+                         bread_moe_ctx_t **out);
+int bread_moe_ctx_destroy(bread_moe_ctx_t *ctx);
+
+/* Synchronises the context's last stream and returns BREAD_ERR_DEVICE (and
+ * the kernel's error word in *device_error, if given) when a kernel flagged
+ * a fault, e.g. a bounded wait that expired.  Clears the word. */
+int bread_moe_ctx_check(bread_moe_ctx_t *ctx, int *device_error);
+
+/* Routing for n_tokens tokens on the device: router GEMV (fp32), softmax,
+ * top-k with ties to the lower index, renormalised weights, and the raw
+ * shared-gate logit (before the sigmoid).  d_x is fp32 [n_tokens][H];
+ * outputs are device arrays d_idx int32 [n_tokens][K] (rank order),
+ * d_w fp32 [n_tokens][K], d_gsh fp32 [n_tokens].
+ * Device form of route_layer, one_layer.cu:937-992. */
+int bread_route(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer, const float *d_x,
+                int n_tokens, int32_t *d_idx, float *d_w, float *d_gsh,
+                bread_stream_t stream);
+
+/* route_layer-compatible shim: one token, results copied to host arrays
+ * (idx[K], w[K]) and the raw shared-gate logit returned in *gsh_logit.
+ * Synchronises the stream (route_layer does a blocking copy,
+ * one_layer.cu:319). */
+int bread_route_layer(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer, const float *d_x,
+                      int *expert_indices, float *expert_weights, float *gsh_logit,
+                      bread_stream_t stream);
+
+/* The MoE FFN for n_tokens tokens, accumulated into the residual:
+ *   hidden[t] += sigmoid(gsh_t) * shared(x_t) + sum_k w_tk * expert_{idx_tk}(x_t)
+ * with expert(x) = down(silu(gate x) * (up x)), summed per element in the
+ * reference order (shared first, then routed experts by rank).
+ * d_x_normed fp32 [n_tokens][H] (the post-attention RMSNorm output),
+ * d_hidden fp32 [n_tokens][H] in/out.  Optional outputs d_idx/d_w/d_gsh as in
+ * bread_route (may be NULL).  n_tokens == 1 runs the single-launch decode
+ * kernel; larger batches run the grouped multi-token path. */
+int bread_moe_forward(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer,
+                      const float *d_x_normed, float *d_hidden, int n_tokens,
+                      int32_t *d_idx, float *d_w, float *d_gsh, bread_stream_t stream);
+
+/* out[t] = x[t] * (1/sqrt(mean(x[t]^2) + eps)) * w, fp32, n_tokens rows of n
+ * (layer_ops.cu:203-212; the device kernel one_layer.cu:158-181 in fp32).
+ * w may be NULL for unit weights.  out may alias x. */
+int bread_rmsnorm_f32(const float *d_x, const float *d_w, float *d_out, int n, int n_tokens,
+                      float eps, bread_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* HBM-resident expert arena                                           */
+/* ------------------------------------------------------------------ */
+
+/* All experts of n_layers layers resident in HBM: one allocation per layer
+ * holding gate/up/down stacked tensors, the shared expert, the fp32 router
+ * and the fp16 shared gate, each 256-byte aligned.  Replaces the reference's
+ * 3 x 256 x 40 separate cudaMalloc calls (loader.c:628-693) and its LRU
+ * (loader.c:325-505). */
+typedef struct bread_arena bread_arena_t;
+
+int bread_arena_create(const bread_moe_shape_t *shape, int n_layers, bread_arena_t **out);
+int bread_arena_destroy(bread_arena_t *arena);
+/* Descriptor of layer `layer` (device pointers into the arena). */
+int bread_arena_layer(const bread_arena_t *arena, int layer, bread_moe_layer_t *out);
+/* Bytes of one layer's allocation. */
+uint64_t bread_arena_layer_bytes(const bread_arena_t *arena);
+
+/* ------------------------------------------------------------------ */
+/* Seeded synthetic weights (bench and test inputs)                    */
+/* ------------------------------------------------------------------ */
+
+/* Counter-based generator (SplitMix64 of seed + i * 0x9E3779B97F4A7C15),
+ * so every byte depends only on (seed, position): the same bytes on any
+ * device or host.  Q4_K: d and dmin fp16 of U(1e-3, 1e-2), scale bytes and
+ * nibbles uniform.  Q6_K: ql, qh uniform, sc int8 uniform in [-32, 31], d
+ * fp16 of U(1e-3, 1e-2).  n_blocks superblocks are written to d_dst. */
+int bread_synth_q4k(void *d_dst, uint64_t n_blocks, uint64_t seed, bread_stream_t stream);
+int bread_synth_q6k(void *d_dst, uint64_t n_blocks, uint64_t seed, bread_stream_t stream);
+/* n values ~ N(mean, std) (Box-Muller over the same counter generator), as
+ * fp32 or as fp16 bits. */
+int bread_synth_normal_f32(float *d_dst, uint64_t n, uint64_t seed, float mean, float std,
+                           bread_stream_t stream);
+int bread_synth_normal_f16(uint16_t *d_dst, uint64_t n, uint64_t seed, float mean, float std,
+                           bread_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BREAD_MOE_H */

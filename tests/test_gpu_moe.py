@@ -1,0 +1,287 @@
+"""GPU parity of routing and the MoE layer against the CPU oracle.
+
+Tier 1: routed expert indices bit-exact (rank order), ties to the lower index.
+Tier 2: layer output within 1e-3 relative L2 and 1e-2 max-abs of the oracle's
+fp32 computation on the same seeded inputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+import breadv2_amd as B
+from breadv2_amd import api
+from oracle import oracle as O
+
+from helpers import MAX_ABS_TOL, REL_L2_TOL, arena_host_layer, host_layer, max_abs, rel_l2
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module")
+def full_layer():
+    s = api.shape()
+    t = api.synth_layer_tensors(s, seed=1234, layer=0)
+    torch.cuda.synchronize()
+    return s, t, host_layer(t)
+
+
+def xs(n_tokens: int, H: int, seed: int) -> np.ndarray:
+    return np.random.default_rng(seed).standard_normal((n_tokens, H)).astype(np.float32)
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def run_forward(ctx, t, x: np.ndarray, hidden: np.ndarray):
+    T = x.shape[0]
+    xd, hd = dev(x), dev(hidden)
+    idx, w, g = ctx.forward(t.desc(), xd, hd, T, want_routing=True)
+    torch.cuda.synchronize()
+    return hd.cpu().numpy(), idx.cpu().numpy(), w.cpu().numpy(), g.cpu().numpy()
+
+
+def oracle_forward(hl, x: np.ndarray, hidden: np.ndarray):
+    h = np.array(hidden, np.float32, copy=True)
+    idx, w, g = O.moe_forward(hl, x, h, x.shape[0], nthreads=8)
+    return h, idx, w, g
+
+
+# ------------------------------------------------------------------ routing
+
+
+def test_route_matches_oracle(full_layer):
+    s, t, hl = full_layer
+    T = 48
+    x = xs(T, s.hidden, 1)
+    ctx = B.MoeContext(s, max_tokens=T)
+    idx, w, g = ctx.route(t.desc(), dev(x), T)
+    torch.cuda.synchronize()
+    idx, w, g = idx.cpu().numpy(), w.cpu().numpy(), g.cpu().numpy()
+    for i in range(T):
+        ri, rw, rg = O.route(hl, x[i])
+        assert np.array_equal(idx[i], ri), f"token {i}: {idx[i]} vs {ri}"
+        np.testing.assert_allclose(w[i], rw, rtol=2e-5, atol=1e-7)
+        np.testing.assert_allclose(g[i], rg, rtol=1e-4, atol=1e-5)
+        assert abs(float(np.sum(w[i], dtype=np.float64)) - 1.0) < 1e-5
+
+
+def test_route_ties_go_to_lower_index(full_layer):
+    """Identical router rows give bit-identical logits; the lower index must
+    rank first (layer_ops.cu:241 strict '>' scan).  Covers a tie inside the
+    top-K and a tie straddling the K/K+1 boundary."""
+    s, t, _ = full_layer
+    router = t.router.clone().view(s.n_experts, s.hidden)
+    x = xs(1, s.hidden, 2)[0]
+    xd = dev(x)
+    base = torch.from_numpy(x / np.linalg.norm(x)).to(DEV)
+    # experts 200 and 7 share a strong row; 150 and 3 share a weaker one
+    router[200] = 3.0 * base
+    router[7] = 3.0 * base
+    router[150] = 1.5 * base
+    router[3] = 1.5 * base
+    lt = api.LayerTensors(s, t.gate_exps, t.up_exps, t.down_exps, t.gate_sh, t.up_sh, t.down_sh,
+                          router.contiguous().view(-1), t.shgate)
+    ctx = B.MoeContext(s, max_tokens=1)
+    idx, w, g = ctx.route(lt.desc(), xd, 1)
+    torch.cuda.synchronize()
+    idx = idx.cpu().numpy()[0]
+    assert list(idx[:4]) == [7, 200, 3, 150]
+    hl = O.HostLayer(O.OShape(s.hidden, s.expert_inter, s.shared_inter, s.n_experts, s.top_k),
+                     np.zeros(1, np.uint8), np.zeros(1, np.uint8), np.zeros(1, np.uint8), np.zeros(1, np.uint8),
+                     np.zeros(1, np.uint8), np.zeros(1, np.uint8), router.cpu().numpy(),
+                     t.shgate.cpu().numpy().view(np.uint16))
+    ri, rw, _ = O.route(hl, x)
+    assert np.array_equal(idx, ri)
+
+
+def test_route_boundary_tie_k():
+    """A K=2 selection where ranks 2 and 3 tie exactly: the lower index is in."""
+    s = api.shape(hidden=512, expert_inter=256, shared_inter=256, n_experts=16, top_k=2)
+    t = api.synth_layer_tensors(s, seed=77)
+    router = torch.zeros(16, 512, device=DEV)
+    x = np.ones(512, np.float32)
+    router[9, :] = 0.01
+    router[12, :] = 0.005
+    router[4, :] = 0.005  # ties with 12: 4 must win
+    t.router.copy_(router.view(-1))
+    ctx = B.MoeContext(s, max_tokens=1)
+    idx, w, _ = ctx.route(t.desc(), dev(x[None]), 1)
+    torch.cuda.synchronize()
+    assert list(idx.cpu().numpy()[0]) == [9, 4]
+
+
+def test_route_nan_rule(full_layer):
+    """A NaN logit makes every probability NaN; the defined rule takes the
+    lowest unused indices 0..K-1 in order (the oracle's rule)."""
+    s, t, hl = full_layer
+    x = xs(1, s.hidden, 3)
+    x[0, 5] = np.nan
+    ctx = B.MoeContext(s, max_tokens=1)
+    idx, w, _ = ctx.route(t.desc(), dev(x), 1)
+    torch.cuda.synchronize()
+    ri, rw, _ = O.route(hl, x[0])
+    assert list(ri) == list(range(s.top_k))
+    assert np.array_equal(idx.cpu().numpy()[0], ri)
+    assert np.all(np.isnan(w.cpu().numpy()))
+
+
+def test_route_layer_shim(full_layer):
+    s, t, hl = full_layer
+    x = xs(1, s.hidden, 4)
+    ctx = B.MoeContext(s, max_tokens=1)
+    hi, hw, hg = ctx.route_layer(t.desc(), dev(x))
+    ri, rw, rg = O.route(hl, x[0])
+    assert hi == list(ri)
+    np.testing.assert_allclose(hw, rw, rtol=2e-5)
+    np.testing.assert_allclose(hg, rg, rtol=1e-4, atol=1e-5)
+
+
+# ------------------------------------------------------------------ MoE layer
+
+
+def test_decode_layer_matches_oracle(full_layer):
+    """Config 2: one decode token through the single-launch kernel."""
+    s, t, hl = full_layer
+    ctx = B.MoeContext(s, max_tokens=1)
+    for seed in range(4):
+        x = xs(1, s.hidden, 100 + seed)
+        hidden = np.zeros((1, s.hidden), np.float32) if seed % 2 == 0 else xs(1, s.hidden, 200 + seed)
+        got, gi, gw, gg = run_forward(ctx, t, x, hidden)
+        ref, ri, rw, rg = oracle_forward(hl, x, hidden)
+        assert np.array_equal(gi, ri)
+        np.testing.assert_allclose(gw, rw, rtol=2e-5, atol=1e-7)
+        d_got = got - hidden
+        d_ref = ref - hidden
+        assert rel_l2(d_got, d_ref) < REL_L2_TOL
+        assert max_abs(got, ref) < MAX_ABS_TOL
+        # far tighter than the contract: fp32 with a different summation order
+        assert rel_l2(d_got, d_ref) < 1e-5
+    assert ctx.check_device() == 0
+
+
+def test_decode_back_to_back_launches(full_layer):
+    """The decode kernel resets its own sync block: many launches in a row,
+    alternating inputs, each equal to its single-launch result bit for bit."""
+    s, t, _ = full_layer
+    ctx = B.MoeContext(s, max_tokens=1)
+    x0, x1 = dev(xs(1, s.hidden, 5)), dev(xs(1, s.hidden, 6))
+    outs = []
+    for x in (x0, x1):
+        h = torch.zeros(1, s.hidden, device=DEV)
+        ctx.forward(t.desc(), x, h, 1)
+        outs.append(h.clone())
+    hs = [torch.zeros(1, s.hidden, device=DEV) for _ in range(20)]
+    for i, h in enumerate(hs):
+        ctx.forward(t.desc(), x0 if i % 2 == 0 else x1, h, 1)
+    torch.cuda.synchronize()
+    for i, h in enumerate(hs):
+        assert torch.equal(h, outs[i % 2]), f"launch {i}"
+    assert ctx.check_device() == 0
+
+
+def test_decode_vs_multi_kernel_path(full_layer):
+    """The single-launch kernel and the multi-kernel path agree."""
+    s, t, _ = full_layer
+    ctx = B.MoeContext(s, max_tokens=2)
+    x = xs(1, s.hidden, 8)
+    h1 = torch.zeros(1, s.hidden, device=DEV)
+    ctx.forward(t.desc(), dev(x), h1, 1)
+    h2 = torch.zeros(2, s.hidden, device=DEV)
+    ctx.forward(t.desc(), dev(np.repeat(x, 2, 0)), h2, 2)
+    torch.cuda.synchronize()
+    a, b = h1.cpu().numpy()[0], h2.cpu().numpy()
+    assert np.array_equal(b[0], b[1])
+    assert rel_l2(a, b[0]) < 1e-5
+
+
+@pytest.mark.parametrize("T", [2, 8, 16])
+def test_multi_token_matches_oracle(full_layer, T):
+    s, t, hl = full_layer
+    ctx = B.MoeContext(s, max_tokens=T)
+    x = xs(T, s.hidden, 300 + T)
+    hidden = xs(T, s.hidden, 400 + T)
+    got, gi, gw, _ = run_forward(ctx, t, x, hidden)
+    ref, ri, rw, _ = oracle_forward(hl, x, hidden)
+    assert np.array_equal(gi, ri)
+    assert rel_l2(got - hidden, ref - hidden) < REL_L2_TOL
+    assert max_abs(got, ref) < MAX_ABS_TOL
+
+
+@pytest.mark.parametrize("H,I,E,K,T", [(512, 256, 16, 2, 1), (512, 256, 16, 2, 3), (768, 512, 32, 1, 2),
+                                       (2048, 512, 64, 4, 1)])
+def test_other_shapes_match_oracle(H, I, E, K, T):
+    """Shapes the single-launch kernel is not built for run the multi-kernel
+    path; K = 1 reduces the combine to one routed expert."""
+    s = api.shape(hidden=H, expert_inter=I, shared_inter=I, n_experts=E, top_k=K)
+    t = api.synth_layer_tensors(s, seed=H + E + K)
+    hl = host_layer(t)
+    ctx = B.MoeContext(s, max_tokens=T)
+    x = xs(T, H, E)
+    hidden = np.zeros((T, H), np.float32)
+    got, gi, _, _ = run_forward(ctx, t, x, hidden)
+    ref, ri, _, _ = oracle_forward(hl, x, hidden)
+    assert np.array_equal(gi, ri)
+    assert rel_l2(got, ref) < REL_L2_TOL
+    assert max_abs(got, ref) < MAX_ABS_TOL
+
+
+def test_null_shared_gate(full_layer):
+    """No ffn_gate_inp_shexp tensor: logit 0, shared weight sigmoid(0) = 0.5
+    (one_layer.cu:974-976)."""
+    s, t, _ = full_layer
+    lt = api.LayerTensors(s, t.gate_exps, t.up_exps, t.down_exps, t.gate_sh, t.up_sh, t.down_sh, t.router, None)
+    hl = host_layer(t, drop_shgate=True)
+    ctx = B.MoeContext(s, max_tokens=1)
+    x = xs(1, s.hidden, 9)
+    hidden = np.zeros((1, s.hidden), np.float32)
+    hd = dev(hidden)
+    _, _, g = ctx.forward(lt.desc(), dev(x), hd, 1, want_routing=True)
+    torch.cuda.synchronize()
+    ref, _, _, rg = oracle_forward(hl, x, hidden)
+    assert g.item() == 0.0 and rg[0] == 0.0
+    assert rel_l2(hd.cpu().numpy(), ref) < REL_L2_TOL
+
+
+def test_rmsnorm_matches_oracle():
+    H, T = 2048, 3
+    x = xs(T, H, 10) * 3.0
+    w = np.random.default_rng(11).uniform(0.5, 1.5, H).astype(np.float32)
+    out = torch.empty(T, H, device=DEV)
+    api.bread_rmsnorm_f32(dev(x), dev(w), out, H, T, 1e-6)
+    torch.cuda.synchronize()
+    for i in range(T):
+        ref = O.rms_norm_weighted(x[i], w, 1e-6)
+        np.testing.assert_allclose(out[i].cpu().numpy(), ref, rtol=2e-6, atol=1e-7)
+
+
+def test_stack_small_matches_oracle():
+    """Config 3 in miniature: h <- h + MoE_l(RMSNorm(h)) over 3 distinct
+    layers of the HBM arena at the full layer shape, 2 steps."""
+    s = api.shape()
+    L = 3
+    arena = B.Arena(s, L)
+    for l in range(L):
+        arena.synth_layer(l, seed=99, router_std=1.0 / np.sqrt(s.hidden))
+    torch.cuda.synchronize()
+    hls = [arena_host_layer(s, arena.layer(l)) for l in range(L)]
+    ctx = B.MoeContext(s, max_tokens=1)
+    h = xs(1, s.hidden, 12)
+    hd = dev(h)
+    xn = torch.empty_like(hd)
+    href = h[0].copy()
+    ones = np.ones(s.hidden, np.float32)
+    for step in range(2):
+        for l in range(L):
+            api.bread_rmsnorm_f32(hd, None, xn, s.hidden, 1, 1e-6)
+            ctx.forward(arena.layer(l), xn, hd, 1)
+            xr = O.rms_norm_weighted(href, ones, 1e-6)
+            hh = href[None].copy()
+            O.moe_forward(hls[l], xr[None], hh, 1)
+            href = hh[0]
+    torch.cuda.synchronize()
+    got = hd.cpu().numpy()[0]
+    assert rel_l2(got - h[0], href - h[0]) < REL_L2_TOL
+    assert max_abs(got, href) < MAX_ABS_TOL
+    arena.close()
