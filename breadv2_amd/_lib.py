@@ -10,6 +10,15 @@ import ctypes
 import os
 from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_uint16, c_uint64, c_void_p
 
+# PyTorch ships its own libamdhip64/libhsa-runtime64 (same soname as the
+# system ROCm).  Loading torch first makes libbread_moe bind to that one
+# runtime; loading it second would bring a second HIP/HSA runtime into the
+# process, and the one that initialises last finds no device.
+try:
+    import torch  # noqa: F401
+except ImportError:  # plain C/ctypes users without torch: the system runtime is the only one
+    pass
+
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libbread_moe.so")
 
@@ -39,7 +48,8 @@ ERR_DEVICE = -8
 class BreadError(RuntimeError):
     def __init__(self, status: int, where: str):
         self.status = status
-        super().__init__(f"{where}: {status_str(status)} ({status})")
+        detail = lib.bread_last_error().decode(errors="replace")
+        super().__init__(f"{where}: {status_str(status)} ({status}): {detail}")
 
 
 class MoeShape(ctypes.Structure):
@@ -72,12 +82,14 @@ class MoeLayer(ctypes.Structure):
         ("down_shexp_type", c_int),
         ("router", c_void_p),
         ("shexp_gate", c_void_p),
+        ("post_norm_w", c_void_p),
     ]
 
 
 # name -> (restype, argtypes); mirrors include/bread_moe.h one to one.
 SIGNATURES = {
     "bread_status_str": (c_char_p, [c_int]),
+    "bread_last_error": (c_char_p, []),
     "bread_set_exit_on_error": (None, [c_int]),
     "bread_matvec": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "bread_matvec_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
@@ -95,6 +107,9 @@ SIGNATURES = {
         c_int,
         [c_void_p, POINTER(MoeLayer), c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p],
     ),
+    "bread_moe_decode_layers": (
+        c_int, [c_void_p, POINTER(MoeLayer), c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "bread_moe_ctx_set_trace": (c_int, [c_void_p, c_void_p, ctypes.c_size_t, POINTER(c_int)]),
     "bread_rmsnorm_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_void_p]),
     "bread_arena_create": (c_int, [POINTER(MoeShape), c_int, POINTER(c_void_p)]),
     "bread_arena_destroy": (c_int, [c_void_p]),

@@ -129,6 +129,7 @@ class LayerTensors:
             QTYPE_Q4_K, QTYPE_Q4_K, QTYPE_Q6_K,
             self.router.data_ptr(),
             self.shgate.data_ptr() if self.shgate is not None else None,
+            None,
         )
 
 
@@ -262,6 +263,29 @@ class MoeContext:
         check(lib.bread_moe_forward(self._h, ctypes.byref(layer), _p(x), _p(hidden), n_tokens, _p(idx), _p(w),
                                     _p(gsh), _s(stream)), "bread_moe_forward")
         return idx, w, gsh
+
+    def decode_layers(self, layers, hidden: torch.Tensor, want_routing: bool = False, stream=None):
+        """bread_moe_decode_layers: one token through len(layers) layers,
+        h <- h + MoE_l(RMSNorm(h) * w_l), in one launch."""
+        n = len(layers)
+        arr = (MoeLayer * n)(*layers)
+        K = self.shape.top_k
+        idx = w = gsh = None
+        if want_routing:
+            idx = torch.empty((n, K), dtype=torch.int32, device=hidden.device)
+            w = torch.empty((n, K), dtype=torch.float32, device=hidden.device)
+            gsh = torch.empty((n,), dtype=torch.float32, device=hidden.device)
+        check(lib.bread_moe_decode_layers(self._h, arr, n, _p(hidden), _p(idx), _p(w), _p(gsh), _s(stream)),
+              "bread_moe_decode_layers")
+        return idx, w, gsh
+
+    def set_trace(self, buf: torch.Tensor | None) -> int:
+        """Record the decode kernel's timeline into buf (int64 device tensor)."""
+        g = ctypes.c_int(0)
+        n = 0 if buf is None else buf.numel()
+        check(lib.bread_moe_ctx_set_trace(self._h, _p(buf), n, ctypes.byref(g)), "bread_moe_ctx_set_trace")
+        self._trace = buf
+        return g.value
 
     def check_device(self) -> int:
         e = ctypes.c_int(0)

@@ -145,28 +145,107 @@ __device__ __forceinline__ float sum16(float v)
     return v;
 }
 
+// Cross-row exchange of gfx950's v_permlane16_swap / v_permlane32_swap with
+// both operands the same register: .a holds, in every lane, the value of the
+// lane 16 (or 32) below it in its 32 (64) lane group, .b the one above, so
+// combining .a and .b merges two rows (halves) in every lane without LDS.
+struct lane_pair {
+    uint32_t a, b;
+};
+
+__device__ __forceinline__ lane_pair swap16(uint32_t v)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return {r[0], r[1]};
+}
+
+__device__ __forceinline__ lane_pair swap32(uint32_t v)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return {r[0], r[1]};
+}
+
 __device__ __forceinline__ float sum32(float v)
 {
     v = sum16(v);
-    v += __shfl_xor(v, 16);
-    return v;
+    const lane_pair p = swap16(__builtin_bit_cast(uint32_t, v));
+    return __builtin_bit_cast(float, p.a) + __builtin_bit_cast(float, p.b);
 }
 
+// Sum over the wave; the result is in every lane.
 __device__ __forceinline__ float wave_sum(float v)
 {
     v = sum32(v);
-    v += __shfl_xor(v, 32);
-    return v;
+    const lane_pair p = swap32(__builtin_bit_cast(uint32_t, v));
+    return __builtin_bit_cast(float, p.a) + __builtin_bit_cast(float, p.b);
 }
 
+// Max over the wave (NaN-ignoring fmaxf); the result is in every lane.
 __device__ __forceinline__ float wave_max(float v)
 {
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    lane_pair p = swap16(__builtin_bit_cast(uint32_t, v));
+    v = fmaxf(__builtin_bit_cast(float, p.a), __builtin_bit_cast(float, p.b));
+    p = swap32(__builtin_bit_cast(uint32_t, v));
+    return fmaxf(__builtin_bit_cast(float, p.a), __builtin_bit_cast(float, p.b));
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v)
+{
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xF, 0xF, true);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, true);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t u64_max(uint64_t a, uint64_t b)
+{
+    return b > a ? b : a;
+}
+
+// Unsigned 64-bit max over the wave; the result is in every lane.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v)
+{
+    v = u64_max(v, dpp_u64<0xB1>(v));
+    v = u64_max(v, dpp_u64<0x4E>(v));
+    v = u64_max(v, dpp_u64<0x141>(v));
+    v = u64_max(v, dpp_u64<0x140>(v));
+    lane_pair lo = swap16((uint32_t)v), hi = swap16((uint32_t)(v >> 32));
+    v = u64_max(((uint64_t)hi.a << 32) | lo.a, ((uint64_t)hi.b << 32) | lo.b);
+    lo = swap32((uint32_t)v);
+    hi = swap32((uint32_t)(v >> 32));
+    return u64_max(((uint64_t)hi.a << 32) | lo.a, ((uint64_t)hi.b << 32) | lo.b);
 }
 
 __device__ __forceinline__ int lane_id()
 {
     return (int)(threadIdx.x & (WAVE - 1));
+}
+
+// Wave index inside the workgroup, marked wave-uniform (scalar register), so
+// addresses and buffer descriptors built from it stay scalar.
+__device__ __forceinline__ int wave_id()
+{
+    return __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
+}
+
+__device__ __forceinline__ int uniform(int v)
+{
+    return __builtin_amdgcn_readfirstlane(v);
+}
+
+__device__ __forceinline__ uint64_t uniform64(uint64_t v)
+{
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+template <typename T>
+__device__ __forceinline__ T *uniform_ptr(T *p)
+{
+    return reinterpret_cast<T *>(uniform64(reinterpret_cast<uint64_t>(p)));
 }

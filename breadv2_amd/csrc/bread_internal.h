@@ -22,36 +22,59 @@ int bread_fail(int status, const char *where, const char *detail);
         if (!(cond)) return bread_fail((status), __func__, (detail));         \
     } while (0)
 
+// hipGetLastError reports the last error of any earlier HIP call on this
+// thread, including calls made by other libraries in the process.  Entry
+// points clear it before launching so the check after the launch reports
+// their own launch only.
+static inline void bread_clear_stale_error()
+{
+    (void)hipGetLastError();
+}
+
 static inline hipStream_t to_hip(bread_stream_t s)
 {
     return reinterpret_cast<hipStream_t>(s);
 }
 
-// Device-side synchronisation block of the single-launch decode kernel.
-// Every field returns to its reset value when a launch ends (the last
-// workgroup out restores it), so launches need no host-side memset and can
-// be captured in a graph.
-struct bread_sync {
-    uint32_t router_done;  // router workgroups finished
-    uint32_t h_done;       // gate/up workgroups finished
-    uint32_t exit_count;   // workgroups finished
-    uint32_t error;        // non-zero: a bounded wait expired (sticky until checked)
-    int32_t route_idx[64]; // published top-k (-1 = not yet published)
+// One counter on its own 128-byte line (atomics to one line serialise).
+struct alignas(128) bread_line {
+    uint32_t v;
+    uint32_t pad[31];
+};
+
+// Device-side synchronisation block of the persistent decode kernel.  Each
+// counter is spread over 8 lines; every field is back at zero when a launch
+// ends (the last workgroup out resets it), so launches need no host-side
+// reset.
+struct bread_decode_sync {
+    bread_line router_done[8];  // router workgroups finished, summed over lines
+    bread_line h_done[8];       // gate/up workgroups finished
+    bread_line out_done[8];     // down workgroups finished (h of the layer is complete)
+    bread_line exit1[8];        // workgroups finished, per line
+    bread_line exit2;           // lines whose workgroups all finished
+    bread_line error;           // non-zero: a bounded wait expired (sticky until checked)
 };
 
 struct bread_moe_ctx {
     bread_moe_shape_t shape;
     int max_tokens;
+    int max_layers;
     int device;
+    int decode_max_blocks;  // co-resident workgroups of the decode kernel
     hipStream_t last_stream;
     // device scratch
-    float *logits;     // [max_tokens][E]
-    float *lbound;     // [max_tokens][E] error bound of each logit
+    float *logits;     // [max_tokens][E] (+1: the decode kernel's shared-gate logit)
     int32_t *idx;      // [max_tokens][K]
     float *w;          // [max_tokens][K]
     float *gsh;        // [max_tokens]
     float *h;          // [max_tokens][K+1][Imax] SwiGLU outputs, slot 0 = shared
-    bread_sync *sync;  // decode kernel synchronisation
+    float *xnorm;      // [H] normalised input published by the decode kernel
+    bread_decode_sync *dsync;
+    void *d_layers;    // device layer table of the decode kernel [max_layers]
+    void *h_layers;    // host copy of the last uploaded table
+    int n_layers_uploaded;
+    uint64_t *trace;   // optional decode timeline (device), trace_words entries
+    size_t trace_words;
 };
 
 struct bread_arena {
@@ -73,3 +96,8 @@ int bread_launch_moe_multi(bread_moe_ctx_t *ctx, const bread_moe_layer_t *L, con
                            float *hidden, int n_tokens, hipStream_t st);
 int bread_launch_moe_decode(bread_moe_ctx_t *ctx, const bread_moe_layer_t *L, const float *x,
                             float *hidden, hipStream_t st);
+int bread_launch_decode_layers(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layers, int n, float *hidden,
+                               int32_t *idx, float *w, float *gsh, hipStream_t st);
+int bread_decode_max_blocks(int *out);
+int bread_decode_grid(const bread_moe_shape_t &s);
+size_t bread_decode_layer_record_bytes();

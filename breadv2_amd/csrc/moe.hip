@@ -16,14 +16,22 @@
 #include "route_dev.h"
 
 static int g_exit_on_error = 0;
+static thread_local char g_last_error[256];
 
 extern "C" void bread_set_exit_on_error(int enable)
 {
     g_exit_on_error = enable;
 }
 
+extern "C" const char *bread_last_error(void)
+{
+    return g_last_error;
+}
+
 int bread_fail(int status, const char *where, const char *detail)
 {
+    snprintf(g_last_error, sizeof(g_last_error), "%s: %s (%s)", where, bread_status_str(status),
+             detail ? detail : "");
     if (g_exit_on_error) {
         fprintf(stderr, "bread: %s: %s (%s)\n", where, bread_status_str(status), detail ? detail : "");
         exit(1);
@@ -111,23 +119,26 @@ extern "C" int bread_moe_ctx_create(const bread_moe_shape_t *shape, int max_toke
     BREAD_REQUIRE(c, BREAD_ERR_NOMEM, "host allocation");
     c->shape = *shape;
     c->max_tokens = max_tokens;
+    c->max_layers = 256;
     hipError_t e = hipGetDevice(&c->device);
     const int E = shape->n_experts, K = shape->top_k;
     const int Imax = shape->expert_inter > shape->shared_inter ? shape->expert_inter : shape->shared_inter;
     const size_t T = (size_t)max_tokens;
-    if (e == hipSuccess) e = hipMalloc((void **)&c->logits, T * E * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc((void **)&c->lbound, T * E * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->logits, (T * E + E + 1) * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->idx, T * K * sizeof(int32_t));
     if (e == hipSuccess) e = hipMalloc((void **)&c->w, T * K * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->gsh, T * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->h, T * (K + 1) * Imax * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc((void **)&c->sync, sizeof(bread_sync));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->xnorm, (size_t)shape->hidden * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->dsync, sizeof(bread_decode_sync));
+    if (e == hipSuccess) e = hipMemset(c->dsync, 0, sizeof(bread_decode_sync));
+    if (e == hipSuccess) e = hipMalloc(&c->d_layers, (size_t)c->max_layers * bread_decode_layer_record_bytes());
     if (e == hipSuccess) {
-        bread_sync init;
-        memset(&init, 0, sizeof(init));
-        for (int k = 0; k < 64; k++) init.route_idx[k] = -1;
-        e = hipMemcpy(c->sync, &init, sizeof(init), hipMemcpyHostToDevice);
+        c->h_layers = calloc((size_t)c->max_layers, bread_decode_layer_record_bytes());
+        if (!c->h_layers) e = hipErrorOutOfMemory;
     }
+    if (e == hipSuccess && bread_decode_max_blocks(&c->decode_max_blocks) != BREAD_OK) e = hipErrorUnknown;
+    if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         bread_moe_ctx_destroy(c);
         return bread_fail(e == hipErrorOutOfMemory ? BREAD_ERR_NOMEM : BREAD_ERR_HIP, "bread_moe_ctx_create",
@@ -141,12 +152,14 @@ extern "C" int bread_moe_ctx_destroy(bread_moe_ctx_t *c)
 {
     if (!c) return BREAD_OK;
     (void)hipFree(c->logits);
-    (void)hipFree(c->lbound);
     (void)hipFree(c->idx);
     (void)hipFree(c->w);
     (void)hipFree(c->gsh);
     (void)hipFree(c->h);
-    (void)hipFree(c->sync);
+    (void)hipFree(c->xnorm);
+    (void)hipFree(c->dsync);
+    (void)hipFree(c->d_layers);
+    free(c->h_layers);
     free(c);
     return BREAD_OK;
 }
@@ -156,13 +169,23 @@ extern "C" int bread_moe_ctx_check(bread_moe_ctx_t *c, int *device_error)
     BREAD_REQUIRE(c, BREAD_ERR_ARG, "NULL context");
     BREAD_HIP(hipStreamSynchronize(c->last_stream));
     uint32_t err = 0;
-    BREAD_HIP(hipMemcpy(&err, &c->sync->error, sizeof(err), hipMemcpyDeviceToHost));
+    BREAD_HIP(hipMemcpy(&err, &c->dsync->error.v, sizeof(err), hipMemcpyDeviceToHost));
     if (device_error) *device_error = (int)err;
     if (err) {
-        const uint32_t zero = 0;
-        BREAD_HIP(hipMemcpy(&c->sync->error, &zero, sizeof(zero), hipMemcpyHostToDevice));
+        // a launch that gave up waiting may have left counters half-way: start clean
+        BREAD_HIP(hipMemset(c->dsync, 0, sizeof(bread_decode_sync)));
+        BREAD_HIP(hipDeviceSynchronize());
         return bread_fail(BREAD_ERR_DEVICE, "bread_moe_ctx_check", "a kernel flagged an error");
     }
+    return BREAD_OK;
+}
+
+extern "C" int bread_moe_ctx_set_trace(bread_moe_ctx_t *c, uint64_t *d_buf, size_t n_words, int *grid_out)
+{
+    BREAD_REQUIRE(c, BREAD_ERR_ARG, "NULL context");
+    c->trace = d_buf;
+    c->trace_words = d_buf ? n_words : 0;
+    if (grid_out) *grid_out = bread_decode_grid(c->shape);
     return BREAD_OK;
 }
 
@@ -299,6 +322,7 @@ int bread_launch_route(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const flo
 {
     const bread_moe_shape_t &s = c->shape;
     const int waves = s.n_experts + 1;
+    bread_clear_stale_error();
     hipLaunchKernelGGL(k_router, dim3((waves + 3) / 4), dim3(256), 0, st, L->router, L->shexp_gate, x, c->logits,
                        gsh, s.hidden, s.n_experts, T);
     BREAD_HIP(hipGetLastError());
@@ -382,12 +406,33 @@ extern "C" int bread_moe_forward(bread_moe_ctx_t *c, const bread_moe_layer_t *L,
     return BREAD_OK;
 }
 
+extern "C" int bread_moe_decode_layers(bread_moe_ctx_t *c, const bread_moe_layer_t *layers, int n,
+                                       float *hidden, int32_t *idx, float *w, float *gsh, bread_stream_t stream)
+{
+    BREAD_REQUIRE(c && layers && hidden, BREAD_ERR_ARG, "NULL context, layers or hidden");
+    BREAD_REQUIRE(n >= 0, BREAD_ERR_ARG, "n_layers < 0");
+    BREAD_REQUIRE(((uintptr_t)hidden & 15) == 0, BREAD_ERR_ALIGN, "hidden must be 16-byte aligned");
+    for (int l = 0; l < n; l++) {
+        int rc = bread_validate_layer(&c->shape, &layers[l]);
+        if (rc) return rc;
+        BREAD_REQUIRE(((uintptr_t)layers[l].post_norm_w & 15) == 0, BREAD_ERR_ALIGN,
+                      "post_norm_w must be 16-byte aligned");
+    }
+    if (n == 0) return BREAD_OK;
+    hipStream_t st = to_hip(stream);
+    c->last_stream = st;
+    int rc = bread_launch_decode_layers(c, layers, n, hidden, idx, w, gsh, st);
+    if (rc == BREAD_ERR_SHAPE) return bread_fail(rc, "bread_moe_decode_layers", "shape not supported by the decode kernel");
+    return rc;
+}
+
 extern "C" int bread_rmsnorm_f32(const float *x, const float *w, float *out, int n, int T, float eps,
                                  bread_stream_t stream)
 {
     BREAD_REQUIRE(x && out, BREAD_ERR_ARG, "NULL pointer");
     BREAD_REQUIRE(n > 0 && T >= 0, BREAD_ERR_ARG, "n must be > 0 and n_tokens >= 0");
     if (T == 0) return BREAD_OK;
+    bread_clear_stale_error();
     hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(256), 0, to_hip(stream), x, w, out, n, eps);
     BREAD_HIP(hipGetLastError());
     return BREAD_OK;

@@ -147,6 +147,7 @@ int launch_matvec(const void *w, const XT *x, YT *y, int rows, int cols, int qty
     if (rc) return rc;
     if (rows == 0) return BREAD_OK;
     const uint64_t rb = row_bytes_of(qtype, cols);
+    bread_clear_stale_error();
     const int waves_per_block = 4;
     int blocks = (rows + waves_per_block - 1) / waves_per_block;
     if (blocks > 65536) blocks = 65536;
@@ -193,6 +194,7 @@ extern "C" int bread_dequant_rows(const void *w, int qtype, int rows, int cols, 
     BREAD_REQUIRE(((uintptr_t)out & 15) == 0, BREAD_ERR_ALIGN, "out must be 16-byte aligned");
     if (rows == 0) return BREAD_OK;
     hipStream_t st = to_hip(stream);
+    bread_clear_stale_error();
     const uint64_t n_blocks = (uint64_t)rows * (uint64_t)(cols / blk);
     const uint8_t *wb = (const uint8_t *)w;
     if (qtype == BREAD_QTYPE_Q8_0) {

@@ -32,19 +32,17 @@ __device__ __forceinline__ float prob_from_key(uint32_t k)
 //     takes the lowest unused index.
 // E <= 64 * MAXV.  Lane k < K returns idx_k / w_k (rank order).
 template <int MAXV>
-__device__ __forceinline__ void topk_wave(const float *logits, int E, int K, int &idx_k, float &w_k)
+__device__ __forceinline__ void topk_wave_vals(float (&p)[MAXV], int E, int K, int &idx_k, float &w_k)
 {
     const int lane = lane_id();
-    float p[MAXV];
     float mx = -__builtin_inff();
 #pragma unroll
     for (int v = 0; v < MAXV; v++) {
         const int i = lane + WAVE * v;
-        p[v] = i < E ? logits[i] : -__builtin_inff();
-        if (p[v] == p[v]) mx = fmaxf(mx, p[v]);
+        if (i < E && p[v] == p[v]) mx = fmaxf(mx, p[v]);
     }
     mx = wave_max(mx);
-    const float l0 = __shfl(p[0], 0);
+    const float l0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[0]), 0));
     if (l0 != l0) mx = l0;
     float s = 0.f;
 #pragma unroll
@@ -61,50 +59,43 @@ __device__ __forceinline__ void topk_wave(const float *logits, int E, int K, int
     int my_idx = 0;
     float my_w = 0.f;
     for (int k = 0; k < K; k++) {
-        // lane-local best unused candidate: key, then lower index
-        uint32_t bk = 0u, bi = 0xFFFFFFFFu;
-        bool have = false;
+        // candidate = (probability key, ~index): the unsigned max is the
+        // largest probability, equal ones going to the lower index; 0 = none
+        uint64_t best = 0;
 #pragma unroll
         for (int v = 0; v < MAXV; v++) {
             const int i = lane + WAVE * v;
-            if (i < E && !((used >> v) & 1u)) {
-                const uint32_t key = prob_key(p[v]);
-                if (!have || key > bk) {  // v ascending == index ascending
-                    bk = key;
-                    bi = (uint32_t)i;
-                    have = true;
-                }
-            }
+            if (i < E && !((used >> v) & 1u))
+                best = u64_max(best, ((uint64_t)prob_key(p[v]) << 32) | (uint32_t)~(uint32_t)i);
         }
-        // 64-bit compare: (key, ~index), larger wins
-        uint32_t ck = have ? bk : 0u;
-        uint32_t ci = have ? ~bi : 0u;
-        bool cv = have;
-#pragma unroll
-        for (int o = 1; o < WAVE; o <<= 1) {
-            const uint32_t ok = __shfl_xor(ck, o);
-            const uint32_t oi = __shfl_xor(ci, o);
-            const bool ov = __shfl_xor((int)cv, o) != 0;
-            const bool take = ov && (!cv || ok > ck || (ok == ck && oi > ci));
-            if (take) {
-                ck = ok;
-                ci = oi;
-                cv = true;
-            }
-        }
-        const int win = (int)(~ci);
-        if ((win & (WAVE - 1)) == lane) used |= 1u << (win / WAVE);
+        const uint64_t win = wave_max_u64(best);
+        const int widx = (int)~(uint32_t)win;
+        if ((widx & (WAVE - 1)) == lane) used |= 1u << (widx / WAVE);
         if (lane == k) {
-            my_idx = win;
-            my_w = prob_from_key(ck);
+            my_idx = widx;
+            my_w = prob_from_key((uint32_t)(win >> 32));
         }
     }
     // rank-order sum, then renormalise (layer_ops.cu:244-249)
     float w_sum = 0.f;
-    for (int k = 0; k < K; k++) w_sum += __shfl(my_w, k);
+    for (int k = 0; k < K; k++)
+        w_sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_w), k));
     if (w_sum > 0.f) my_w = my_w / w_sum;
     idx_k = my_idx;
     w_k = my_w;
+}
+
+template <int MAXV>
+__device__ __forceinline__ void topk_wave(const float *logits, int E, int K, int &idx_k, float &w_k)
+{
+    const int lane = lane_id();
+    float p[MAXV];
+#pragma unroll
+    for (int v = 0; v < MAXV; v++) {
+        const int i = lane + WAVE * v;
+        p[v] = i < E ? logits[i] : -__builtin_inff();
+    }
+    topk_wave_vals<MAXV>(p, E, K, idx_k, w_k);
 }
 
 // Dot of one fp32 router row (H = 256 * NB4) with x: lane holds columns

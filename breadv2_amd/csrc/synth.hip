@@ -135,6 +135,7 @@ extern "C" int bread_synth_q4k(void *dst, uint64_t n_blocks, uint64_t seed, brea
     BREAD_REQUIRE(((uintptr_t)dst & 3) == 0, BREAD_ERR_ALIGN, "destination must be 4-byte aligned");
     if (!n_blocks) return BREAD_OK;
     const uint64_t nb = n_blocks * Q4K_BYTES;
+    bread_clear_stale_error();
     hipLaunchKernelGGL(k_synth_quant<BREAD_QTYPE_Q4_K>, grid_for((nb + 3) / 4), dim3(256), 0, to_hip(stream),
                        (uint8_t *)dst, nb, seed);
     BREAD_HIP(hipGetLastError());
@@ -147,6 +148,7 @@ extern "C" int bread_synth_q6k(void *dst, uint64_t n_blocks, uint64_t seed, brea
     BREAD_REQUIRE(((uintptr_t)dst & 3) == 0, BREAD_ERR_ALIGN, "destination must be 4-byte aligned");
     if (!n_blocks) return BREAD_OK;
     const uint64_t nb = n_blocks * Q6K_BYTES;
+    bread_clear_stale_error();
     hipLaunchKernelGGL(k_synth_quant<BREAD_QTYPE_Q6_K>, grid_for((nb + 3) / 4), dim3(256), 0, to_hip(stream),
                        (uint8_t *)dst, nb, seed);
     BREAD_HIP(hipGetLastError());
@@ -158,6 +160,7 @@ extern "C" int bread_synth_normal_f32(float *dst, uint64_t n, uint64_t seed, flo
 {
     BREAD_REQUIRE(dst, BREAD_ERR_ARG, "NULL destination");
     if (!n) return BREAD_OK;
+    bread_clear_stale_error();
     hipLaunchKernelGGL(k_synth_normal<float>, grid_for((n + 1) / 2), dim3(256), 0, to_hip(stream), dst, n, seed,
                        mean, std);
     BREAD_HIP(hipGetLastError());
@@ -169,6 +172,7 @@ extern "C" int bread_synth_normal_f16(uint16_t *dst, uint64_t n, uint64_t seed, 
 {
     BREAD_REQUIRE(dst, BREAD_ERR_ARG, "NULL destination");
     if (!n) return BREAD_OK;
+    bread_clear_stale_error();
     hipLaunchKernelGGL(k_synth_normal<uint16_t>, grid_for((n + 1) / 2), dim3(256), 0, to_hip(stream), dst, n,
                        seed, mean, std);
     BREAD_HIP(hipGetLastError());

@@ -63,6 +63,10 @@ typedef enum {
 /* Text for a status code (static storage). */
 const char *bread_status_str(int status);
 
+/* Where and why the last failing entry point on this thread failed,
+ * including the HIP runtime's message for BREAD_ERR_HIP ("" if none). */
+const char *bread_last_error(void);
+
 /* When non-zero, every entry point that would return an error prints it and
  * calls exit(1), as the reference does (bread_utils.h:14-21,
  * kernels.cu:303-307).  Default 0. */
@@ -132,6 +136,9 @@ typedef struct {
     int gate_shexp_type, up_shexp_type, down_shexp_type;
     const float *router;          /* ffn_gate_inp, fp32 [E][H] */
     const uint16_t *shexp_gate;   /* ffn_gate_inp_shexp, fp16 [H], may be NULL */
+    const float *post_norm_w;     /* post_attention_norm, fp32 [H] (loader.h:88), may be
+                                     NULL for unit weights; read by bread_moe_decode_layers
+                                     only (bread_moe_forward takes the normalised input) */
 } bread_moe_layer_t;
 
 /* Scratch and synchronisation state for MoE calls on one stream.  Created
@@ -176,6 +183,30 @@ int bread_route_layer(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer, cons
 int bread_moe_forward(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer,
                       const float *d_x_normed, float *d_hidden, int n_tokens,
                       int32_t *d_idx, float *d_w, float *d_gsh, bread_stream_t stream);
+
+/* One decode token through a stack of MoE layers in a single launch:
+ *   for l < n_layers:  x = RMSNorm(hidden) * layers[l].post_norm_w  (eps = shape.rms_eps);
+ *                      hidden += MoE_l(x)
+ * the MoE part of the reference's per-layer loop (main.cu:685 ->
+ * one_layer.cu:1812-1983, with the fp32 order of :1413-1471).  d_hidden is
+ * fp32 [H] in/out.  Optional per-layer routing outputs d_idx int32
+ * [n_layers][K], d_w fp32 [n_layers][K], d_gsh fp32 [n_layers] (raw
+ * shared-gate logits); NULL skips them.  Needs the shape the persistent
+ * kernel is built for (H 2048, I = I_sh = 512, E <= 256, K <= 11) and
+ * n_layers <= 256; returns BREAD_ERR_SHAPE otherwise.  The host layer array
+ * is copied into the context; a different array than the previous call's
+ * costs one synchronous upload. */
+int bread_moe_decode_layers(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layers, int n_layers,
+                            float *d_hidden, int32_t *d_idx, float *d_w, float *d_gsh,
+                            bread_stream_t stream);
+
+/* Timeline of the decode kernel: when d_buf is non-NULL, every launch with
+ * grid * n_layers * 8 <= n_words records 64-bit wall-clock stamps (100 MHz)
+ * at d_buf[(workgroup * n_layers + layer) * 8 + point], points 0 start,
+ * 1 inputs ready, 2 routing known, 3 weight loads issued, 4 SwiGLU outputs
+ * ready, 5 done.  *grid_out receives the launch's workgroup count.  NULL
+ * turns it off. */
+int bread_moe_ctx_set_trace(bread_moe_ctx_t *ctx, uint64_t *d_buf, size_t n_words, int *grid_out);
 
 /* out[t] = x[t] * (1/sqrt(mean(x[t]^2) + eps)) * w, fp32, n_tokens rows of n
  * (layer_ops.cu:203-212; the device kernel one_layer.cu:158-181 in fp32).

@@ -66,3 +66,41 @@ def arena_host_layer(s, d) -> "O.HostLayer":
         d2h(d.up_shexp, b["up_sh"]), d2h(d.down_shexp, b["down_sh"]),
         d2h(d.router, b["router"]).view(np.float32), d2h(d.shexp_gate, b["shgate"]).view(np.uint16),
     )
+
+
+def assert_moe_close(got, ref, base=None):
+    """The north-star tolerance on a MoE-layer output: relative L2 < 1e-3 and
+    max-abs < 1e-2.  `base` (the residual added before the layer) is removed
+    first so the check is on the layer's own contribution.  At BASELINE's
+    synthetic weight scale (d ~ U(1e-3, 1e-2), 6-bit scales) outputs reach
+    1e5..1e6, where one fp32 ulp is 0.01..0.1, so the max-abs bound is applied
+    to the output divided by its RMS; the unit-scale tests apply it raw."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    if base is not None:
+        got = got - np.asarray(base, np.float64)
+        ref = ref - np.asarray(base, np.float64)
+    rl2 = rel_l2(got, ref)
+    rms = float(np.sqrt(np.mean(ref * ref)))
+    assert rl2 < REL_L2_TOL, f"rel L2 {rl2:.3e}"
+    assert max_abs(got, ref) / max(rms, 1.0) < MAX_ABS_TOL, f"max-abs {max_abs(got, ref):.3e} (rms {rms:.3e})"
+    return rl2
+
+
+def scale_layer_d(t, shift: int = 6) -> None:
+    """Divide every superblock scale (d, dmin of Q4_K; d of Q6_K) of a device
+    layer by 2**shift in place (exact in fp16 for BASELINE's range), so the
+    layer's outputs are of order one."""
+    import torch
+
+    f = np.float16(2.0 ** -shift)
+    for name in ("gate_exps", "up_exps", "gate_sh", "up_sh"):
+        a = getattr(t, name).cpu().numpy().reshape(-1, 144)
+        hv = a[:, 0:4].copy().view(np.float16) * f
+        a[:, 0:4] = hv.view(np.uint8)
+        getattr(t, name).copy_(torch.from_numpy(a.reshape(-1)))
+    for name in ("down_exps", "down_sh"):
+        a = getattr(t, name).cpu().numpy().reshape(-1, 210)
+        hv = a[:, 208:210].copy().view(np.float16) * f
+        a[:, 208:210] = hv.view(np.uint8)
+        getattr(t, name).copy_(torch.from_numpy(a.reshape(-1)))
