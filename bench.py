@@ -6,10 +6,12 @@ working set is ~21 GB, far above the 256 MB Infinity Cache): all 256 experts
 of 40 layers resident in HBM (Qwen3.5-35B-A3B shape: hidden 2048, expert and
 shared intermediate 512, 256 experts, top-8, Q4_K gate/up, Q6_K down, fp32
 router ~N(0, 0.02), fp16 shared gate).  One step = one MoE layer for one
-decode token:
+decode token, one kernel launch:
     x = RMSNorm(h)  (eps 1e-6, unit weights);  h += MoE_l(x)
 with l cycling over the 40 resident layers, each step reading the previous
 step's output (a real decode dependency, no overlap between steps).
+config.stack reports configs[2] as well: one decode token through all 40
+layers in a single launch, 128 tokens.
 
 value = decode MoE-layer tokens per second (steps / s).
 roofline: the single-launch MoE kernel, expert-weight bytes per launch
@@ -95,6 +97,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--layers", type=int, default=40)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--stack-tokens", type=int, default=128,
+                    help="config 3: decode tokens through the whole resident stack, one launch per token")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 512 MiB device copy (known bytes) to calibrate rocprofv3 FETCH/WRITE_SIZE")
@@ -125,11 +129,10 @@ def main() -> int:
     ctx = B.MoeContext(s, max_tokens=1)
     stream = torch.cuda.Stream()
     h = torch.randn(1, s.hidden, device="cuda:0", generator=torch.Generator("cuda:0").manual_seed(1))
-    xn = torch.empty_like(h)
 
     def step(i):
-        api.bread_rmsnorm_f32(h, None, xn, s.hidden, 1, 1e-6, stream)
-        ctx.forward(descs[i % L], xn, h, 1, stream=stream)
+        # one MoE layer of one decode token: x = RMSNorm(h); h += MoE_l(x), one launch
+        ctx.decode_layers([descs[i % L]], h, stream=stream)
 
     with torch.cuda.stream(stream):
         for i in range(args.warmup):
@@ -149,16 +152,32 @@ def main() -> int:
         total_ms = e0.elapsed_time(e1)
         log(f"timed {args.steps} steps: {total_ms:.2f} ms")
 
-        # per-launch duration of the MoE kernel (events around each launch)
+        # per-launch duration of the MoE kernel (events around each launch, on
+        # the stream it runs on)
         nk = min(args.steps, 1000)
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nk)]
         for i in range(nk):
-            api.bread_rmsnorm_f32(h, None, xn, s.hidden, 1, 1e-6, stream)
             evs[i][0].record(stream)
-            ctx.forward(descs[i % L], xn, h, 1, stream=stream)
+            step(i)
             evs[i][1].record(stream)
         torch.cuda.synchronize()
         kern_us = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+
+        # config 3: the whole 40-layer stack per decode token, one launch
+        stack_us = None
+        if args.stack_tokens > 0:
+            for _ in range(3):
+                ctx.decode_layers(descs, h, stream=stream)
+            torch.cuda.synchronize()
+            s0 = torch.cuda.Event(enable_timing=True)
+            s1 = torch.cuda.Event(enable_timing=True)
+            s0.record(stream)
+            for _ in range(args.stack_tokens):
+                ctx.decode_layers(descs, h, stream=stream)
+            s1.record(stream)
+            torch.cuda.synchronize()
+            stack_us = s0.elapsed_time(s1) * 1e3 / args.stack_tokens
+            log(f"stack: {args.stack_tokens} tokens x {L} layers, {stack_us:.1f} us/token")
     if ctx.check_device():
         raise RuntimeError("decode kernel flagged a device error")
     if args.calib_copy:
@@ -194,8 +213,8 @@ def main() -> int:
             "global_batch": 1,
             "resident_layers": L,
             "resident_gb": round(L * arena.layer_bytes / 1e9, 2),
-            "step": "rmsnorm + single-launch MoE layer",
-            "tok_s_40_layer_stack": round(value / 40.0, 2),
+            "step": "one launch: RMSNorm + MoE layer (router GEMV, softmax/top-8, gate/up, SwiGLU, down, "
+                    "shared expert, combine)",
         },
         "roofline": {
             "bound": "hbm",
@@ -214,6 +233,16 @@ def main() -> int:
         },
         "cpu_baseline": None,
     }
+    if stack_us is not None:
+        result["config"]["stack"] = {
+            "workload": f"config3: one decode token through all {L} resident layers per launch",
+            "tokens": args.stack_tokens,
+            "us_per_token": round(stack_us, 2),
+            "tok_s": round(1e6 / stack_us, 1),
+            "layer_tok_s": round(L * 1e6 / stack_us, 1),
+            "expert_gbs": round(L * LAYER_EXPERT_BYTES / (stack_us * 1e-6) / 1e9, 1),
+            "frac": round(L * LAYER_EXPERT_BYTES / (stack_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        }
     if not args.no_cpu:
         res, threads, cores = cpu_baseline(arena, s, args.cpu_seconds)
         v, n, el = res[threads]

@@ -42,17 +42,9 @@ struct alignas(128) bread_line {
     uint32_t pad[31];
 };
 
-// Device-side synchronisation block of the persistent decode kernel.  Each
-// counter is spread over 8 lines; every field is back at zero when a launch
-// ends (the last workgroup out resets it), so launches need no host-side
-// reset.
+// Device-side status of the persistent decode kernel.
 struct bread_decode_sync {
-    bread_line router_done[8];  // router workgroups finished, summed over lines
-    bread_line h_done[8];       // gate/up workgroups finished
-    bread_line out_done[8];     // down workgroups finished (h of the layer is complete)
-    bread_line exit1[8];        // workgroups finished, per line
-    bread_line exit2;           // lines whose workgroups all finished
-    bread_line error;           // non-zero: a bounded wait expired (sticky until checked)
+    bread_line error;  // non-zero: a bounded wait expired (sticky until checked)
 };
 
 struct bread_moe_ctx {
@@ -68,7 +60,11 @@ struct bread_moe_ctx {
     float *w;          // [max_tokens][K]
     float *gsh;        // [max_tokens]
     float *h;          // [max_tokens][K+1][Imax] SwiGLU outputs, slot 0 = shared
-    float *xnorm;      // [H] normalised input published by the decode kernel
+    uint64_t *tlogits; // [256] decode router logits, (epoch tag << 32) | fp32 bits
+    float *xbuf;       // [2][H] decode layer outputs by parity (sentinel = unwritten)
+    float *hbuf;       // [3][(Kmax+1) * I] decode SwiGLU outputs by layer mod 3
+    uint32_t epoch;    // layers run by the decode kernel on this context
+    int hphase;        // epoch mod 3
     bread_decode_sync *dsync;
     void *d_layers;    // device layer table of the decode kernel [max_layers]
     void *h_layers;    // host copy of the last uploaded table
@@ -100,4 +96,8 @@ int bread_launch_decode_layers(bread_moe_ctx_t *ctx, const bread_moe_layer_t *la
                                int32_t *idx, float *w, float *gsh, hipStream_t st);
 int bread_decode_max_blocks(int *out);
 int bread_decode_grid(const bread_moe_shape_t &s);
+int bread_decode_trace_points();
+int bread_decode_reset(bread_moe_ctx_t *ctx);
+size_t bread_decode_xbuf_floats();
+size_t bread_decode_hbuf_floats();
 size_t bread_decode_layer_record_bytes();

@@ -129,9 +129,11 @@ extern "C" int bread_moe_ctx_create(const bread_moe_shape_t *shape, int max_toke
     if (e == hipSuccess) e = hipMalloc((void **)&c->w, T * K * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->gsh, T * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->h, T * (K + 1) * Imax * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc((void **)&c->xnorm, (size_t)shape->hidden * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->tlogits, 256 * sizeof(uint64_t));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->xbuf, bread_decode_xbuf_floats() * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->hbuf, bread_decode_hbuf_floats() * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->dsync, sizeof(bread_decode_sync));
-    if (e == hipSuccess) e = hipMemset(c->dsync, 0, sizeof(bread_decode_sync));
+    if (e == hipSuccess && bread_decode_reset(c) != BREAD_OK) e = hipErrorUnknown;
     if (e == hipSuccess) e = hipMalloc(&c->d_layers, (size_t)c->max_layers * bread_decode_layer_record_bytes());
     if (e == hipSuccess) {
         c->h_layers = calloc((size_t)c->max_layers, bread_decode_layer_record_bytes());
@@ -156,7 +158,9 @@ extern "C" int bread_moe_ctx_destroy(bread_moe_ctx_t *c)
     (void)hipFree(c->w);
     (void)hipFree(c->gsh);
     (void)hipFree(c->h);
-    (void)hipFree(c->xnorm);
+    (void)hipFree(c->tlogits);
+    (void)hipFree(c->xbuf);
+    (void)hipFree(c->hbuf);
     (void)hipFree(c->dsync);
     (void)hipFree(c->d_layers);
     free(c->h_layers);
@@ -172,8 +176,9 @@ extern "C" int bread_moe_ctx_check(bread_moe_ctx_t *c, int *device_error)
     BREAD_HIP(hipMemcpy(&err, &c->dsync->error.v, sizeof(err), hipMemcpyDeviceToHost));
     if (device_error) *device_error = (int)err;
     if (err) {
-        // a launch that gave up waiting may have left counters half-way: start clean
-        BREAD_HIP(hipMemset(c->dsync, 0, sizeof(bread_decode_sync)));
+        // a launch that gave up waiting may have left counters half-way: start
+        // clean, counters, tags and epoch together
+        if (bread_decode_reset(c) != BREAD_OK) return BREAD_ERR_HIP;
         BREAD_HIP(hipDeviceSynchronize());
         return bread_fail(BREAD_ERR_DEVICE, "bread_moe_ctx_check", "a kernel flagged an error");
     }

@@ -1,28 +1,58 @@
-// moe_decode.hip — persistent single-launch MoE decode (one token, B = 1) for
-// gfx950 at the Qwen3.5-35B-A3B shape (H 2048, I = I_sh = 512, E <= 256,
-// K <= 11), over one layer or a stack of layers per launch.
+// moe_decode.hip — persistent MoE decode (one token, B = 1) for gfx950 at the
+// Qwen3.5-35B-A3B shape (H 2048, I = I_sh = 512, E <= 256, K <= 8), over one
+// layer or a stack of layers per launch.
 //
 // For each layer l of the launch:  x = RMSNorm(h) * w_l  (or the given x for
-// a single pre-normalised layer),  h += MoE_l(x).  One cooperative grid with
-// four workgroup roles that stay fixed across layers:
-//   router  (R): one wave per router row plus one for the shared-gate dot;
-//                router rows are loaded before h is ready; router workgroup 0
-//                also publishes the normalised x.
-//   shared  (S): shared-expert gate/up + SwiGLU (weights loaded before h is
-//                ready; they do not depend on routing).
-//   routed  (G): routed-expert gate/up + SwiGLU; each workgroup runs
-//                softmax/top-k itself from the published logits (no publish
-//                hop), then streams its rows.
-//   down    (D): down projection of all K+1 slots for DR output rows; weight
-//                loads are issued as soon as the routing is known, then the
-//                combine runs in the reference order (shared, then ranks).
-// Layer-to-layer and phase-to-phase dependencies are device counters, each
-// spread over 8 cache lines (one contended line costs ~10 ns per atomic on
-// MI355X).  Data that crosses workgroups (h, x, logits, SwiGLU outputs) is
-// written and read with device-coherent (sc1) accesses, so no L2-wide
-// writeback or invalidate is needed.  Every wait is bounded and flags an
-// error instead of hanging; the last workgroup out resets the counters, so
-// launches need no host-side reset.
+// a single pre-normalised layer),  h += MoE_l(x).
+//
+// Grid: one 1024-thread workgroup per CU (256), all resident at once.
+// Workgroup g owns router row g, gate/up rows 2g and 2g+1 of every expert
+// slot (slot 0 = shared expert, slot k = routed rank k-1) and output rows
+// 8g..8g+7.  Its 16 waves have fixed jobs:
+//   waves 0..3   poll the previous layer's output and the router logits
+//                (wave 0 then runs softmax/top-k and the combine);
+//   waves 1..8   router row and shared-gate dot, then the gate/up rows of
+//                routed slot k = wave;
+//   waves 9, 10  shared-expert gate/up rows (before routing is known);
+//   waves 9..15  the down-projection bands of the routed slots (8 rows x
+//                420 B each);
+//   waves 4..15  the next layer's routing-independent weights (router row,
+//                norm weights, shared-gate vector, shared gate/up rows and
+//                shared down band), once this layer's h is in.
+// Weights travel HBM -> LDS by gfx950 direct-to-LDS loads, so no wave holds
+// weight registers while loads are in flight.  Waves that issue loads are
+// never the ones that poll: on gfx9, s_waitcnt vmcnt counts loads and stores
+// together and in order, so a poll issued behind weight loads would wait for
+// them.
+//
+// Routing is published rank by rank: wave 0 writes expert k to LDS as soon as
+// selection pass k ends, and the gate/up and down waves start that slot's
+// loads at once, so the top-k passes overlap the expert streams.  The Q6_K
+// down weights are dequantised into registers while h is in flight; after it
+// arrives only the dot products remain.
+//
+// Three exchanges per layer cross workgroups, each carried by the data
+// itself (no counters, no atomics, no waits for store completion):
+//   logits   each workgroup stores its router logit as a 64-bit word tagged
+//            with the layer's epoch; every workgroup polls the words directly
+//            and runs softmax/top-k itself;
+//   h        SwiGLU outputs (K+1) x 512, triple-buffered by layer, and
+//   hidden   the layer's output rows, double-buffered by layer parity: a slot
+//            holds a signalling-NaN sentinel until its owner stores the value,
+//            and readers poll until no sentinel is left.  Arithmetic never
+//            produces a signalling NaN, so a stored value never looks unwritten.
+//            At the start of layer l the owner re-arms its slots of the hidden
+//            buffer layer l writes (last read during layer l-1) and of the h
+//            buffer layer l+1 writes (last read during layer l-2): having seen
+//            every workgroup's h of layer l-1, it knows all of them are past
+//            those reads.  The same wave's next loads wait for the re-arm stores
+//            (s_waitcnt counts both in order), and everything it publishes
+//            later comes after, so no reader can see a stale value.
+// The host passes the number of layers run so far on this context (the
+// epoch); tags and parities derive from it.  Data that crosses workgroups is
+// written and read with device-coherent (sc1) accesses, so no cache writeback
+// or invalidate is needed.  Every wait is bounded and flags a sticky error
+// instead of hanging.
 //
 // Replaces the reference's 45 launches per layer and its host routing round
 // trip (one_layer.cu:1812-1983, route_layer :937-992), and the per-layer host
@@ -35,27 +65,54 @@
 
 namespace {
 
+constexpr int G = 256;                   // workgroups, one per CU
+constexpr int NT = 1024;                 // threads per workgroup
+constexpr int NWV = NT / WAVE;           // 16 waves
 constexpr int DH = 2048;
 constexpr int DI = 512;
 constexpr int NBH = DH / QK;             // Q4_K superblocks per gate/up row
-constexpr int NBI = DI / QK;             // Q6_K superblocks per down row
 constexpr int GU_ROW = NBH * Q4K_BYTES;  // 1152 B
-constexpr int DN_ROW = NBI * Q6K_BYTES;  // 420 B
-constexpr int UPW = 2;                   // gate/up (slot, row) units per wave
-constexpr int UPB = 4 * UPW;             // units per gate/up workgroup
-constexpr int DR = 4;                    // output rows per down workgroup
-constexpr int SPW = 3;                   // slots per down wave: K + 1 <= 4 * SPW
-constexpr int MAXK = 4 * SPW - 1;
-constexpr int NLINES = 8;
+constexpr int DN_ROW = (DI / QK) * Q6K_BYTES;  // 420 B
+constexpr int GR = DI / G;               // gate/up rows per workgroup and slot
+constexpr int OR = DH / G;               // output rows per workgroup
+constexpr int BAND = OR * DN_ROW;        // one slot's down rows of a workgroup: 3360 B
+constexpr int BAND16 = BAND / 16;        // 210 16-byte chunks
+constexpr int MAXK = 8;
+constexpr int NSLOT = MAXK + 1;
+constexpr int NPOLL = 4;                 // waves 0..3 poll the hidden and logit exchanges
+constexpr int W_GU = 1;                  // waves 1..8: router partials, routed gate/up
+constexpr int W_SH = 9;                  // waves 9, 10: shared gate/up
+constexpr int W_DN = 9;                  // waves 9..15: routed down bands
+constexpr int N_DN = NWV - W_DN;         // 7
+constexpr int DN_LOADS = (MAXK * BAND16 + N_DN * WAVE - 1) / (N_DN * WAVE);  // 4
+constexpr int W_PF = 4;                  // waves 4..15 prefetch the next layer's fixed weights
 constexpr uint32_t SPIN_LIMIT = 1u << 18;
 constexpr uint32_t BUF_WORD3 = 0x00020000u;  // raw buffer descriptor word 3 (gfx9)
 constexpr int AUX_COHERENT = 16;             // sc1: device-coherent access
+constexpr uint32_t SENTINEL = 0x7FA5A5A5u;   // signalling NaN: "not written yet"
 
-static_assert(NBH == 8 && NBI == 2, "lane layouts assume H = 2048 and I = 512");
-static_assert(DI % UPB == 0, "a gate/up workgroup must stay inside one slot");
+static_assert(DH % G == 0 && DI % G == 0 && GR == 2 && OR == 8, "row ownership assumes 256 workgroups");
+static_assert(NBH == 8 && DI / QK == 2, "lane layouts assume H = 2048 and I = 512");
+static_assert(BAND % 16 == 0, "down bands are loaded in 16-byte chunks");
+static_assert(NPOLL * WAVE * 8 == DH && NPOLL * WAVE == 256, "pollers: 8 columns, one logit a lane");
+static_assert(W_GU + MAXK == W_SH && W_SH + 2 <= NWV, "wave roles");
 
 // Trace points recorded per (workgroup, layer) when a trace buffer is given.
-enum { TP_START = 0, TP_READY = 1, TP_ROUTED = 2, TP_LOADS = 3, TP_HREADY = 4, TP_DONE = 5, TP_N = 8 };
+enum {
+    TP_START = 0,   // layer entered
+    TP_XREADY = 1,  // previous layer's output seen, x in LDS
+    TP_LOGIT = 2,   // own logit published
+    TP_POLLED = 3,  // every logit seen
+    TP_RANK1 = 4,   // rank-1 expert known
+    TP_ROUTED = 5,  // every rank known, weights in LDS
+    TP_DDOT = 6,    // wave 0's down dots done
+    TP_COMB = 7,    // down dots of every wave done (after the barrier)
+    TP_HREADY = 8,  // every h seen
+    TP_OUT = 9,     // output rows stored
+    TP_CYC0 = 10,   // core clock (s_memtime) at TP_POLLED
+    TP_CYC1 = 11,   // core clock at TP_ROUTED
+    TP_N = 12
+};
 
 struct DecLayer {
     const uint8_t *gate_exps, *up_exps, *down_exps;
@@ -70,20 +127,47 @@ struct DecArgs {
     const DecLayer *layers;  // device table, or NULL: use `one`
     DecLayer one;
     int L;
+    uint32_t epoch0;         // layers run on this context before this launch
+    int hphase0;             // epoch0 % 3 (kept separately: 2^32 is not a multiple of 3)
     const float *x0;         // non-NULL: layer 0 input given (already normalised)
-    float *hidden;
+    float *hidden;           // [H] caller's hidden: input of layer 0, output of every layer
     float eps;
-    float *logits;           // [E + 1]: logits, then the shared-gate logit
-    float *xnorm;            // [H]
-    float *hbuf;             // [(K + 1) * I]
+    uint64_t *tlogits;       // [256] epoch-tagged logits
+    float *xbuf;             // [2][H] layer outputs by parity (sentinel protocol)
+    float *hbuf;             // [3][NSLOT * I] SwiGLU outputs by layer mod 3 (sentinel protocol)
     int32_t *idx_out;        // [L][K] or NULL
     float *w_out;            // [L][K] or NULL
     float *gsh_out;          // [L] or NULL
     bread_decode_sync *sync;
-    uint64_t *trace;         // [grid][L][TP_N] or NULL
+    uint64_t *trace;         // [G][L][TP_N] or NULL
     int E, K;
-    int nR, nS, nG, nD;
 };
+
+struct Smem {
+    float x[DH];                       // normalised input of the layer
+    float nw[DH];                      // RMSNorm weights (prefetched)
+    float h[NSLOT * DI];               // SwiGLU outputs of every slot
+    uint32_t down[NSLOT * BAND / 4];   // down bands: slot 0 prefetched, 1..K after routing
+    float wrow[DH];                    // router row g (prefetched)
+    uint16_t shg[DH];                  // shared-expert gate vector (prefetched)
+    uint4 shw[2][4][WAVE];             // shared gate/up rows: [row][hg, qg, hu, qu][lane] (prefetched)
+    uint4 gu[MAXK][4 * GR][WAVE];      // routed gate/up rows: [slot-1][4 row + (hg, qg, hu, qu)][lane]
+    float lg[256];                     // router logits of the layer
+    float red[NPOLL];                  // sum-of-squares partials
+    float rl[MAXK], gl[MAXK];          // router / shared-gate partials
+    float dot[NSLOT][OR];              // down dots
+    float hown[OR];                    // this workgroup's rows of h before the layer
+    int idx[MAXK];                     // routed experts, rank order
+    uint32_t key[MAXK];                // their probability keys
+    float w[MAXK];                     // their weights
+    float sgsh;                        // sigmoid of the shared-gate logit
+    int nready;                        // ranks published in idx
+    int lgcnt;                         // polling waves done with the logits
+    int dncnt;                         // down waves whose bands are in LDS
+    int abort;                         // a wait failed: the workgroup leaves
+};
+// more than half of a CU's 160 KB, so the dispatcher puts one workgroup per CU
+static_assert(sizeof(Smem) > 80 * 1024 && sizeof(Smem) <= 160 * 1024, "LDS footprint");
 
 // ---------------------------------------------------------------- memory helpers
 
@@ -92,51 +176,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, (int)BUF_WORD3);
 }
 
-// 16-byte buffer load at voff (per lane) + soff (wave-uniform constant)
-template <int AUX>
-__device__ __forceinline__ float4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff = 0)
+// An empty asm hides v's value from the optimiser, so per-lane address math
+// that depends on it is recomputed where it is used instead of being hoisted
+// out of the layer loop and kept live (spilled) across the whole kernel.
+__device__ __forceinline__ int opaque(int v)
 {
-    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, AUX));
+    asm volatile("" : "+v"(v));
+    return v;
 }
 
-template <int AUX>
-__device__ __forceinline__ uint4 bload4u(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff = 0)
+// Direct-to-LDS load (gfx950 global_load_lds_dwordx4): lane i of the wave
+// writes its 16 bytes at lds_wave_base + 16 i; the wave base must be uniform.
+// The data is in LDS once the issuing wave's vmcnt drains.
+__device__ __forceinline__ void lds_load16(const void *src, void *lds_wave_base)
 {
-    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, AUX));
-}
-
-__device__ __forceinline__ uint32_t bload1u(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff = 0)
-{
-    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
-}
-
-template <int AUX>
-__device__ __forceinline__ void bstore4(float4 v, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff = 0)
-{
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v),
-                                           r, (int)voff, (int)soff, AUX);
-}
-
-// 8 bytes at a 2-byte aligned buffer offset, from aligned dword loads (the
-// buffer-load form of ld8_a2: every dword read holds a wanted byte).
-__device__ __forceinline__ uint2 bld8_a2(__amdgpu_buffer_rsrc_t r, uint32_t off)
-{
-    const uint32_t a = off & ~3u, sh = off & 3u;
-    const uint32_t w0 = bload1u(r, a), w1 = bload1u(r, a + 4), w2 = bload1u(r, (off + 7) & ~3u);
-    uint2 o;
-    o.x = __builtin_amdgcn_alignbyte(w1, w0, sh);
-    o.y = __builtin_amdgcn_alignbyte(w2, w1, sh);
-    return o;
-}
-
-__device__ __forceinline__ uint32_t bld16_a2(__amdgpu_buffer_rsrc_t r, uint32_t off)
-{
-    return (bload1u(r, off & ~3u) >> (8u * (off & 3u))) & 0xFFFFu;
-}
-
-__device__ __forceinline__ float cload(const float *p)
-{
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_global_load_lds(src, lds_wave_base, 16, 0, 0);
 }
 
 __device__ __forceinline__ void cstore(float *p, float v)
@@ -144,10 +198,58 @@ __device__ __forceinline__ void cstore(float *p, float v)
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+__device__ __forceinline__ void cstore2(float *p, float a, float b)
+{
+    __hip_atomic_store(reinterpret_cast<uint64_t *>(p),
+                       ((uint64_t)__builtin_bit_cast(uint32_t, b) << 32) | __builtin_bit_cast(uint32_t, a),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// LDS flags shared by the waves of the workgroup.  LDS performs one wave's
+// accesses in order, so data written before a flag is seen by a wave that
+// has seen the flag; the signal fences keep the compiler from reordering.
+__device__ __forceinline__ int lds_get(const int *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ void lds_put(int *p, int v)
+{
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ void lds_add(int *p, int v)
+{
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Wave-level bounded wait for an LDS flag; false if the workgroup aborts.
+// slow: sleep longer between looks (for waits expected to last microseconds).
+__device__ __forceinline__ bool lds_wait(const Smem &S, const int *p, int target, bool slow = false)
+{
+    for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
+        if (lds_get(p) >= target) {
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            return true;
+        }
+        if (lds_get(&S.abort)) return false;
+        if (slow) __builtin_amdgcn_s_sleep(8);
+        else __builtin_amdgcn_s_sleep(1);
+    }
+    return false;
+}
+
+// Called by one lane.
+__device__ __forceinline__ void trace_here(const DecArgs &a, int l, int tp)
+{
+    if (a.trace) a.trace[((size_t)blockIdx.x * a.L + l) * TP_N + tp] = wall_clock64();
+}
+
 __device__ __forceinline__ void trace_point(const DecArgs &a, int l, int tp)
 {
-    if (a.trace && threadIdx.x == 0)
-        a.trace[((size_t)blockIdx.x * a.L + l) * TP_N + tp] = wall_clock64();
+    if (threadIdx.x == 0) trace_here(a, l, tp);
 }
 
 // The layer record is the same for the whole grid: keep it in scalar registers.
@@ -181,145 +283,92 @@ __device__ __forceinline__ void flag_error(bread_decode_sync *s, uint32_t code)
     __hip_atomic_fetch_or(&s->error.v, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Wave-wide bounded wait until the sum of a counter's 8 lines reaches target.
-__device__ __forceinline__ bool wait_lines(bread_decode_sync *s, const bread_line *lines, uint32_t target)
+__device__ __forceinline__ bool unwritten(float v)
 {
-    const int lane = lane_id();
+    return __builtin_bit_cast(uint32_t, v) == SENTINEL;
+}
+
+// Per-thread bounded poll of 4 coherent floats at byte offset off of a
+// buffer until none is the sentinel.  Returns false on time-out (flagging the
+// error) or when another workgroup flagged one.
+__device__ __forceinline__ bool poll4(bread_decode_sync *s, __amdgpu_buffer_rsrc_t r, uint32_t off, float4 &v)
+{
     for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
-        const uint32_t v =
-            lane < NLINES ? __hip_atomic_load(&lines[lane].v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
-        uint32_t tot = 0;
-#pragma unroll
-        for (int k = 0; k < NLINES; k++) tot += __builtin_amdgcn_readlane(v, k);
-        if (tot >= target) return true;
+        v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX_COHERENT));
+        if (!unwritten(v.x) && !unwritten(v.y) && !unwritten(v.z) && !unwritten(v.w)) return true;
         if ((it & 63) == 63 && has_error(s)) return false;
-        __builtin_amdgcn_s_sleep(2);
+        __builtin_amdgcn_s_sleep(1);
     }
-    if (lane == 0) flag_error(s, 1u);
+    flag_error(s, 1u);
     return false;
 }
 
-// Workgroup-wide wait: wave 0 polls (one poller per workgroup keeps the
-// counter lines' traffic low), the others wait at the barrier.
-__device__ __forceinline__ void wait_lines_wg(bread_decode_sync *s, const bread_line *lines, uint32_t target)
+// Per-thread bounded poll of router logit i of this epoch (tagged word).
+__device__ __forceinline__ bool poll_logit(bread_decode_sync *s, const uint64_t *p, uint32_t tag, float &v)
 {
-    if (wave_id() == 0) wait_lines(s, lines, target);
-    __syncthreads();
-}
-
-// Workgroup-wide: every memory access of every wave has completed (s_waitcnt
-// 0 before the barrier), then one counter line is bumped.  Every write that
-// another workgroup reads is a device-coherent (sc1) store, complete once it
-// is acknowledged, so no cache writeback is needed: an agent-scope release or
-// acquire fence here (an L2 writeback / invalidate) costs ~5-30 ns per
-// workgroup, serialised, on MI355X.
-__device__ __forceinline__ void signal_line(bread_line *lines)
-{
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0)
-        __hip_atomic_fetch_add(&lines[blockIdx.x % NLINES].v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Softmax/top-k over the published logits (coherent loads) by one wave;
-// lane k < K gets (idx_k, w_k); also returns the raw shared-gate logit.
-__device__ __forceinline__ void route_from_logits(const DecArgs &a, int &ik, float &wk, float &gsh)
-{
-    const int lane = lane_id();
-    float p[4];
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-        const int i = lane + WAVE * v;
-        p[v] = i < a.E ? cload(a.logits + i) : -__builtin_inff();
+    for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
+        const uint64_t w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((uint32_t)(w >> 32) == tag) {
+            v = __builtin_bit_cast(float, (uint32_t)w);
+            return true;
+        }
+        if ((it & 63) == 63 && has_error(s)) return false;
+        __builtin_amdgcn_s_sleep(1);
     }
-    gsh = cload(a.logits + a.E);
-    topk_wave_vals<4>(p, a.E, a.K, ik, wk);
+    flag_error(s, 2u);
+    return false;
 }
 
-// ---------------------------------------------------------------- router role
+// ---------------------------------------------------------------- routing
 
-// A router wave holds columns 4*lane + 256*m (m < 8) of its row and of x.
-__device__ void router_role(const DecArgs &a)
+// Selection over E <= 256 probabilities, lane i holding entries i + 64 v.
+// A probability key (bits + 2, or 1 for NaN, 0 for none; below 2^30) is
+// packed with its register number as (key << 2) | (3 - v): within a lane the
+// packed keys are distinct, and across the wave the unsigned maximum is the
+// largest probability with, among equal ones, the lowest v; the lowest lane
+// holding that maximum then has the lowest index i = lane + 64 v.  That is
+// cpu_topk's strict '>' scan from i = 0 (layer_ops.cu:231-243).  Each lane
+// keeps its four packed keys sorted, so a pass is one wave max, one ballot
+// and a shift in the winning lane.
+struct Sel {
+    uint32_t k0, k1, k2, k3;  // packed keys, descending
+};
+
+__device__ __forceinline__ void cswap(uint32_t &a, uint32_t &b)
 {
-    const int wid = wave_id(), lane = lane_id();
-    const int v = (int)blockIdx.x * 4 + wid;
-    const bool row = v < a.E, gate = v == a.E;
-    const uint32_t vo = 16u * (uint32_t)lane;
-    for (int l = 0; l < a.L; l++) {
-        const DecLayer Ly = load_layer(a, l);
-        trace_point(a, l, TP_START);
-        float4 wr[8];
-        if (row) {
-            const auto r = rsrc(Ly.router + (size_t)v * DH, DH * 4);
-#pragma unroll
-            for (int m = 0; m < 8; m++) wr[m] = bload4<0>(r, vo, 1024u * m);
-        } else if (gate && Ly.shg) {
-            const auto r = rsrc(Ly.shg, DH * 2);
-#pragma unroll
-            for (int m = 0; m < 8; m++) {
-                const uint2 g = __builtin_bit_cast(
-                    uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)(8 * lane), (int)(512 * m), 0));
-                wr[m] = make_float4(h2f(g.x), h2f(g.x >> 16), h2f(g.y), h2f(g.y >> 16));
-            }
-        } else {
-#pragma unroll
-            for (int m = 0; m < 8; m++) wr[m] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-        if (l > 0) wait_lines_wg(a.sync, a.sync->out_done, (uint32_t)(l * a.nD));
-        trace_point(a, l, TP_READY);
-        float4 xv[8];
-        if (l == 0 && a.x0) {
-            const auto xr = rsrc(a.x0, DH * 4);
-#pragma unroll
-            for (int m = 0; m < 8; m++) xv[m] = bload4<0>(xr, vo, 1024u * m);
-        } else {
-            const auto hr = rsrc(a.hidden, DH * 4);
-            float ss = 0.f;
-#pragma unroll
-            for (int m = 0; m < 8; m++) {
-                xv[m] = bload4<AUX_COHERENT>(hr, vo, 1024u * m);
-                ss = fmaf(xv[m].x, xv[m].x, ss);
-                ss = fmaf(xv[m].y, xv[m].y, ss);
-                ss = fmaf(xv[m].z, xv[m].z, ss);
-                ss = fmaf(xv[m].w, xv[m].w, ss);
-            }
-            ss = wave_sum(ss);
-            const float inv = 1.0f / sqrtf(ss / (float)DH + a.eps);  // layer_ops.cu:209
-            if (Ly.norm_w) {
-                const auto nr = rsrc(Ly.norm_w, DH * 4);
-#pragma unroll
-                for (int m = 0; m < 8; m++) {
-                    const float4 nw = bload4<0>(nr, vo, 1024u * m);
-                    xv[m] = make_float4(xv[m].x * inv * nw.x, xv[m].y * inv * nw.y, xv[m].z * inv * nw.z,
-                                        xv[m].w * inv * nw.w);
-                }
-            } else {
-#pragma unroll
-                for (int m = 0; m < 8; m++)
-                    xv[m] = make_float4(xv[m].x * inv, xv[m].y * inv, xv[m].z * inv, xv[m].w * inv);
-            }
-        }
-        float acc = 0.f;
-#pragma unroll
-        for (int m = 0; m < 8; m++) {
-            acc = fmaf(wr[m].x, xv[m].x, acc);
-            acc = fmaf(wr[m].y, xv[m].y, acc);
-            acc = fmaf(wr[m].z, xv[m].z, acc);
-            acc = fmaf(wr[m].w, xv[m].w, acc);
-        }
-        acc = wave_sum(acc);
-        if ((row || gate) && lane == 0) cstore(a.logits + v, acc);  // v == E: the shared-gate logit
-        if (blockIdx.x == 0 && wid == 0) {
-            const auto xr = rsrc(a.xnorm, DH * 4);
-#pragma unroll
-            for (int m = 0; m < 8; m++) bstore4<AUX_COHERENT>(xv[m], xr, vo, 1024u * m);
-        }
-        trace_point(a, l, TP_DONE);
-        signal_line(a.sync->router_done);
-    }
+    const uint32_t hi = umax32(a, b), lo = a ^ b ^ hi;
+    a = hi;
+    b = lo;
 }
 
-// ---------------------------------------------------------------- gate/up roles
+__device__ __forceinline__ Sel sel_init(const uint32_t (&key)[4])
+{
+    Sel s{(key[0] << 2) | 3u, (key[1] << 2) | 2u, (key[2] << 2) | 1u, key[3] << 2};
+    cswap(s.k0, s.k1);
+    cswap(s.k2, s.k3);
+    cswap(s.k0, s.k2);
+    cswap(s.k1, s.k3);
+    cswap(s.k1, s.k2);
+    return s;
+}
+
+// One pass: returns the winning index; M gets its probability key.
+__device__ __forceinline__ int sel_pass(Sel &s, int lane, uint32_t &M)
+{
+    const uint32_t top = wave_max_u32(s.k0);
+    const uint64_t b = __builtin_amdgcn_ballot_w64(s.k0 == top);
+    const int wl = (int)__builtin_ctzll(b);
+    if (lane == wl) {
+        s.k0 = s.k1;
+        s.k1 = s.k2;
+        s.k2 = s.k3;
+        s.k3 = 0u;
+    }
+    M = top >> 2;
+    return wl + WAVE * (int)(3u - (top & 3u));
+}
+
+// ---------------------------------------------------------------- gate/up
 
 // A gate/up lane owns qs chunk c = lane%8 of superblock sbl = lane/8 of a row:
 // x columns base + [0,16) (low nibbles) and base + 32 + [0,16) (high nibbles),
@@ -330,68 +379,41 @@ __device__ __forceinline__ int gu_base(int lane)
     return (lane >> 3) * QK + 64 * (c >> 1) + 16 * (c & 1);
 }
 
-__device__ __forceinline__ void load_x32(__amdgpu_buffer_rsrc_t r, int base, float (&xl)[16], float (&xh)[16])
+// Direct-to-LDS loads of gate/up rows r0 .. r0+N of one expert: w[4i + q]
+// receives, for row r0+i, q = 0: the gate superblock head of the lane,
+// 1: its gate qs chunk, 2/3: the same for up.
+template <int N>
+__device__ __forceinline__ void gu_issue(const uint8_t *gbase, const uint8_t *ubase, int r0, uint4 (*w)[WAVE])
 {
+    const int lane = opaque(lane_id());
+    const uint32_t oh = (uint32_t)((lane >> 3) * Q4K_BYTES);
+    const uint32_t oq = oh + 16u + 16u * (uint32_t)(lane & 7);
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const uint8_t *gr = gbase + (size_t)(r0 + i) * GU_ROW, *ur = ubase + (size_t)(r0 + i) * GU_ROW;
+        lds_load16(gr + oh, &w[4 * i + 0][0]);
+        lds_load16(gr + oq, &w[4 * i + 1][0]);
+        lds_load16(ur + oh, &w[4 * i + 2][0]);
+        lds_load16(ur + oq, &w[4 * i + 3][0]);
+    }
+}
+
+// Gate/up + SwiGLU of the N rows staged by gu_issue (the wave's own loads
+// must have landed); every lane gets the results.
+template <int N>
+__device__ __forceinline__ void gu_compute(const Smem &S, const uint4 (*w)[WAVE], float (&out)[N])
+{
+    const int lane = opaque(lane_id());
+    const int base = gu_base(lane);
+    const uint32_t j = (uint32_t)(lane & 7) >> 1;
+    float xl[16], xh[16];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-        const float4 lo = bload4<AUX_COHERENT>(r, (uint32_t)(4 * base), (uint32_t)(16 * q));
-        const float4 hi = bload4<AUX_COHERENT>(r, (uint32_t)(4 * base), (uint32_t)(128 + 16 * q));
+        const float4 lo = *reinterpret_cast<const float4 *>(&S.x[base + 4 * q]);
+        const float4 hi = *reinterpret_cast<const float4 *>(&S.x[base + 32 + 4 * q]);
         xl[4 * q] = lo.x; xl[4 * q + 1] = lo.y; xl[4 * q + 2] = lo.z; xl[4 * q + 3] = lo.w;
         xh[4 * q] = hi.x; xh[4 * q + 1] = hi.y; xh[4 * q + 2] = hi.z; xh[4 * q + 3] = hi.w;
     }
-}
-
-// x = RMSNorm(h) * w (or the given x of a single pre-normalised layer).
-__device__ __forceinline__ void gu_x_from_hidden(const DecArgs &a, const DecLayer &Ly, int l, int base,
-                                                 float (&xl)[16], float (&xh)[16])
-{
-    if (l == 0 && a.x0) {
-        load_x16(a.x0, base, xl);
-        load_x16(a.x0, base + 32, xh);
-        return;
-    }
-    load_x32(rsrc(a.hidden, DH * 4), base, xl, xh);
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        ss = fmaf(xl[i], xl[i], ss);
-        ss = fmaf(xh[i], xh[i], ss);
-    }
-    ss = wave_sum(ss);
-    const float inv = 1.0f / sqrtf(ss / (float)DH + a.eps);
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const float wl = Ly.norm_w ? Ly.norm_w[base + i] : 1.f;
-        const float wh = Ly.norm_w ? Ly.norm_w[base + 32 + i] : 1.f;
-        xl[i] = xl[i] * inv * wl;
-        xh[i] = xh[i] * inv * wh;
-    }
-}
-
-__device__ __forceinline__ void gu_issue(const uint8_t *gbase, const uint8_t *ubase, int r0, uint4 (&hg)[UPW],
-                                         uint4 (&qg)[UPW], uint4 (&hu)[UPW], uint4 (&qu)[UPW])
-{
-    const int lane = lane_id();
-    const uint32_t oh = (uint32_t)((lane >> 3) * Q4K_BYTES);
-    const uint32_t oq = oh + 16u + 16u * (uint32_t)(lane & 7);
-    const auto gr = rsrc(gbase + (size_t)r0 * GU_ROW, UPW * GU_ROW);
-    const auto ur = rsrc(ubase + (size_t)r0 * GU_ROW, UPW * GU_ROW);
-#pragma unroll
-    for (int i = 0; i < UPW; i++) {
-        hg[i] = bload4u<0>(gr, oh, (uint32_t)(i * GU_ROW));
-        qg[i] = bload4u<0>(gr, oq, (uint32_t)(i * GU_ROW));
-        hu[i] = bload4u<0>(ur, oh, (uint32_t)(i * GU_ROW));
-        qu[i] = bload4u<0>(ur, oq, (uint32_t)(i * GU_ROW));
-    }
-}
-
-// Gate/up + SwiGLU for UPW consecutive rows of one slot by one wave.
-__device__ __forceinline__ void gu_compute(const DecArgs &a, int slot, int r0, const float (&xl)[16],
-                                           const float (&xh)[16], const uint4 (&hg)[UPW], const uint4 (&qg)[UPW],
-                                           const uint4 (&hu)[UPW], const uint4 (&qu)[UPW])
-{
-    const int lane = lane_id();
-    const uint32_t j = (uint32_t)(lane & 7) >> 1;
     float sxl = 0.f, sxh = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
@@ -399,192 +421,436 @@ __device__ __forceinline__ void gu_compute(const DecArgs &a, int slot, int r0, c
         sxh += xh[i];
     }
 #pragma unroll
-    for (int i = 0; i < UPW; i++) {
-        const float g = wave_sum(q4k_chunk_dot_sx(hg[i], qg[i], j, xl, xh, sxl, sxh));
-        const float u = wave_sum(q4k_chunk_dot_sx(hu[i], qu[i], j, xl, xh, sxl, sxh));
-        if (lane == 0) cstore(a.hbuf + slot * DI + r0 + i, silu_mul(g, u));
+    for (int i = 0; i < N; i++) {
+        const float gt = wave_sum(q4k_chunk_dot_sx(w[4 * i][lane], w[4 * i + 1][lane], j, xl, xh, sxl, sxh));
+        const float up = wave_sum(q4k_chunk_dot_sx(w[4 * i + 2][lane], w[4 * i + 3][lane], j, xl, xh, sxl, sxh));
+        out[i] = silu_mul(gt, up);
     }
 }
 
-__device__ void shared_role(const DecArgs &a)
+// ---------------------------------------------------------------- down
+
+// 8 bytes at a 2-byte aligned LDS byte offset, from aligned dwords.
+__device__ __forceinline__ uint2 lds8_a2(const uint32_t *base, uint32_t off)
 {
-    const int wid = wave_id(), lane = lane_id();
-    const int r0 = (((int)blockIdx.x - a.nR) * 4 + wid) * UPW;  // rows of the shared expert
-    const int base = gu_base(lane);
-    for (int l = 0; l < a.L; l++) {
-        const DecLayer Ly = load_layer(a, l);
-        trace_point(a, l, TP_START);
-        uint4 hg[UPW], qg[UPW], hu[UPW], qu[UPW];
-        gu_issue(Ly.gate_sh, Ly.up_sh, r0, hg, qg, hu, qu);
-        if (l > 0) wait_lines_wg(a.sync, a.sync->out_done, (uint32_t)(l * a.nD));
-        trace_point(a, l, TP_READY);
-        float xl[16], xh[16];
-        gu_x_from_hidden(a, Ly, l, base, xl, xh);
-        gu_compute(a, 0, r0, xl, xh, hg, qg, hu, qu);
-        trace_point(a, l, TP_DONE);
-        signal_line(a.sync->h_done);
-    }
+    const uint32_t a = off >> 2, sh = off & 3u;
+    const uint32_t w0 = base[a], w1 = base[a + 1], w2 = base[(off + 7) >> 2];
+    uint2 o;
+    o.x = __builtin_amdgcn_alignbyte(w1, w0, sh);
+    o.y = __builtin_amdgcn_alignbyte(w2, w1, sh);
+    return o;
 }
 
-__device__ void routed_role(const DecArgs &a)
+__device__ __forceinline__ uint32_t lds16_a2(const uint32_t *base, uint32_t off)
 {
-    __shared__ int s_e;
-    const int wid = wave_id(), lane = lane_id();
-    const int u0 = DI + ((int)blockIdx.x - a.nR - a.nS) * UPB;  // first (slot, row) unit
-    const int slot = u0 / DI;                                   // 1..K: rank slot - 1
-    const int r0 = u0 % DI + wid * UPW;
-    const int base = gu_base(lane);
-    for (int l = 0; l < a.L; l++) {
-        const DecLayer Ly = load_layer(a, l);
-        trace_point(a, l, TP_START);
-        wait_lines_wg(a.sync, a.sync->router_done, (uint32_t)((l + 1) * a.nR));
-        trace_point(a, l, TP_READY);
-        float xl[16], xh[16];
-        load_x32(rsrc(a.xnorm, DH * 4), base, xl, xh);
-        if (wid == 0) {
-            int ik;
-            float wk, g;
-            route_from_logits(a, ik, wk, g);
-            const int e = __shfl(ik, slot - 1);
-            if (lane == 0) s_e = (e >= 0 && e < a.E) ? e : 0;
-        }
-        __syncthreads();
-        const int e = uniform(s_e);
-        trace_point(a, l, TP_ROUTED);
-        uint4 hg[UPW], qg[UPW], hu[UPW], qu[UPW];
-        gu_issue(Ly.gate_exps + (uint64_t)e * Ly.gate_eb, Ly.up_exps + (uint64_t)e * Ly.up_eb, r0, hg, qg, hu, qu);
-        gu_compute(a, slot, r0, xl, xh, hg, qg, hu, qu);
-        trace_point(a, l, TP_DONE);
-        signal_line(a.sync->h_done);
-    }
+    return (base[off >> 2] >> (8u * (off & 3u))) & 0xFFFFu;
 }
 
-// ---------------------------------------------------------------- down role
-
-// A down lane owns row r0 + lane/16, superblock b = (lane/8)%2 of it and the
-// Q6_K unit (half n, l in [8t, 8t+8)) of that superblock; wave w handles
-// slots w, w+4, w+8 for the workgroup's DR rows.
-__device__ void down_role(const DecArgs &a)
+// Down unit u: slot u/2, rows 4*(u%2) .. +4 of the workgroup, 16 lanes a row;
+// a lane owns superblock b = (lane/8)%2, half n = (lane/4)%2 and l in
+// [8t, 8t+8), t = lane%4 (the Q6_K unit of quant_dot.h), i.e. the 32 weights
+// at columns b*256 + 128n + 32s + 8t + k, s < 4, k < 8.
+//
+// Pre-decode: w[8s + k] = (d * sc) * (q - 32), the dequantised weight
+// (dequant_q4k_cpu.c:155-170, same rounding order).
+__device__ __forceinline__ void down_predecode(const Smem &S, int u, float (&w)[32])
 {
-    __shared__ int s_idx[MAXK];
-    __shared__ float s_w[MAXK];
-    __shared__ float s_gsh;
-    __shared__ float s_dot[MAXK + 1][DR];
-    const int wid = wave_id(), lane = lane_id();
-    const int dwg = (int)blockIdx.x - a.nR - a.nS - a.nG;
-    const int r0 = dwg * DR;
-    const int q = lane >> 4;
-    const int b = (lane >> 3) & 1;
-    const int n = (lane >> 2) & 1, t = lane & 3;
+    const int lane = opaque(lane_id());
+    const int slot = u >> 1;
+    const int row = 4 * (u & 1) + (lane >> 4);
+    const int b = (lane >> 3) & 1, n = (lane >> 2) & 1, t = lane & 3;
+    const uint32_t ob = (uint32_t)(slot * BAND + row * DN_ROW + b * Q6K_BYTES);
+    const uint2 ql0 = lds8_a2(S.down, ob + 64 * n + 8 * t);
+    const uint2 ql1 = lds8_a2(S.down, ob + 64 * n + 32 + 8 * t);
+    const uint2 qh = lds8_a2(S.down, ob + 128 + 32 * n + 8 * t);
+    const uint2 scw = lds8_a2(S.down, ob + 192 + 8 * n);
+    const float d = h2f(lds16_a2(S.down, ob + 208));
     const uint32_t i2 = (uint32_t)t >> 1;
-    // byte offsets of this lane's fields inside the workgroup's DR rows
-    const uint32_t ob = (uint32_t)(q * DN_ROW + b * Q6K_BYTES);
-    const uint32_t o_ql0 = ob + 64 * n + 8 * t, o_ql1 = o_ql0 + 32;
-    const uint32_t o_qh = ob + 128 + 32 * n + 8 * t, o_sc = ob + 192 + 8 * n, o_d = ob + 208;
-    const uint32_t o_h = (uint32_t)(4 * (b * QK + 128 * n + 8 * t));
-    for (int l = 0; l < a.L; l++) {
-        const DecLayer Ly = load_layer(a, l);
-        trace_point(a, l, TP_START);
-        wait_lines_wg(a.sync, a.sync->router_done, (uint32_t)((l + 1) * a.nR));
-        trace_point(a, l, TP_READY);
-        if (wid == 0) {
-            int ik;
-            float wk, g;
-            route_from_logits(a, ik, wk, g);
-            if (lane < a.K) {
-                s_idx[lane] = (ik >= 0 && ik < a.E) ? ik : 0;
-                s_w[lane] = wk;
-            }
-            if (lane == 0) s_gsh = g;
-            if (dwg == 0 && lane < a.K) {
-                if (a.idx_out) a.idx_out[l * a.K + lane] = ik;
-                if (a.w_out) a.w_out[l * a.K + lane] = wk;
-                if (a.gsh_out && lane == 0) a.gsh_out[l] = g;
-            }
-        }
-        __syncthreads();
-        trace_point(a, l, TP_ROUTED);
-        uint2 ql0[SPW], ql1[SPW], qh[SPW], scw[SPW];
-        uint32_t d16[SPW];
 #pragma unroll
-        for (int si = 0; si < SPW; si++) {
-            const int slot = wid + 4 * si;
-            if (slot <= a.K) {
-                const uint8_t *base =
-                    slot == 0 ? Ly.down_sh : Ly.down_exps + (uint64_t)uniform(s_idx[slot - 1]) * Ly.down_eb;
-                const auto r = rsrc(base + (size_t)r0 * DN_ROW, DR * DN_ROW);
-                ql0[si] = bld8_a2(r, o_ql0);
-                ql1[si] = bld8_a2(r, o_ql1);
-                qh[si] = bld8_a2(r, o_qh);
-                scw[si] = bld8_a2(r, o_sc);
-                d16[si] = bld16_a2(r, o_d);
-            }
-        }
-        trace_point(a, l, TP_LOADS);
-        wait_lines_wg(a.sync, a.sync->h_done, (uint32_t)((l + 1) * (a.nS + a.nG)));
-        trace_point(a, l, TP_HREADY);
-        const auto hr = rsrc(a.hbuf, (uint32_t)((a.K + 1) * DI * 4));
+    for (int half = 0; half < 2; half++) {
+        uint32_t q[4];
+        q6k_unpack(half ? ql0.y : ql0.x, half ? ql1.y : ql1.x, half ? qh.y : qh.x, q);
 #pragma unroll
-        for (int si = 0; si < SPW; si++) {
-            const int slot = wid + 4 * si;
-            if (slot <= a.K) {
-                float xs[4][8];
+        for (int s = 0; s < 4; s++) {
+            const float ds = d * q6k_scale(scw, i2 + 2 * s);
 #pragma unroll
-                for (int s = 0; s < 4; s++) {
-                    const float4 v0 = bload4<AUX_COHERENT>(hr, o_h, (uint32_t)(4 * slot * DI + 128 * s));
-                    const float4 v1 = bload4<AUX_COHERENT>(hr, o_h, (uint32_t)(4 * slot * DI + 128 * s + 16));
-                    xs[s][0] = v0.x; xs[s][1] = v0.y; xs[s][2] = v0.z; xs[s][3] = v0.w;
-                    xs[s][4] = v1.x; xs[s][5] = v1.y; xs[s][6] = v1.z; xs[s][7] = v1.w;
-                }
-                const float dv = sum16(q6k_unit_dot(ql0[si], ql1[si], qh[si], scw[si], i2, h2f(d16[si]), xs));
-                if ((lane & 15) == 0) s_dot[slot][q] = dv;
-            }
+            for (int k = 0; k < 4; k++) w[8 * s + 4 * half + k] = ds * (float)((int)byte_of(q[s], k) - 32);
         }
-        __syncthreads();
-        if (wid == 0 && lane < DR) {
-            const int r = r0 + lane;
-            float v = cload(a.hidden + r);
-            v += sigmoidf_ref(s_gsh) * s_dot[0][lane];                      // one_layer.cu:1447-1449
-            for (int k = 0; k < a.K; k++) v += s_w[k] * s_dot[k + 1][lane];  // :1469
-            cstore(a.hidden + r, v);
-        }
-        trace_point(a, l, TP_DONE);
-        signal_line(a.sync->out_done);
+    }
+}
+
+// Down units beyond the 16 waves (u >= 16, only for K = 8) are pre-decoded by
+// waves 1 and 2 into their own gate/up staging slot of LDS, free once their
+// gate/up is done: element 8s + k of lane i at float4 [2s + k/4][i].
+__device__ __forceinline__ void predecode_to_lds(const Smem &S, int u, float4 (*dst)[WAVE])
+{
+    float w[32];
+    down_predecode(S, u, w);
+    const int lane = opaque(lane_id());
+#pragma unroll
+    for (int q = 0; q < 8; q++) dst[q][lane] = make_float4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
+}
+
+__device__ __forceinline__ float down_acc(const Smem &S, int u, const float (&w)[32])
+{
+    const int lane = opaque(lane_id());
+    const int slot = u >> 1;
+    const int b = (lane >> 3) & 1, n = (lane >> 2) & 1, t = lane & 3;
+    const float *hs = S.h + slot * DI + b * QK + 128 * n + 8 * t;
+    float acc = 0.f;
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const float4 v0 = *reinterpret_cast<const float4 *>(hs + 32 * s);
+        const float4 v1 = *reinterpret_cast<const float4 *>(hs + 32 * s + 4);
+        acc = fmaf(w[8 * s + 0], v0.x, acc);
+        acc = fmaf(w[8 * s + 1], v0.y, acc);
+        acc = fmaf(w[8 * s + 2], v0.z, acc);
+        acc = fmaf(w[8 * s + 3], v0.w, acc);
+        acc = fmaf(w[8 * s + 4], v1.x, acc);
+        acc = fmaf(w[8 * s + 5], v1.y, acc);
+        acc = fmaf(w[8 * s + 6], v1.z, acc);
+        acc = fmaf(w[8 * s + 7], v1.w, acc);
+    }
+    return sum16(acc);
+}
+
+__device__ __forceinline__ void down_dot(Smem &S, int u, const float (&w)[32])
+{
+    const int lane = opaque(lane_id());
+    const float acc = down_acc(S, u, w);
+    if ((lane & 15) == 0) S.dot[u >> 1][4 * (u & 1) + (lane >> 4)] = acc;
+}
+
+__device__ __forceinline__ void down_dot_lds(Smem &S, int u, const float4 (*src)[WAVE])
+{
+    const int lane = opaque(lane_id());
+    float w[32];
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        const float4 v = src[q][lane];
+        w[4 * q] = v.x; w[4 * q + 1] = v.y; w[4 * q + 2] = v.z; w[4 * q + 3] = v.w;
+    }
+    const float acc = down_acc(S, u, w);
+    if ((lane & 15) == 0) S.dot[u >> 1][4 * (u & 1) + (lane >> 4)] = acc;
+}
+
+// ---------------------------------------------------------------- fixed weights
+
+// Routing-independent weights of a layer into LDS, by waves 4..15: router
+// row g and norm weights (waves 4..11), shared-gate vector, shared gate/up
+// rows and shared down band (waves 12..15).
+__device__ __forceinline__ void prefetch_fixed(Smem &S, const DecLayer &Ly, int g, int E, int wid)
+{
+    const int lane = opaque(lane_id());
+    if (wid < W_PF) return;
+    if (wid < W_PF + 8) {
+        const int c = WAVE * (wid - W_PF) + lane;  // 16-byte chunk of a 2048-float row
+        if (g < E) lds_load16(Ly.router + (size_t)g * DH + 4 * c, &S.wrow[4 * WAVE * (wid - W_PF)]);
+        if (Ly.norm_w) lds_load16(Ly.norm_w + 4 * c, &S.nw[4 * WAVE * (wid - W_PF)]);
+    } else {
+        const int w4 = wid - (W_PF + 8);  // 0..3
+        if (Ly.shg) lds_load16(Ly.shg + 8 * (WAVE * w4 + lane), &S.shg[8 * WAVE * w4]);
+        // shared gate/up: wave w4 loads row w4/2, gate (w4 even) or up
+        const int r = GR * g + (w4 >> 1);
+        const uint8_t *base = ((w4 & 1) ? Ly.up_sh : Ly.gate_sh) + (size_t)r * GU_ROW;
+        const uint32_t oh = (uint32_t)((lane >> 3) * Q4K_BYTES);
+        const uint32_t oq = oh + 16u + 16u * (uint32_t)(lane & 7);
+        lds_load16(base + oh, &S.shw[w4 >> 1][2 * (w4 & 1)][0]);
+        lds_load16(base + oq, &S.shw[w4 >> 1][2 * (w4 & 1) + 1][0]);
+        const int c = WAVE * w4 + lane;  // shared down band chunk
+        if (c < BAND16) lds_load16(Ly.down_sh + (size_t)g * BAND + 16 * c, &S.down[4 * WAVE * w4]);
     }
 }
 
 // ---------------------------------------------------------------- kernel
 
-__global__ __launch_bounds__(256, 4) void k_decode(DecArgs a)
+__global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
 {
-    const int bid = (int)blockIdx.x;
-    if (bid < a.nR)
-        router_role(a);
-    else if (bid < a.nR + a.nS)
-        shared_role(a);
-    else if (bid < a.nR + a.nS + a.nG)
-        routed_role(a);
-    else
-        down_role(a);
-    // exit: the last workgroup out (two levels of 8 lines) resets every counter
+    __shared__ Smem S;
+    const int g = (int)blockIdx.x;
+    const int tid = (int)threadIdx.x;
+    const int wid = wave_id(), lane = lane_id();
+    const int K = a.K, E = a.E;
+    const int NH = (K + 1) * DI;  // h values in use per parity
+    const int NU = 2 * (K + 1);   // down units
+    bread_decode_sync *sy = a.sync;
+    const float sent = __builtin_bit_cast(float, SENTINEL);
+    if (tid == 0) S.abort = 0;
+    prefetch_fixed(S, load_layer(a, 0), g, E, wid);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        bread_decode_sync *s = a.sync;
-        const int total = a.nR + a.nS + a.nG + a.nD;
-        const int grp = bid % NLINES;
-        const uint32_t members = (uint32_t)((total - grp + NLINES - 1) / NLINES);
-        const uint32_t o1 = __hip_atomic_fetch_add(&s->exit1[grp].v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (o1 == members - 1) {
-            const uint32_t o2 = __hip_atomic_fetch_add(&s->exit2.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (o2 == (uint32_t)NLINES - 1) {
-                for (int k = 0; k < NLINES; k++) {
-                    __hip_atomic_store(&s->router_done[k].v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(&s->h_done[k].v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(&s->out_done[k].v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(&s->exit1[k].v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    for (int l = 0; l < a.L; l++) {
+        // per-lane values recomputed each layer rather than kept live
+        const int tid = opaque((int)threadIdx.x);
+        const int lane = tid & (WAVE - 1);
+        const DecLayer Ly = load_layer(a, l);
+        const uint32_t tag = a.epoch0 + (uint32_t)l + 1u;
+        const int par = (int)((a.epoch0 + (uint32_t)l) & 1u);
+        float *xout = a.xbuf + par * DH;             // this layer's output rows
+        const int hp = (a.hphase0 + l) % 3;
+        float *hcur = a.hbuf + hp * (NSLOT * DI);                  // this layer's h
+        float *hnext = a.hbuf + (hp == 2 ? 0 : hp + 1) * (NSLOT * DI);  // next layer's
+        trace_point(a, l, TP_START);
+
+        // ---- P1: h of the layer (caller's buffer for the first layer, else
+        // the previous layer's output, polled) by waves 0..3, 8 columns a lane
+        float4 h0 = make_float4(0.f, 0.f, 0.f, 0.f), h1 = h0;
+        if (wid < NPOLL) {
+            if (wid == 0) {
+                // re-arm this workgroup's rows of this layer's output buffer
+                // and of the next layer's h buffer
+                if (lane < OR) cstore(xout + OR * g + lane, sent);
+                if (lane <= K) cstore2(hnext + lane * DI + GR * g, sent, sent);
+                if (tid == 0) {
+                    S.nready = 0;
+                    S.lgcnt = 0;
+                    S.dncnt = 0;
                 }
-                __hip_atomic_store(&s->exit2.v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
+            bool ok = true;
+            if (l == 0) {
+                const float *src = a.x0 ? a.x0 : a.hidden;
+                h0 = *reinterpret_cast<const float4 *>(src + 8 * tid);
+                h1 = *reinterpret_cast<const float4 *>(src + 8 * tid + 4);
+            } else {
+                const auto r = rsrc(a.xbuf + (par ^ 1) * DH, DH * 4);
+                ok = poll4(sy, r, 32u * (uint32_t)tid, h0) && poll4(sy, r, 32u * (uint32_t)tid + 16u, h1);
+            }
+            if (tid == g) {
+                if (l == 0 && a.x0) {
+                    h0 = *reinterpret_cast<const float4 *>(a.hidden + OR * g);
+                    h1 = *reinterpret_cast<const float4 *>(a.hidden + OR * g + 4);
+                }
+                *reinterpret_cast<float4 *>(&S.hown[0]) = h0;
+                *reinterpret_cast<float4 *>(&S.hown[4]) = h1;
+                if (l == 0 && a.x0) {
+                    h0 = *reinterpret_cast<const float4 *>(a.x0 + 8 * tid);
+                    h1 = *reinterpret_cast<const float4 *>(a.x0 + 8 * tid + 4);
+                }
+            }
+            float ss = fmaf(h0.x, h0.x, fmaf(h0.y, h0.y, fmaf(h0.z, h0.z, h0.w * h0.w)));
+            ss = fmaf(h1.x, h1.x, fmaf(h1.y, h1.y, fmaf(h1.z, h1.z, fmaf(h1.w, h1.w, ss))));
+            ss = wave_sum(ss);
+            if (lane == 0) S.red[wid] = ss;
+            if (!ok) S.abort = 1;
+        } else {
+            __builtin_amdgcn_s_waitcnt(0);  // prefetched weights have landed
+        }
+        __syncthreads();
+        if (S.abort) break;
+        if (wid < NPOLL) {
+            if (!(l == 0 && a.x0)) {
+                const float ss = S.red[0] + S.red[1] + S.red[2] + S.red[3];
+                const float inv = 1.0f / sqrtf(ss / (float)DH + a.eps);  // layer_ops.cu:209
+                if (Ly.norm_w) {
+                    const float4 w0 = *reinterpret_cast<const float4 *>(&S.nw[8 * tid]);
+                    const float4 w1 = *reinterpret_cast<const float4 *>(&S.nw[8 * tid + 4]);
+                    h0 = make_float4(h0.x * inv * w0.x, h0.y * inv * w0.y, h0.z * inv * w0.z, h0.w * inv * w0.w);
+                    h1 = make_float4(h1.x * inv * w1.x, h1.y * inv * w1.y, h1.z * inv * w1.z, h1.w * inv * w1.w);
+                } else {
+                    h0 = make_float4(h0.x * inv, h0.y * inv, h0.z * inv, h0.w * inv);
+                    h1 = make_float4(h1.x * inv, h1.y * inv, h1.z * inv, h1.w * inv);
+                }
+            }
+            *reinterpret_cast<float4 *>(&S.x[8 * tid]) = h0;
+            *reinterpret_cast<float4 *>(&S.x[8 * tid + 4]) = h1;
+        }
+        __syncthreads();
+        trace_point(a, l, TP_XREADY);
+
+        // ---- P2: router / shared-gate partials (waves 1..8, 4 columns a lane)
+        if (wid >= W_GU && wid < W_GU + MAXK) {
+            const int tr = tid - W_GU * WAVE;
+            const float4 xv = *reinterpret_cast<const float4 *>(&S.x[4 * tr]);
+            float r = 0.f, q = 0.f;
+            if (g < E) {
+                const float4 wr = *reinterpret_cast<const float4 *>(&S.wrow[4 * tr]);
+                r = fmaf(wr.x, xv.x, fmaf(wr.y, xv.y, fmaf(wr.z, xv.z, wr.w * xv.w)));
+            }
+            if (Ly.shg) {
+                const uint2 hh = *reinterpret_cast<const uint2 *>(&S.shg[4 * tr]);
+                q = fmaf(h2f(hh.x), xv.x, fmaf(h2f(hh.x >> 16), xv.y, fmaf(h2f(hh.y), xv.z, h2f(hh.y >> 16) * xv.w)));
+            }
+            r = wave_sum(r);
+            q = wave_sum(q);
+            if (lane == 0) {
+                S.rl[wid - W_GU] = r;
+                S.gl[wid - W_GU] = q;
+            }
+        }
+        __syncthreads();
+
+        // ---- P3: logits, routing, expert streams
+        if (wid < NPOLL) {
+            float logit = 0.f;
+#pragma unroll
+            for (int w = 0; w < MAXK; w++) logit += S.rl[w];
+            if (wid == 0) {
+                if (lane == 0 && g < E)
+                    __hip_atomic_store(a.tlogits + g,
+                                       ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, logit),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                trace_point(a, l, TP_LOGIT);
+            }
+            // poll one logit a lane
+            float v = -__builtin_inff();
+            bool ok = true;
+            if (tid < E) {
+                if (tid == g) v = logit;
+                else ok = poll_logit(sy, a.tlogits + tid, tag, v);
+            }
+            S.lg[tid] = v;
+            if (!ok) lds_put(&S.abort, 1);
+            if (lane == 0) lds_add(&S.lgcnt, 1);
+            if (wid == 0) {
+                // the selection passes gate every expert stream: let this wave
+                // issue ahead of the other waves on its SIMD
+                __builtin_amdgcn_s_setprio(3);
+                if (lds_wait(S, &S.lgcnt, NPOLL)) {
+                    trace_point(a, l, TP_POLLED);
+                    if (a.trace && tid == 0) a.trace[((size_t)blockIdx.x * a.L + l) * TP_N + TP_CYC0] = __builtin_amdgcn_s_memtime();
+                    float p[4];
+#pragma unroll
+                    for (int vv = 0; vv < 4; vv++) p[vv] = S.lg[lane + WAVE * vv];
+                    uint32_t key[4];
+                    softmax_keys<4>(p, E, key);
+                    Sel sel = sel_init(key);
+#pragma unroll
+                    for (int k = 0; k < MAXK; k++) {
+                        if (k >= K) break;
+                        uint32_t M;
+                        const int win = sel_pass(sel, lane, M);
+                        if (lane == 0) {
+                            S.idx[k] = win < E ? win : 0;
+                            S.key[k] = M;
+                            lds_put(&S.nready, k + 1);
+                        }
+                        if (k == 0) trace_point(a, l, TP_RANK1);
+                    }
+                    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                    const int my_idx = lane < K ? S.idx[lane] : 0;
+                    const float wk = renorm_weight(lane < K ? S.key[lane] : 0u, K);
+                    float gsh = 0.f;
+#pragma unroll
+                    for (int w = 0; w < MAXK; w++) gsh += S.gl[w];
+                    if (lane < K) S.w[lane] = wk;
+                    if (lane == 0) S.sgsh = sigmoidf_ref(gsh);
+                    if (g == 0) {
+                        if (a.idx_out && lane < K) a.idx_out[l * K + lane] = my_idx;
+                        if (a.w_out && lane < K) a.w_out[l * K + lane] = wk;
+                        if (a.gsh_out && lane == 0) a.gsh_out[l] = gsh;
+                    }
+                    trace_point(a, l, TP_ROUTED);
+                    if (a.trace && tid == 0) a.trace[((size_t)blockIdx.x * a.L + l) * TP_N + TP_CYC1] = __builtin_amdgcn_s_memtime();
+                } else if (lane == 0) {
+                    lds_put(&S.abort, 1);
+                }
+                __builtin_amdgcn_s_setprio(0);
+            }
+        }
+        if (wid >= W_GU && wid < W_GU + K) {
+            // routed gate/up of slot k = wave, as soon as rank k is known
+            const int slot = wid - W_GU + 1;
+            if (lds_wait(S, &S.nready, slot)) {
+                const int e = S.idx[slot - 1];
+                gu_issue<GR>(Ly.gate_exps + (uint64_t)e * Ly.gate_eb, Ly.up_exps + (uint64_t)e * Ly.up_eb, GR * g,
+                             S.gu[slot - 1]);
+                __builtin_amdgcn_s_waitcnt(0);
+                float hv[GR];
+                gu_compute<GR>(S, S.gu[slot - 1], hv);
+                if (lane == 0) {
+                    cstore2(hcur + slot * DI + GR * g, hv[0], hv[1]);
+                }
+            }
+        }
+        if (wid == W_SH || wid == W_SH + 1) {
+            // shared gate/up (weights prefetched), while routing runs
+            float hsh[1];
+            gu_compute<1>(S, S.shw[wid - W_SH], hsh);
+            if (lane == 0) cstore(hcur + GR * g + (wid - W_SH), hsh[0]);
+        }
+        if (wid >= W_DN) {
+            // routed down bands; chunk ch (16 B) of band slot ch / 210 lands
+            // at byte 16 ch of S.down
+            const int nchunk = (K + 1) * BAND16;
+            const int c0 = BAND16 + WAVE * (wid - W_DN);
+            const int ln = opaque(lane);
+            bool ok = true;
+            // gate/up first: the down bands are not needed before the h
+            // exchange, so their loads wait until every rank's gate/up is issued
+            ok = lds_wait(S, &S.nready, K, true);
+#pragma unroll
+            for (int i = 0; i < DN_LOADS; i++) {
+                const int cw = c0 + N_DN * WAVE * i;  // first chunk of this wave's load
+                if (cw >= nchunk) break;
+                const int shi = min((cw + WAVE - 1) / BAND16, K);
+                ok = ok && lds_wait(S, &S.nready, shi);
+                if (!ok) break;
+                const int ch = cw + ln;
+                if (ch < nchunk) {
+                    const int slot = ch / BAND16;
+                    const uint8_t *base = Ly.down_exps + (uint64_t)S.idx[slot - 1] * Ly.down_eb;
+                    lds_load16(base + (size_t)g * BAND + 16 * (ch - slot * BAND16), &S.down[4 * cw]);
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            if (lane == 0) lds_add(&S.dncnt, 1);
+        }
+
+        // ---- P4: pre-decode this wave's down unit once every band is in
+        // (units 16, 17 by waves 1, 2 into LDS)
+        float w0[32];
+        const bool extra = wid >= W_GU && wid < W_GU + 2 && wid - W_GU + NWV < NU;
+        float4 (*xw)[WAVE] = reinterpret_cast<float4 (*)[WAVE]>(&S.gu[wid >= W_GU && wid < W_GU + 2 ? wid - W_GU : 0][0][0]);
+        if (wid < NU && lds_wait(S, &S.dncnt, N_DN)) {
+            down_predecode(S, wid, w0);
+            if (extra) predecode_to_lds(S, wid - W_GU + NWV, xw);
+        }
+
+        // ---- P5: every slot's h into LDS, polled
+        if (!lds_get(&S.abort)) {
+            const auto hr = rsrc(hcur, (uint32_t)(NH * 4));
+            bool ok = true;
+            for (int ch = tid; ch < NH / 4; ch += NT) {
+                float4 v;
+                ok = ok && poll4(sy, hr, 16u * (uint32_t)ch, v);
+                *reinterpret_cast<float4 *>(&S.h[4 * ch]) = v;
+            }
+            if (!ok) S.abort = 1;
+
+        }
+        __syncthreads();
+        if (S.abort) break;
+        trace_point(a, l, TP_HREADY);
+
+        // ---- P6: down dots
+        if (wid < NU) {
+            down_dot(S, wid, w0);
+            if (extra) down_dot_lds(S, wid - W_GU + NWV, xw);
+        }
+        trace_point(a, l, TP_DDOT);
+        __syncthreads();
+        trace_point(a, l, TP_COMB);
+
+        // ---- P7: next layer's fixed weights (every buffer they land in has
+        // been consumed) by waves 4..15; combine in the reference order
+        // (one_layer.cu:1443-1471) and publish the rows to the next layer and
+        // the caller by wave 0
+        if (l + 1 < a.L) prefetch_fixed(S, load_layer(a, l + 1), g, E, wid);
+        if (wid == 0 && lane < OR) {
+            float d[NSLOT], wt[MAXK];
+#pragma unroll
+            for (int k = 0; k < NSLOT; k++) d[k] = S.dot[k][lane];
+#pragma unroll
+            for (int k = 0; k < MAXK; k++) wt[k] = S.w[k];
+            float v = S.hown[lane];
+            v += S.sgsh * d[0];
+#pragma unroll
+            for (int k = 0; k < MAXK; k++)
+                if (k < K) v += wt[k] * d[k + 1];
+            if (l + 1 < a.L) cstore(xout + OR * g + lane, v);
+            a.hidden[OR * g + lane] = v;
+            if (lane == 0) trace_here(a, l, TP_OUT);
         }
     }
 }
@@ -610,41 +876,44 @@ DecLayer to_dec(const bread_moe_layer_t &L)
 bool decode_shape_ok(const bread_moe_shape_t &s)
 {
     return s.hidden == DH && s.expert_inter == DI && s.shared_inter == DI && s.n_experts <= 256 &&
-           s.n_experts >= s.top_k && s.top_k <= MAXK;
+           s.n_experts >= s.top_k && s.top_k >= 1 && s.top_k <= MAXK;
 }
 
-void fill_roles(const bread_moe_shape_t &s, DecArgs &a)
+bool layer_ok(const bread_moe_layer_t &L)
 {
-    a.E = s.n_experts;
-    a.K = s.top_k;
-    a.nR = (s.n_experts + 1 + 3) / 4;
-    a.nS = DI / UPB;
-    a.nG = s.top_k * DI / UPB;
-    a.nD = DH / DR;
+    // buffer loads and 16-byte band loads assume these alignments
+    const uintptr_t m = (uintptr_t)L.gate_exps | (uintptr_t)L.up_exps | (uintptr_t)L.down_exps |
+                        (uintptr_t)L.gate_shexp | (uintptr_t)L.up_shexp | (uintptr_t)L.down_shexp |
+                        (uintptr_t)L.router | (uintptr_t)L.post_norm_w;
+    return (m & 15u) == 0 && (L.gate_expert_bytes & 15u) == 0 && (L.up_expert_bytes & 15u) == 0 &&
+           (L.down_expert_bytes & 15u) == 0 && ((uintptr_t)L.shexp_gate & 7u) == 0;
 }
 
 int launch(bread_moe_ctx_t *c, DecArgs &a, hipStream_t st)
 {
-    const int grid = a.nR + a.nS + a.nG + a.nD;
-    // One layer: every wait is on lower-indexed workgroups, which in-order
-    // dispatch starts first, so the grid need not be co-resident.  Several
-    // layers: later layers wait on higher-indexed workgroups too, so the whole
-    // grid must be resident at once (a cooperative launch checks it).
-    if (a.L > 1 && grid > c->decode_max_blocks) return BREAD_ERR_SHAPE;
-    a.logits = c->logits;
-    a.xnorm = c->xnorm;
-    a.hbuf = c->h;
+    // Every workgroup waits on every other one, so all G must be resident at
+    // once.  G equals the CU count and the LDS footprint allows one workgroup
+    // per CU, so an otherwise idle device runs the whole grid at once.  A
+    // cooperative launch would guarantee it but costs ~20 us per launch on
+    // MI355X (a normal one ~2.4 us); without it, a device shared with other
+    // long-running work can delay some workgroups, and the bounded waits then
+    // flag an error rather than hang.
+    if (c->decode_max_blocks < G) return BREAD_ERR_SHAPE;
+    a.E = c->shape.n_experts;
+    a.K = c->shape.top_k;
+    a.tlogits = c->tlogits;
+    a.xbuf = c->xbuf;
+    a.hbuf = c->hbuf;
     a.sync = c->dsync;
-    a.trace = (c->trace && (size_t)grid * a.L * TP_N <= c->trace_words) ? c->trace : nullptr;
+    a.trace = (c->trace && (size_t)G * a.L * TP_N <= c->trace_words) ? c->trace : nullptr;
     a.eps = c->shape.rms_eps;
+    a.epoch0 = c->epoch;
+    a.hphase0 = c->hphase;
     bread_clear_stale_error();
-    if (a.L == 1) {
-        hipLaunchKernelGGL(k_decode, dim3(grid), dim3(256), 0, st, a);
-        BREAD_HIP(hipGetLastError());
-    } else {
-        void *args[] = {&a};
-        BREAD_HIP(hipLaunchCooperativeKernel((const void *)k_decode, dim3(grid), dim3(256), args, 0, st));
-    }
+    hipLaunchKernelGGL(k_decode, dim3(G), dim3(NT), 0, st, a);
+    BREAD_HIP(hipGetLastError());
+    c->epoch += (uint32_t)a.L;
+    c->hphase = (c->hphase + a.L) % 3;
     return BREAD_OK;
 }
 
@@ -655,7 +924,7 @@ int bread_decode_max_blocks(int *out)
     int dev = 0, cus = 0, per_cu = 0;
     BREAD_HIP(hipGetDevice(&dev));
     BREAD_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    BREAD_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_decode, 256, 0));
+    BREAD_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_decode, NT, 0));
     *out = cus * per_cu;
     return BREAD_OK;
 }
@@ -663,10 +932,9 @@ int bread_decode_max_blocks(int *out)
 int bread_launch_moe_decode(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, float *hidden,
                             hipStream_t st)
 {
-    if (!decode_shape_ok(c->shape)) return BREAD_ERR_SHAPE;
+    if (!decode_shape_ok(c->shape) || !layer_ok(*L)) return BREAD_ERR_SHAPE;
     DecArgs a;
     memset(&a, 0, sizeof(a));
-    fill_roles(c->shape, a);
     a.layers = nullptr;
     a.one = to_dec(*L);
     a.L = 1;
@@ -683,23 +951,30 @@ int bread_launch_decode_layers(bread_moe_ctx_t *c, const bread_moe_layer_t *laye
 {
     if (!decode_shape_ok(c->shape)) return BREAD_ERR_SHAPE;
     BREAD_REQUIRE(n <= c->max_layers, BREAD_ERR_CAPACITY, "more layers than the context holds");
-    // the device layer table is re-uploaded only when it changes
-    DecLayer *tab = (DecLayer *)c->h_layers;
-    bool same = c->n_layers_uploaded == n;
-    for (int l = 0; l < n; l++) {
-        const DecLayer d = to_dec(layers[l]);
-        if (same && memcmp(&tab[l], &d, sizeof(d)) != 0) same = false;
-        tab[l] = d;
-    }
-    if (!same) {
-        BREAD_HIP(hipMemcpyAsync(c->d_layers, tab, (size_t)n * sizeof(DecLayer), hipMemcpyHostToDevice, st));
-        BREAD_HIP(hipStreamSynchronize(st));
-        c->n_layers_uploaded = n;
-    }
+    for (int l = 0; l < n; l++)
+        if (!layer_ok(layers[l])) return BREAD_ERR_SHAPE;
     DecArgs a;
     memset(&a, 0, sizeof(a));
-    fill_roles(c->shape, a);
-    a.layers = (const DecLayer *)c->d_layers;
+    if (n == 1) {
+        // one layer travels in the kernel arguments: no table upload
+        a.layers = nullptr;
+        a.one = to_dec(layers[0]);
+    } else {
+        // the device layer table is re-uploaded only when it changes
+        DecLayer *tab = (DecLayer *)c->h_layers;
+        bool same = c->n_layers_uploaded == n;
+        for (int l = 0; l < n; l++) {
+            const DecLayer d = to_dec(layers[l]);
+            if (same && memcmp(&tab[l], &d, sizeof(d)) != 0) same = false;
+            tab[l] = d;
+        }
+        if (!same) {
+            BREAD_HIP(hipMemcpyAsync(c->d_layers, tab, (size_t)n * sizeof(DecLayer), hipMemcpyHostToDevice, st));
+            BREAD_HIP(hipStreamSynchronize(st));
+            c->n_layers_uploaded = n;
+        }
+        a.layers = (const DecLayer *)c->d_layers;
+    }
     a.L = n;
     a.x0 = nullptr;
     a.hidden = hidden;
@@ -709,15 +984,39 @@ int bread_launch_decode_layers(bread_moe_ctx_t *c, const bread_moe_layer_t *laye
     return launch(c, a, st);
 }
 
+// Exchange buffers start out "unwritten" (sentinel everywhere).
+int bread_decode_reset(bread_moe_ctx_t *c)
+{
+    BREAD_HIP(hipMemsetD32((hipDeviceptr_t)c->xbuf, (int)SENTINEL, 2 * DH));
+    BREAD_HIP(hipMemsetD32((hipDeviceptr_t)c->hbuf, (int)SENTINEL, 3 * NSLOT * DI));
+    BREAD_HIP(hipMemset(c->tlogits, 0, 256 * sizeof(uint64_t)));
+    BREAD_HIP(hipMemset(c->dsync, 0, sizeof(bread_decode_sync)));
+    c->epoch = 0;
+    c->hphase = 0;
+    return BREAD_OK;
+}
+
+size_t bread_decode_xbuf_floats()
+{
+    return 2 * DH;
+}
+
+size_t bread_decode_hbuf_floats()
+{
+    return 3 * NSLOT * DI;
+}
+
 size_t bread_decode_layer_record_bytes()
 {
     return sizeof(DecLayer);
 }
 
-int bread_decode_grid(const bread_moe_shape_t &s)
+int bread_decode_grid(const bread_moe_shape_t &)
 {
-    DecArgs a;
-    memset(&a, 0, sizeof(a));
-    fill_roles(s, a);
-    return a.nR + a.nS + a.nG + a.nD;
+    return G;
+}
+
+int bread_decode_trace_points()
+{
+    return TP_N;
 }

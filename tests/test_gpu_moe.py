@@ -299,3 +299,51 @@ def test_stack_small_matches_oracle():
     got = hd.cpu().numpy()[0]
     assert_moe_close(got, href, base=h[0])
     arena.close()
+
+
+def test_decode_layers_stack_matches_oracle():
+    """Config 3 in one launch per token: h <- h + MoE_l(RMSNorm(h) * w_l) over
+    4 arena layers with non-unit norm weights, for 2 tokens; single-layer
+    launches in between keep the context's counters in step (the kernel's
+    counters and tags only grow, indexed by the context's layer epoch)."""
+    s = api.shape()
+    L = 4
+    arena = B.Arena(s, L)
+    for l in range(L):
+        arena.synth_layer(l, seed=77, router_std=1.0 / np.sqrt(s.hidden))
+    rng = np.random.default_rng(13)
+    nws = [rng.uniform(0.5, 1.5, s.hidden).astype(np.float32) for _ in range(L)]
+    nwd = [dev(w) for w in nws]
+    descs = []
+    for l in range(L):
+        d = arena.layer(l)
+        d.post_norm_w = nwd[l].data_ptr()
+        descs.append(d)
+    torch.cuda.synchronize()
+    hls = [arena_host_layer(s, arena.layer(l)) for l in range(L)]
+    ctx = B.MoeContext(s, max_tokens=1)
+    h0 = xs(1, s.hidden, 14)[0]
+    hd = dev(h0[None])
+    href = h0.copy()
+    for step in range(2):
+        idx, w, _ = ctx.decode_layers(descs, hd, want_routing=True)
+        torch.cuda.synchronize()
+        ridx = []
+        for l in range(L):
+            xr = O.rms_norm_weighted(href, nws[l], s.rms_eps)
+            hh = href[None].copy()
+            ri, rw, _ = O.moe_forward(hls[l], xr[None], hh, 1)
+            ridx.append(ri[0])
+            href = hh[0]
+        assert np.array_equal(idx.cpu().numpy(), np.stack(ridx)), f"step {step}"
+        assert_moe_close(hd.cpu().numpy()[0], href, base=h0)
+        # a single-layer launch on the same context between stack launches
+        xo = dev(xs(1, s.hidden, 15))
+        ho = torch.zeros(1, s.hidden, device=DEV)
+        ctx.forward(descs[0], xo, ho, 1)
+        torch.cuda.synchronize()
+        ref1 = np.zeros((1, s.hidden), np.float32)
+        O.moe_forward(hls[0], xo.cpu().numpy(), ref1, 1)
+        assert_moe_close(ho.cpu().numpy(), ref1)
+    assert ctx.check_device() == 0
+    arena.close()
