@@ -178,8 +178,9 @@ int bread_route_layer(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer, cons
  * reference order (shared first, then routed experts by rank).
  * d_x_normed fp32 [n_tokens][H] (the post-attention RMSNorm output),
  * d_hidden fp32 [n_tokens][H] in/out.  Optional outputs d_idx/d_w/d_gsh as in
- * bread_route (may be NULL).  n_tokens == 1 runs the single-launch decode
- * kernel; larger batches run the grouped multi-token path. */
+ * bread_route (may be NULL).  n_tokens == 1 runs the persistent decode
+ * kernel when the shape allows it (see bread_moe_decode_layers); other
+ * shapes and larger batches run the multi-token path. */
 int bread_moe_forward(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer,
                       const float *d_x_normed, float *d_hidden, int n_tokens,
                       int32_t *d_idx, float *d_w, float *d_gsh, bread_stream_t stream);
@@ -192,20 +193,26 @@ int bread_moe_forward(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer,
  * fp32 [H] in/out.  Optional per-layer routing outputs d_idx int32
  * [n_layers][K], d_w fp32 [n_layers][K], d_gsh fp32 [n_layers] (raw
  * shared-gate logits); NULL skips them.  Needs the shape the persistent
- * kernel is built for (H 2048, I = I_sh = 512, E <= 256, K <= 11) and
- * n_layers <= 256; returns BREAD_ERR_SHAPE otherwise.  The host layer array
- * is copied into the context; a different array than the previous call's
- * costs one synchronous upload. */
+ * kernel is built for (H 2048, I = I_sh = 512, E <= 256, K <= 8), 16-byte
+ * aligned weights and n_layers <= 256; returns BREAD_ERR_SHAPE otherwise.
+ * For n_layers > 1 the host layer array is copied into the context; a
+ * different array than the previous call's costs one synchronous upload.
+ * The kernel runs one 1024-thread workgroup per CU and every workgroup waits
+ * on the others, so it needs the whole device: launches that overlap on one
+ * device (any context or stream) are not allowed, and one that cannot get
+ * all CUs times out and flags a device error (bread_moe_ctx_check). */
 int bread_moe_decode_layers(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layers, int n_layers,
                             float *d_hidden, int32_t *d_idx, float *d_w, float *d_gsh,
                             bread_stream_t stream);
 
 /* Timeline of the decode kernel: when d_buf is non-NULL, every launch with
- * grid * n_layers * 8 <= n_words records 64-bit wall-clock stamps (100 MHz)
- * at d_buf[(workgroup * n_layers + layer) * 8 + point], points 0 start,
- * 1 inputs ready, 2 routing known, 3 weight loads issued, 4 SwiGLU outputs
- * ready, 5 done.  *grid_out receives the launch's workgroup count.  NULL
- * turns it off. */
+ * grid * n_layers * 12 <= n_words records 64-bit wall-clock stamps (100 MHz)
+ * at d_buf[(workgroup * n_layers + layer) * 12 + point], points 0 layer
+ * start, 1 input normalised, 2 own logit published, 3 every logit seen,
+ * 4 rank-1 expert known, 5 routing done, 6 own down dots done, 7 every down
+ * dot done, 8 every SwiGLU output seen, 9 output rows stored; 10 and 11 hold
+ * the core clock (s_memtime) at points 3 and 5.  *grid_out receives the
+ * launch's workgroup count.  NULL turns it off. */
 int bread_moe_ctx_set_trace(bread_moe_ctx_t *ctx, uint64_t *d_buf, size_t n_words, int *grid_out);
 
 /* out[t] = x[t] * (1/sqrt(mean(x[t]^2) + eps)) * w, fp32, n_tokens rows of n
