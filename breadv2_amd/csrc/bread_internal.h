@@ -60,9 +60,9 @@ struct bread_moe_ctx {
     float *w;          // [max_tokens][K]
     float *gsh;        // [max_tokens]
     float *h;          // [max_tokens][K+1][Imax] SwiGLU outputs, slot 0 = shared
-    uint64_t *tlogits; // [256] decode router logits, (epoch tag << 32) | fp32 bits
-    float *xbuf;       // [2][H] decode layer outputs by parity (sentinel = unwritten)
-    float *hbuf;       // [3][(Kmax+1) * I] decode SwiGLU outputs by layer mod 3
+    uint64_t *tlogits; // decode router logits, (epoch tag << 32) | fp32 bits, one per 64 B
+    float *xbuf;       // decode layer outputs by parity, one 128 B record per workgroup
+    float *hbuf;       // decode SwiGLU outputs by layer mod 3, one 128 B record per workgroup
     uint32_t epoch;    // layers run by the decode kernel on this context
     int hphase;        // epoch mod 3
     bread_decode_sync *dsync;
@@ -100,4 +100,5 @@ int bread_decode_trace_points();
 int bread_decode_reset(bread_moe_ctx_t *ctx);
 size_t bread_decode_xbuf_floats();
 size_t bread_decode_hbuf_floats();
+size_t bread_decode_tlogit_words();
 size_t bread_decode_layer_record_bytes();

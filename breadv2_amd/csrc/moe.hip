@@ -129,7 +129,7 @@ extern "C" int bread_moe_ctx_create(const bread_moe_shape_t *shape, int max_toke
     if (e == hipSuccess) e = hipMalloc((void **)&c->w, T * K * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->gsh, T * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->h, T * (K + 1) * Imax * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc((void **)&c->tlogits, 256 * sizeof(uint64_t));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->tlogits, bread_decode_tlogit_words() * sizeof(uint64_t));
     if (e == hipSuccess) e = hipMalloc((void **)&c->xbuf, bread_decode_xbuf_floats() * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->hbuf, bread_decode_hbuf_floats() * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->dsync, sizeof(bread_decode_sync));

@@ -9,8 +9,9 @@
 // Workgroup g owns router row g, gate/up rows 2g and 2g+1 of every expert
 // slot (slot 0 = shared expert, slot k = routed rank k-1) and output rows
 // 8g..8g+7.  Its 16 waves have fixed jobs:
-//   waves 0..3   poll the previous layer's output and the router logits
-//                (wave 0 then runs softmax/top-k and the combine);
+//   all waves    poll the previous layer's output (two columns a thread);
+//   waves 0..3   poll the router logits (wave 0 then runs softmax/top-k and
+//                the combine);
 //   waves 1..8   router row and shared-gate dot, then the gate/up rows of
 //                routed slot k = wave;
 //   waves 9, 10  shared-expert gate/up rows (before routing is known);
@@ -20,10 +21,11 @@
 //                norm weights, shared-gate vector, shared gate/up rows and
 //                shared down band), once this layer's h is in.
 // Weights travel HBM -> LDS by gfx950 direct-to-LDS loads, so no wave holds
-// weight registers while loads are in flight.  Waves that issue loads are
-// never the ones that poll: on gfx9, s_waitcnt vmcnt counts loads and stores
-// together and in order, so a poll issued behind weight loads would wait for
-// them.
+// weight registers while loads are in flight.  On gfx9, s_waitcnt vmcnt counts
+// loads and stores together and in order, so a poll issued behind weight
+// loads waits for them: the logit pollers never hold weight loads, and the
+// next layer's weights are requested early enough (after this layer's h is
+// in) to have landed before that layer's first poll returns.
 //
 // Routing is published rank by rank: wave 0 writes expert k to LDS as soon as
 // selection pass k ends, and the gate/up and down waves start that slot's
@@ -79,7 +81,7 @@ constexpr int BAND = OR * DN_ROW;        // one slot's down rows of a workgroup:
 constexpr int BAND16 = BAND / 16;        // 210 16-byte chunks
 constexpr int MAXK = 8;
 constexpr int NSLOT = MAXK + 1;
-constexpr int NPOLL = 4;                 // waves 0..3 poll the hidden and logit exchanges
+constexpr int NPOLL = 4;                 // waves 0..3 poll the logits, one a lane
 constexpr int W_GU = 1;                  // waves 1..8: router partials, routed gate/up
 constexpr int W_SH = 9;                  // waves 9, 10: shared gate/up
 constexpr int W_DN = 9;                  // waves 9..15: routed down bands
@@ -90,11 +92,17 @@ constexpr uint32_t SPIN_LIMIT = 1u << 18;
 constexpr uint32_t BUF_WORD3 = 0x00020000u;  // raw buffer descriptor word 3 (gfx9)
 constexpr int AUX_COHERENT = 16;             // sc1: device-coherent access
 constexpr uint32_t SENTINEL = 0x7FA5A5A5u;   // signalling NaN: "not written yet"
+// Exchange layouts: every workgroup publishes into lines of its own, so a
+// store never invalidates lines other workgroups write (measured on MI355X:
+// an all-to-all round over shared lines costs up to 1.8x one over private
+// lines).
+constexpr int LG_STRIDE = 8;             // tagged logit words: one per 64 B
+constexpr int XREC = 32;                 // floats per workgroup record (128 B): output rows, h values
 
 static_assert(DH % G == 0 && DI % G == 0 && GR == 2 && OR == 8, "row ownership assumes 256 workgroups");
 static_assert(NBH == 8 && DI / QK == 2, "lane layouts assume H = 2048 and I = 512");
 static_assert(BAND % 16 == 0, "down bands are loaded in 16-byte chunks");
-static_assert(NPOLL * WAVE * 8 == DH && NPOLL * WAVE == 256, "pollers: 8 columns, one logit a lane");
+static_assert(NPOLL * WAVE == 256 && 2 * NT == DH, "pollers: one logit a lane; two columns a thread");
 static_assert(W_GU + MAXK == W_SH && W_SH + 2 <= NWV, "wave roles");
 
 // Trace points recorded per (workgroup, layer) when a trace buffer is given.
@@ -132,9 +140,9 @@ struct DecArgs {
     const float *x0;         // non-NULL: layer 0 input given (already normalised)
     float *hidden;           // [H] caller's hidden: input of layer 0, output of every layer
     float eps;
-    uint64_t *tlogits;       // [256] epoch-tagged logits
-    float *xbuf;             // [2][H] layer outputs by parity (sentinel protocol)
-    float *hbuf;             // [3][NSLOT * I] SwiGLU outputs by layer mod 3 (sentinel protocol)
+    uint64_t *tlogits;       // [256][LG_STRIDE] epoch-tagged logits
+    float *xbuf;             // [2][G][XREC] layer outputs by parity: rows 8g..8g+7 of workgroup g
+    float *hbuf;             // [3][G][XREC] SwiGLU outputs by layer mod 3: [slot][rows 2g, 2g+1]
     int32_t *idx_out;        // [L][K] or NULL
     float *w_out;            // [L][K] or NULL
     float *gsh_out;          // [L] or NULL
@@ -153,7 +161,7 @@ struct Smem {
     uint4 shw[2][4][WAVE];             // shared gate/up rows: [row][hg, qg, hu, qu][lane] (prefetched)
     uint4 gu[MAXK][4 * GR][WAVE];      // routed gate/up rows: [slot-1][4 row + (hg, qg, hu, qu)][lane]
     float lg[256];                     // router logits of the layer
-    float red[NPOLL];                  // sum-of-squares partials
+    float red[NWV];                    // sum-of-squares partials
     float rl[MAXK], gl[MAXK];          // router / shared-gate partials
     float dot[NSLOT][OR];              // down dots
     float hown[OR];                    // this workgroup's rows of h before the layer
@@ -289,13 +297,27 @@ __device__ __forceinline__ bool unwritten(float v)
 }
 
 // Per-thread bounded poll of 4 coherent floats at byte offset off of a
-// buffer until none is the sentinel.  Returns false on time-out (flagging the
-// error) or when another workgroup flagged one.
-__device__ __forceinline__ bool poll4(bread_decode_sync *s, __amdgpu_buffer_rsrc_t r, uint32_t off, float4 &v)
+// buffer until none of the checked ones (all four, or the low two when hi is
+// false) is the sentinel.  Returns false on time-out (flagging the error) or
+// when another workgroup flagged one.
+__device__ __forceinline__ bool poll4(bread_decode_sync *s, __amdgpu_buffer_rsrc_t r, uint32_t off, float4 &v,
+                                      bool hi = true)
 {
     for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
         v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX_COHERENT));
-        if (!unwritten(v.x) && !unwritten(v.y) && !unwritten(v.z) && !unwritten(v.w)) return true;
+        if (!unwritten(v.x) && !unwritten(v.y) && !(hi && (unwritten(v.z) || unwritten(v.w)))) return true;
+        if ((it & 63) == 63 && has_error(s)) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    flag_error(s, 1u);
+    return false;
+}
+
+__device__ __forceinline__ bool poll2(bread_decode_sync *s, __amdgpu_buffer_rsrc_t r, uint32_t off, float2 &v)
+{
+    for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
+        v = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, AUX_COHERENT));
+        if (!unwritten(v.x) && !unwritten(v.y)) return true;
         if ((it & 63) == 63 && has_error(s)) return false;
         __builtin_amdgcn_s_sleep(1);
     }
@@ -329,7 +351,10 @@ __device__ __forceinline__ bool poll_logit(bread_decode_sync *s, const uint64_t 
 // holding that maximum then has the lowest index i = lane + 64 v.  That is
 // cpu_topk's strict '>' scan from i = 0 (layer_ops.cu:231-243).  Each lane
 // keeps its four packed keys sorted, so a pass is one wave max, one ballot
-// and a shift in the winning lane.
+// and a shift in the winning lane.  (A radix search for the K-th largest key
+// finds the whole set without passes, but on gfx950 its ballot counts chain
+// through VCC and took longer than the eight passes, and the passes publish
+// rank 1 far sooner.)
 struct Sel {
     uint32_t k0, k1, k2, k3;  // packed keys, descending
 };
@@ -358,12 +383,11 @@ __device__ __forceinline__ int sel_pass(Sel &s, int lane, uint32_t &M)
     const uint32_t top = wave_max_u32(s.k0);
     const uint64_t b = __builtin_amdgcn_ballot_w64(s.k0 == top);
     const int wl = (int)__builtin_ctzll(b);
-    if (lane == wl) {
-        s.k0 = s.k1;
-        s.k1 = s.k2;
-        s.k2 = s.k3;
-        s.k3 = 0u;
-    }
+    const bool w = lane == wl;
+    s.k0 = w ? s.k1 : s.k0;
+    s.k1 = w ? s.k2 : s.k1;
+    s.k2 = w ? s.k3 : s.k2;
+    s.k3 = w ? 0u : s.k3;
     M = top >> 2;
     return wl + WAVE * (int)(3u - (top & 3u));
 }
@@ -571,7 +595,6 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
     const int tid = (int)threadIdx.x;
     const int wid = wave_id(), lane = lane_id();
     const int K = a.K, E = a.E;
-    const int NH = (K + 1) * DI;  // h values in use per parity
     const int NU = 2 * (K + 1);   // down units
     bread_decode_sync *sy = a.sync;
     const float sent = __builtin_bit_cast(float, SENTINEL);
@@ -586,75 +609,61 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
         const DecLayer Ly = load_layer(a, l);
         const uint32_t tag = a.epoch0 + (uint32_t)l + 1u;
         const int par = (int)((a.epoch0 + (uint32_t)l) & 1u);
-        float *xout = a.xbuf + par * DH;             // this layer's output rows
+        float *xout = a.xbuf + par * (G * XREC);     // this layer's output rows
         const int hp = (a.hphase0 + l) % 3;
-        float *hcur = a.hbuf + hp * (NSLOT * DI);                  // this layer's h
-        float *hnext = a.hbuf + (hp == 2 ? 0 : hp + 1) * (NSLOT * DI);  // next layer's
+        float *hcur = a.hbuf + hp * (G * XREC);                    // this layer's h
+        float *hnext = a.hbuf + (hp == 2 ? 0 : hp + 1) * (G * XREC);  // next layer's
         trace_point(a, l, TP_START);
 
         // ---- P1: h of the layer (caller's buffer for the first layer, else
-        // the previous layer's output, polled) by waves 0..3, 8 columns a lane
-        float4 h0 = make_float4(0.f, 0.f, 0.f, 0.f), h1 = h0;
-        if (wid < NPOLL) {
-            if (wid == 0) {
-                // re-arm this workgroup's rows of this layer's output buffer
-                // and of the next layer's h buffer
-                if (lane < OR) cstore(xout + OR * g + lane, sent);
-                if (lane <= K) cstore2(hnext + lane * DI + GR * g, sent, sent);
-                if (tid == 0) {
-                    S.nready = 0;
-                    S.lgcnt = 0;
-                    S.dncnt = 0;
-                }
+        // the previous layer's output, polled), thread t: columns 2t, 2t+1
+        if (wid == 0) {
+            // re-arm this workgroup's rows of this layer's output buffer and
+            // its record of the next layer's h buffer
+            if (lane < OR) cstore(xout + XREC * g + lane, sent);
+            if (lane <= K) cstore2(hnext + XREC * g + GR * lane, sent, sent);
+            if (tid == 0) {
+                S.nready = 0;
+                S.lgcnt = 0;
+                S.dncnt = 0;
             }
+        }
+        float2 hv;
+        {
             bool ok = true;
+            const bool own = (tid >> 2) == g;  // threads 4g..4g+3 hold rows 8g..8g+7
             if (l == 0) {
                 const float *src = a.x0 ? a.x0 : a.hidden;
-                h0 = *reinterpret_cast<const float4 *>(src + 8 * tid);
-                h1 = *reinterpret_cast<const float4 *>(src + 8 * tid + 4);
+                hv = *reinterpret_cast<const float2 *>(src + 2 * tid);
+                if (own && a.x0) {
+                    const float2 o = *reinterpret_cast<const float2 *>(a.hidden + 2 * tid);
+                    *reinterpret_cast<float2 *>(&S.hown[2 * (tid & 3)]) = o;
+                }
             } else {
-                const auto r = rsrc(a.xbuf + (par ^ 1) * DH, DH * 4);
-                ok = poll4(sy, r, 32u * (uint32_t)tid, h0) && poll4(sy, r, 32u * (uint32_t)tid + 16u, h1);
+                const auto r = rsrc(a.xbuf + (par ^ 1) * (G * XREC), G * XREC * 4);
+                ok = poll2(sy, r, 4u * (uint32_t)(XREC * (tid >> 2) + 2 * (tid & 3)), hv);
             }
-            if (tid == g) {
-                if (l == 0 && a.x0) {
-                    h0 = *reinterpret_cast<const float4 *>(a.hidden + OR * g);
-                    h1 = *reinterpret_cast<const float4 *>(a.hidden + OR * g + 4);
-                }
-                *reinterpret_cast<float4 *>(&S.hown[0]) = h0;
-                *reinterpret_cast<float4 *>(&S.hown[4]) = h1;
-                if (l == 0 && a.x0) {
-                    h0 = *reinterpret_cast<const float4 *>(a.x0 + 8 * tid);
-                    h1 = *reinterpret_cast<const float4 *>(a.x0 + 8 * tid + 4);
-                }
-            }
-            float ss = fmaf(h0.x, h0.x, fmaf(h0.y, h0.y, fmaf(h0.z, h0.z, h0.w * h0.w)));
-            ss = fmaf(h1.x, h1.x, fmaf(h1.y, h1.y, fmaf(h1.z, h1.z, fmaf(h1.w, h1.w, ss))));
-            ss = wave_sum(ss);
+            if (own && !(l == 0 && a.x0)) *reinterpret_cast<float2 *>(&S.hown[2 * (tid & 3)]) = hv;
+            const float ss = wave_sum(fmaf(hv.x, hv.x, hv.y * hv.y));
             if (lane == 0) S.red[wid] = ss;
             if (!ok) S.abort = 1;
-        } else {
-            __builtin_amdgcn_s_waitcnt(0);  // prefetched weights have landed
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's prefetched weights have landed too
         }
         __syncthreads();
         if (S.abort) break;
-        if (wid < NPOLL) {
-            if (!(l == 0 && a.x0)) {
-                const float ss = S.red[0] + S.red[1] + S.red[2] + S.red[3];
-                const float inv = 1.0f / sqrtf(ss / (float)DH + a.eps);  // layer_ops.cu:209
-                if (Ly.norm_w) {
-                    const float4 w0 = *reinterpret_cast<const float4 *>(&S.nw[8 * tid]);
-                    const float4 w1 = *reinterpret_cast<const float4 *>(&S.nw[8 * tid + 4]);
-                    h0 = make_float4(h0.x * inv * w0.x, h0.y * inv * w0.y, h0.z * inv * w0.z, h0.w * inv * w0.w);
-                    h1 = make_float4(h1.x * inv * w1.x, h1.y * inv * w1.y, h1.z * inv * w1.z, h1.w * inv * w1.w);
-                } else {
-                    h0 = make_float4(h0.x * inv, h0.y * inv, h0.z * inv, h0.w * inv);
-                    h1 = make_float4(h1.x * inv, h1.y * inv, h1.z * inv, h1.w * inv);
-                }
+        if (!(l == 0 && a.x0)) {
+            float ss = 0.f;
+#pragma unroll
+            for (int w = 0; w < NWV; w++) ss += S.red[w];
+            const float inv = 1.0f / sqrtf(ss / (float)DH + a.eps);  // layer_ops.cu:209
+            if (Ly.norm_w) {
+                const float2 nw = *reinterpret_cast<const float2 *>(&S.nw[2 * tid]);
+                hv = make_float2(hv.x * inv * nw.x, hv.y * inv * nw.y);
+            } else {
+                hv = make_float2(hv.x * inv, hv.y * inv);
             }
-            *reinterpret_cast<float4 *>(&S.x[8 * tid]) = h0;
-            *reinterpret_cast<float4 *>(&S.x[8 * tid + 4]) = h1;
         }
+        *reinterpret_cast<float2 *>(&S.x[2 * tid]) = hv;
         __syncthreads();
         trace_point(a, l, TP_XREADY);
 
@@ -687,7 +696,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             for (int w = 0; w < MAXK; w++) logit += S.rl[w];
             if (wid == 0) {
                 if (lane == 0 && g < E)
-                    __hip_atomic_store(a.tlogits + g,
+                    __hip_atomic_store(a.tlogits + LG_STRIDE * g,
                                        ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, logit),
                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 trace_point(a, l, TP_LOGIT);
@@ -697,7 +706,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             bool ok = true;
             if (tid < E) {
                 if (tid == g) v = logit;
-                else ok = poll_logit(sy, a.tlogits + tid, tag, v);
+                else ok = poll_logit(sy, a.tlogits + LG_STRIDE * tid, tag, v);
             }
             S.lg[tid] = v;
             if (!ok) lds_put(&S.abort, 1);
@@ -759,7 +768,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                 float hv[GR];
                 gu_compute<GR>(S, S.gu[slot - 1], hv);
                 if (lane == 0) {
-                    cstore2(hcur + slot * DI + GR * g, hv[0], hv[1]);
+                    cstore2(hcur + XREC * g + GR * slot, hv[0], hv[1]);
                 }
             }
         }
@@ -767,7 +776,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             // shared gate/up (weights prefetched), while routing runs
             float hsh[1];
             gu_compute<1>(S, S.shw[wid - W_SH], hsh);
-            if (lane == 0) cstore(hcur + GR * g + (wid - W_SH), hsh[0]);
+            if (lane == 0) cstore(hcur + XREC * g + (wid - W_SH), hsh[0]);
         }
         if (wid >= W_DN) {
             // routed down bands; chunk ch (16 B) of band slot ch / 210 lands
@@ -807,17 +816,21 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             if (extra) predecode_to_lds(S, wid - W_GU + NWV, xw);
         }
 
-        // ---- P5: every slot's h into LDS, polled
+        // ---- P5: every slot's h into LDS, polled: chunk c = (workgroup w,
+        // q): float4 q of w's record holds slots 2q and 2q+1 (rows 2w, 2w+1)
         if (!lds_get(&S.abort)) {
-            const auto hr = rsrc(hcur, (uint32_t)(NH * 4));
+            const int NQ = (K + 2) >> 1;  // float4 chunks in use per record
+            const auto hr = rsrc(hcur, G * XREC * 4);
             bool ok = true;
-            for (int ch = tid; ch < NH / 4; ch += NT) {
+            for (int c = tid; c < G * NQ; c += NT) {
+                const int w = c / NQ, q = c - w * NQ;
+                const bool hi = 2 * q + 1 <= K;
                 float4 v;
-                ok = ok && poll4(sy, hr, 16u * (uint32_t)ch, v);
-                *reinterpret_cast<float4 *>(&S.h[4 * ch]) = v;
+                ok = ok && poll4(sy, hr, 4u * (uint32_t)(XREC * w + 4 * q), v, hi);
+                *reinterpret_cast<float2 *>(&S.h[2 * q * DI + GR * w]) = make_float2(v.x, v.y);
+                if (hi) *reinterpret_cast<float2 *>(&S.h[(2 * q + 1) * DI + GR * w]) = make_float2(v.z, v.w);
             }
             if (!ok) S.abort = 1;
-
         }
         __syncthreads();
         if (S.abort) break;
@@ -848,7 +861,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
 #pragma unroll
             for (int k = 0; k < MAXK; k++)
                 if (k < K) v += wt[k] * d[k + 1];
-            if (l + 1 < a.L) cstore(xout + OR * g + lane, v);
+            if (l + 1 < a.L) cstore(xout + XREC * g + lane, v);
             a.hidden[OR * g + lane] = v;
             if (lane == 0) trace_here(a, l, TP_OUT);
         }
@@ -987,9 +1000,9 @@ int bread_launch_decode_layers(bread_moe_ctx_t *c, const bread_moe_layer_t *laye
 // Exchange buffers start out "unwritten" (sentinel everywhere).
 int bread_decode_reset(bread_moe_ctx_t *c)
 {
-    BREAD_HIP(hipMemsetD32((hipDeviceptr_t)c->xbuf, (int)SENTINEL, 2 * DH));
-    BREAD_HIP(hipMemsetD32((hipDeviceptr_t)c->hbuf, (int)SENTINEL, 3 * NSLOT * DI));
-    BREAD_HIP(hipMemset(c->tlogits, 0, 256 * sizeof(uint64_t)));
+    BREAD_HIP(hipMemsetD32((hipDeviceptr_t)c->xbuf, (int)SENTINEL, bread_decode_xbuf_floats()));
+    BREAD_HIP(hipMemsetD32((hipDeviceptr_t)c->hbuf, (int)SENTINEL, bread_decode_hbuf_floats()));
+    BREAD_HIP(hipMemset(c->tlogits, 0, bread_decode_tlogit_words() * sizeof(uint64_t)));
     BREAD_HIP(hipMemset(c->dsync, 0, sizeof(bread_decode_sync)));
     c->epoch = 0;
     c->hphase = 0;
@@ -998,12 +1011,17 @@ int bread_decode_reset(bread_moe_ctx_t *c)
 
 size_t bread_decode_xbuf_floats()
 {
-    return 2 * DH;
+    return 2 * G * XREC;
+}
+
+size_t bread_decode_tlogit_words()
+{
+    return 256 * LG_STRIDE;
 }
 
 size_t bread_decode_hbuf_floats()
 {
-    return 3 * NSLOT * DI;
+    return 3 * G * XREC;
 }
 
 size_t bread_decode_layer_record_bytes()

@@ -347,3 +347,83 @@ def test_decode_layers_stack_matches_oracle():
         assert_moe_close(ho.cpu().numpy(), ref1)
     assert ctx.check_device() == 0
     arena.close()
+
+
+def _tie_router(s, t, x, groups):
+    """Router with all rows zero except `groups`: (scale, [experts]) rows set
+    to scale * x / |x| (identical rows give bit-identical logits)."""
+    router = torch.zeros(s.n_experts, s.hidden, device=DEV)
+    base = torch.from_numpy(x / np.linalg.norm(x)).to(DEV)
+    for scale, experts in groups:
+        for e in experts:
+            router[e] = scale * base
+    return api.LayerTensors(s, t.gate_exps, t.up_exps, t.down_exps, t.gate_sh, t.up_sh, t.down_sh,
+                            router.contiguous().view(-1), t.shgate)
+
+
+def _oracle_route_only(s, lt, x):
+    hl = O.HostLayer(O.OShape(s.hidden, s.expert_inter, s.shared_inter, s.n_experts, s.top_k),
+                     np.zeros(1, np.uint8), np.zeros(1, np.uint8), np.zeros(1, np.uint8), np.zeros(1, np.uint8),
+                     np.zeros(1, np.uint8), np.zeros(1, np.uint8), lt.router.cpu().numpy(),
+                     lt.shgate.cpu().numpy().view(np.uint16))
+    return O.route(hl, x)
+
+
+def test_decode_routing_ties(full_layer):
+    """The decode kernel's own selection: ties inside the top-8 and a five-way
+    tie across the rank-8 boundary go to the lower indices, in rank order."""
+    s, t, _ = full_layer
+    x = xs(1, s.hidden, 21)[0]
+    lt = _tie_router(s, t, x, [(3.0, [200, 7]), (1.5, [150, 3]), (1.0, [250, 31, 90, 17, 5])])
+    ctx = B.MoeContext(s, max_tokens=1)
+    h = torch.zeros(1, s.hidden, device=DEV)
+    idx, w, _ = ctx.forward(lt.desc(), dev(x[None]), h, 1, want_routing=True)
+    torch.cuda.synchronize()
+    got = list(idx.cpu().numpy()[0])
+    assert got == [7, 200, 3, 150, 5, 17, 31, 90]
+    ri, rw, _ = _oracle_route_only(s, lt, x)
+    assert got == list(ri)
+    np.testing.assert_allclose(w.cpu().numpy()[0], rw, rtol=2e-5, atol=1e-7)
+    assert ctx.check_device() == 0
+
+
+def test_decode_routing_nan_rule(full_layer):
+    """A NaN input makes every probability NaN: indices 0..K-1 in order."""
+    s, t, hl = full_layer
+    x = xs(1, s.hidden, 22)
+    x[0, 11] = np.nan
+    ctx = B.MoeContext(s, max_tokens=1)
+    h = torch.zeros(1, s.hidden, device=DEV)
+    idx, w, _ = ctx.forward(t.desc(), dev(x), h, 1, want_routing=True)
+    torch.cuda.synchronize()
+    ri, _, _ = O.route(hl, x[0])
+    assert list(idx.cpu().numpy()[0]) == list(ri) == list(range(s.top_k))
+    assert np.all(np.isnan(w.cpu().numpy()))
+    # the context keeps working after a NaN token
+    h2 = torch.zeros(1, s.hidden, device=DEV)
+    x2 = xs(1, s.hidden, 23)
+    idx2, _, _ = ctx.forward(t.desc(), dev(x2), h2, 1, want_routing=True)
+    torch.cuda.synchronize()
+    ref = np.zeros((1, s.hidden), np.float32)
+    ri2, _, _ = O.moe_forward(hl, x2, ref, 1, nthreads=8)
+    assert np.array_equal(idx2.cpu().numpy(), ri2)
+    assert_moe_close(h2.cpu().numpy(), ref)
+    assert ctx.check_device() == 0
+
+
+@pytest.mark.parametrize("E,K", [(16, 1), (16, 2), (256, 3), (40, 8)])
+def test_decode_small_k_matches_oracle(E, K):
+    """The decode kernel at H 2048 / I 512 with other expert counts and K."""
+    s = api.shape(n_experts=E, top_k=K)
+    t = api.synth_layer_tensors(s, seed=E * 10 + K)
+    hl = host_layer(t)
+    ctx = B.MoeContext(s, max_tokens=1)
+    for seed in range(3):
+        x = xs(1, s.hidden, 700 + seed)
+        hidden = xs(1, s.hidden, 800 + seed)
+        got, gi, gw, _ = run_forward(ctx, t, x, hidden)
+        ref, ri, rw, _ = oracle_forward(hl, x, hidden)
+        assert np.array_equal(gi, ri)
+        np.testing.assert_allclose(gw, rw, rtol=2e-5, atol=1e-7)
+        assert_moe_close(got, ref, base=hidden)
+    assert ctx.check_device() == 0
