@@ -87,7 +87,9 @@ constexpr int W_SH = 9;                  // waves 9, 10: shared gate/up
 constexpr int W_DN = 9;                  // waves 9..15: routed down bands
 constexpr int N_DN = NWV - W_DN;         // 7
 constexpr int DN_LOADS = (MAXK * BAND16 + N_DN * WAVE - 1) / (N_DN * WAVE);  // 4
-constexpr int W_PF = 4;                  // waves 4..15 prefetch the next layer's fixed weights
+constexpr int W_PF = 12;                 // waves 12..15 prefetch routing-independent weights, never poll
+constexpr int N_XPOLL = 8;               // waves 0..7 poll the previous layer's output, 4 columns a thread
+constexpr int N_HPOLL = W_PF;            // waves 0..11 poll the SwiGLU outputs
 constexpr uint32_t SPIN_LIMIT = 1u << 18;
 constexpr uint32_t BUF_WORD3 = 0x00020000u;  // raw buffer descriptor word 3 (gfx9)
 constexpr int AUX_COHERENT = 16;             // sc1: device-coherent access
@@ -102,8 +104,9 @@ constexpr int XREC = 32;                 // floats per workgroup record (128 B):
 static_assert(DH % G == 0 && DI % G == 0 && GR == 2 && OR == 8, "row ownership assumes 256 workgroups");
 static_assert(NBH == 8 && DI / QK == 2, "lane layouts assume H = 2048 and I = 512");
 static_assert(BAND % 16 == 0, "down bands are loaded in 16-byte chunks");
-static_assert(NPOLL * WAVE == 256 && 2 * NT == DH, "pollers: one logit a lane; two columns a thread");
+static_assert(NPOLL * WAVE == 256 && 4 * N_XPOLL * WAVE == DH, "pollers: one logit a lane; four columns a thread");
 static_assert(W_GU + MAXK == W_SH && W_SH + 2 <= NWV, "wave roles");
+static_assert(G * ((MAXK + 2) / 2) <= 2 * N_HPOLL * WAVE, "h poll: at most two chunks a thread");
 
 // Trace points recorded per (workgroup, layer) when a trace buffer is given.
 enum {
@@ -117,8 +120,8 @@ enum {
     TP_COMB = 7,    // down dots of every wave done (after the barrier)
     TP_HREADY = 8,  // every h seen
     TP_OUT = 9,     // output rows stored
-    TP_CYC0 = 10,   // core clock (s_memtime) at TP_POLLED
-    TP_CYC1 = 11,   // core clock at TP_ROUTED
+    TP_HLAST = 10,  // the last routed slot's gate/up wave stored its h
+    TP_DNIN = 11,   // every routed down band in LDS (seen by wave 0)
     TP_N = 12
 };
 
@@ -155,7 +158,8 @@ struct Smem {
     float x[DH];                       // normalised input of the layer
     float nw[DH];                      // RMSNorm weights (prefetched)
     float h[NSLOT * DI];               // SwiGLU outputs of every slot
-    uint32_t down[NSLOT * BAND / 4];   // down bands: slot 0 prefetched, 1..K after routing
+    uint32_t down[MAXK * BAND / 4];    // routed down bands, slot k at (k - 1) * BAND
+    uint32_t sdown[2][BAND / 4];       // shared down band, by layer parity (prefetched a layer ahead)
     float wrow[DH];                    // router row g (prefetched)
     uint16_t shg[DH];                  // shared-expert gate vector (prefetched)
     uint4 shw[2][4][WAVE];             // shared gate/up rows: [row][hg, qg, hu, qu][lane] (prefetched)
@@ -172,6 +176,7 @@ struct Smem {
     int nready;                        // ranks published in idx
     int lgcnt;                         // polling waves done with the logits
     int dncnt;                         // down waves whose bands are in LDS
+    int gucnt;                         // routed gate/up waves whose weights are in LDS
     int abort;                         // a wait failed: the workgroup leaves
 };
 // more than half of a CU's 160 KB, so the dispatcher puts one workgroup per CU
@@ -477,18 +482,19 @@ __device__ __forceinline__ uint32_t lds16_a2(const uint32_t *base, uint32_t off)
 //
 // Pre-decode: w[8s + k] = (d * sc) * (q - 32), the dequantised weight
 // (dequant_q4k_cpu.c:155-170, same rounding order).
-__device__ __forceinline__ void down_predecode(const Smem &S, int u, float (&w)[32])
+__device__ __forceinline__ void down_predecode(const Smem &S, int u, int sb, float (&w)[32])
 {
     const int lane = opaque(lane_id());
     const int slot = u >> 1;
     const int row = 4 * (u & 1) + (lane >> 4);
     const int b = (lane >> 3) & 1, n = (lane >> 2) & 1, t = lane & 3;
-    const uint32_t ob = (uint32_t)(slot * BAND + row * DN_ROW + b * Q6K_BYTES);
-    const uint2 ql0 = lds8_a2(S.down, ob + 64 * n + 8 * t);
-    const uint2 ql1 = lds8_a2(S.down, ob + 64 * n + 32 + 8 * t);
-    const uint2 qh = lds8_a2(S.down, ob + 128 + 32 * n + 8 * t);
-    const uint2 scw = lds8_a2(S.down, ob + 192 + 8 * n);
-    const float d = h2f(lds16_a2(S.down, ob + 208));
+    const uint32_t *band = slot == 0 ? S.sdown[sb] : S.down + (slot - 1) * (BAND / 4);
+    const uint32_t ob = (uint32_t)(row * DN_ROW + b * Q6K_BYTES);
+    const uint2 ql0 = lds8_a2(band, ob + 64 * n + 8 * t);
+    const uint2 ql1 = lds8_a2(band, ob + 64 * n + 32 + 8 * t);
+    const uint2 qh = lds8_a2(band, ob + 128 + 32 * n + 8 * t);
+    const uint2 scw = lds8_a2(band, ob + 192 + 8 * n);
+    const float d = h2f(lds16_a2(band, ob + 208));
     const uint32_t i2 = (uint32_t)t >> 1;
 #pragma unroll
     for (int half = 0; half < 2; half++) {
@@ -506,10 +512,10 @@ __device__ __forceinline__ void down_predecode(const Smem &S, int u, float (&w)[
 // Down units beyond the 16 waves (u >= 16, only for K = 8) are pre-decoded by
 // waves 1 and 2 into their own gate/up staging slot of LDS, free once their
 // gate/up is done: element 8s + k of lane i at float4 [2s + k/4][i].
-__device__ __forceinline__ void predecode_to_lds(const Smem &S, int u, float4 (*dst)[WAVE])
+__device__ __forceinline__ void predecode_to_lds(const Smem &S, int u, int sb, float4 (*dst)[WAVE])
 {
     float w[32];
-    down_predecode(S, u, w);
+    down_predecode(S, u, sb, w);
     const int lane = opaque(lane_id());
 #pragma unroll
     for (int q = 0; q < 8; q++) dst[q][lane] = make_float4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
@@ -560,30 +566,31 @@ __device__ __forceinline__ void down_dot_lds(Smem &S, int u, const float4 (*src)
 
 // ---------------------------------------------------------------- fixed weights
 
-// Routing-independent weights of a layer into LDS, by waves 4..15: router
-// row g and norm weights (waves 4..11), shared-gate vector, shared gate/up
-// rows and shared down band (waves 12..15).
-__device__ __forceinline__ void prefetch_fixed(Smem &S, const DecLayer &Ly, int g, int E, int wid)
+// Routing-independent weights of a layer into LDS, by waves 12..15 (256
+// lanes, 8 direct-to-LDS loads each): router row g, norm weights, shared-gate
+// vector, shared gate/up rows and the shared down band (into sdown[sb]).
+// These waves never poll, so the loads delay no exchange (gfx9 completes a
+// wave's loads in order).
+__device__ __forceinline__ void prefetch(Smem &S, const DecLayer &Ly, int g, int E, int wid, int sb)
 {
     const int lane = opaque(lane_id());
     if (wid < W_PF) return;
-    if (wid < W_PF + 8) {
-        const int c = WAVE * (wid - W_PF) + lane;  // 16-byte chunk of a 2048-float row
-        if (g < E) lds_load16(Ly.router + (size_t)g * DH + 4 * c, &S.wrow[4 * WAVE * (wid - W_PF)]);
-        if (Ly.norm_w) lds_load16(Ly.norm_w + 4 * c, &S.nw[4 * WAVE * (wid - W_PF)]);
-    } else {
-        const int w4 = wid - (W_PF + 8);  // 0..3
-        if (Ly.shg) lds_load16(Ly.shg + 8 * (WAVE * w4 + lane), &S.shg[8 * WAVE * w4]);
-        // shared gate/up: wave w4 loads row w4/2, gate (w4 even) or up
-        const int r = GR * g + (w4 >> 1);
-        const uint8_t *base = ((w4 & 1) ? Ly.up_sh : Ly.gate_sh) + (size_t)r * GU_ROW;
-        const uint32_t oh = (uint32_t)((lane >> 3) * Q4K_BYTES);
-        const uint32_t oq = oh + 16u + 16u * (uint32_t)(lane & 7);
-        lds_load16(base + oh, &S.shw[w4 >> 1][2 * (w4 & 1)][0]);
-        lds_load16(base + oq, &S.shw[w4 >> 1][2 * (w4 & 1) + 1][0]);
-        const int c = WAVE * w4 + lane;  // shared down band chunk
-        if (c < BAND16) lds_load16(Ly.down_sh + (size_t)g * BAND + 16 * c, &S.down[4 * WAVE * w4]);
+    const int w4 = wid - W_PF;           // 0..3
+    const int c = WAVE * w4 + lane;      // 0..255
+#pragma unroll
+    for (int i = 0; i < 2; i++) {        // 16-byte chunk c + 256 i of a 2048-float row
+        if (g < E) lds_load16(Ly.router + (size_t)g * DH + 4 * (c + 256 * i), &S.wrow[4 * (WAVE * w4 + 256 * i)]);
+        if (Ly.norm_w) lds_load16(Ly.norm_w + 4 * (c + 256 * i), &S.nw[4 * (WAVE * w4 + 256 * i)]);
     }
+    if (Ly.shg) lds_load16(Ly.shg + 8 * c, &S.shg[8 * WAVE * w4]);
+    // shared gate/up: wave w4 loads row w4/2, gate (w4 even) or up
+    const int r = GR * g + (w4 >> 1);
+    const uint8_t *base = ((w4 & 1) ? Ly.up_sh : Ly.gate_sh) + (size_t)r * GU_ROW;
+    const uint32_t oh = (uint32_t)((lane >> 3) * Q4K_BYTES);
+    const uint32_t oq = oh + 16u + 16u * (uint32_t)(lane & 7);
+    lds_load16(base + oh, &S.shw[w4 >> 1][2 * (w4 & 1)][0]);
+    lds_load16(base + oq, &S.shw[w4 >> 1][2 * (w4 & 1) + 1][0]);
+    if (c < BAND16) lds_load16(Ly.down_sh + (size_t)g * BAND + 16 * c, &S.sdown[sb][4 * WAVE * w4]);
 }
 
 // ---------------------------------------------------------------- kernel
@@ -599,7 +606,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
     bread_decode_sync *sy = a.sync;
     const float sent = __builtin_bit_cast(float, SENTINEL);
     if (tid == 0) S.abort = 0;
-    prefetch_fixed(S, load_layer(a, 0), g, E, wid);
+    prefetch(S, load_layer(a, 0), g, E, wid, 0);
     __syncthreads();
 
     for (int l = 0; l < a.L; l++) {
@@ -616,7 +623,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
         trace_point(a, l, TP_START);
 
         // ---- P1: h of the layer (caller's buffer for the first layer, else
-        // the previous layer's output, polled), thread t: columns 2t, 2t+1
+        // the previous layer's output, polled) by waves 0..7, thread t:
+        // columns 4t .. 4t+3
         if (wid == 0) {
             // re-arm this workgroup's rows of this layer's output buffer and
             // its record of the next layer's h buffer
@@ -626,44 +634,47 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                 S.nready = 0;
                 S.lgcnt = 0;
                 S.dncnt = 0;
+                S.gucnt = 0;
             }
         }
-        float2 hv;
-        {
+        float4 hv = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (wid < N_XPOLL) {
             bool ok = true;
-            const bool own = (tid >> 2) == g;  // threads 4g..4g+3 hold rows 8g..8g+7
+            const bool own = (tid >> 1) == g;  // threads 2g, 2g+1 hold rows 8g..8g+7
             if (l == 0) {
                 const float *src = a.x0 ? a.x0 : a.hidden;
-                hv = *reinterpret_cast<const float2 *>(src + 2 * tid);
-                if (own && a.x0) {
-                    const float2 o = *reinterpret_cast<const float2 *>(a.hidden + 2 * tid);
-                    *reinterpret_cast<float2 *>(&S.hown[2 * (tid & 3)]) = o;
-                }
+                hv = *reinterpret_cast<const float4 *>(src + 4 * tid);
+                if (own && a.x0)
+                    *reinterpret_cast<float4 *>(&S.hown[4 * (tid & 1)]) =
+                        *reinterpret_cast<const float4 *>(a.hidden + 4 * tid);
             } else {
                 const auto r = rsrc(a.xbuf + (par ^ 1) * (G * XREC), G * XREC * 4);
-                ok = poll2(sy, r, 4u * (uint32_t)(XREC * (tid >> 2) + 2 * (tid & 3)), hv);
+                ok = poll4(sy, r, 4u * (uint32_t)(XREC * (tid >> 1) + 4 * (tid & 1)), hv);
             }
-            if (own && !(l == 0 && a.x0)) *reinterpret_cast<float2 *>(&S.hown[2 * (tid & 3)]) = hv;
-            const float ss = wave_sum(fmaf(hv.x, hv.x, hv.y * hv.y));
+            if (own && !(l == 0 && a.x0)) *reinterpret_cast<float4 *>(&S.hown[4 * (tid & 1)]) = hv;
+            const float ss = wave_sum(fmaf(hv.x, hv.x, fmaf(hv.y, hv.y, fmaf(hv.z, hv.z, hv.w * hv.w))));
             if (lane == 0) S.red[wid] = ss;
             if (!ok) S.abort = 1;
-            __builtin_amdgcn_s_waitcnt(0);  // this wave's prefetched weights have landed too
+        } else if (wid >= W_PF) {
+            __builtin_amdgcn_s_waitcnt(0);  // the layer's prefetched weights have landed
         }
         __syncthreads();
         if (S.abort) break;
-        if (!(l == 0 && a.x0)) {
-            float ss = 0.f;
+        if (wid < N_XPOLL) {
+            if (!(l == 0 && a.x0)) {
+                float ss = 0.f;
 #pragma unroll
-            for (int w = 0; w < NWV; w++) ss += S.red[w];
-            const float inv = 1.0f / sqrtf(ss / (float)DH + a.eps);  // layer_ops.cu:209
-            if (Ly.norm_w) {
-                const float2 nw = *reinterpret_cast<const float2 *>(&S.nw[2 * tid]);
-                hv = make_float2(hv.x * inv * nw.x, hv.y * inv * nw.y);
-            } else {
-                hv = make_float2(hv.x * inv, hv.y * inv);
+                for (int w = 0; w < N_XPOLL; w++) ss += S.red[w];
+                const float inv = 1.0f / sqrtf(ss / (float)DH + a.eps);  // layer_ops.cu:209
+                if (Ly.norm_w) {
+                    const float4 nw = *reinterpret_cast<const float4 *>(&S.nw[4 * tid]);
+                    hv = make_float4(hv.x * inv * nw.x, hv.y * inv * nw.y, hv.z * inv * nw.z, hv.w * inv * nw.w);
+                } else {
+                    hv = make_float4(hv.x * inv, hv.y * inv, hv.z * inv, hv.w * inv);
+                }
             }
+            *reinterpret_cast<float4 *>(&S.x[4 * tid]) = hv;
         }
-        *reinterpret_cast<float2 *>(&S.x[2 * tid]) = hv;
         __syncthreads();
         trace_point(a, l, TP_XREADY);
 
@@ -717,7 +728,6 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                 __builtin_amdgcn_s_setprio(3);
                 if (lds_wait(S, &S.lgcnt, NPOLL)) {
                     trace_point(a, l, TP_POLLED);
-                    if (a.trace && tid == 0) a.trace[((size_t)blockIdx.x * a.L + l) * TP_N + TP_CYC0] = __builtin_amdgcn_s_memtime();
                     float p[4];
 #pragma unroll
                     for (int vv = 0; vv < 4; vv++) p[vv] = S.lg[lane + WAVE * vv];
@@ -750,7 +760,6 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                         if (a.gsh_out && lane == 0) a.gsh_out[l] = gsh;
                     }
                     trace_point(a, l, TP_ROUTED);
-                    if (a.trace && tid == 0) a.trace[((size_t)blockIdx.x * a.L + l) * TP_N + TP_CYC1] = __builtin_amdgcn_s_memtime();
                 } else if (lane == 0) {
                     lds_put(&S.abort, 1);
                 }
@@ -765,10 +774,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                 gu_issue<GR>(Ly.gate_exps + (uint64_t)e * Ly.gate_eb, Ly.up_exps + (uint64_t)e * Ly.up_eb, GR * g,
                              S.gu[slot - 1]);
                 __builtin_amdgcn_s_waitcnt(0);
+                if (lane == 0) lds_add(&S.gucnt, 1);
                 float hv[GR];
                 gu_compute<GR>(S, S.gu[slot - 1], hv);
                 if (lane == 0) {
                     cstore2(hcur + XREC * g + GR * slot, hv[0], hv[1]);
+                    if (slot == K) trace_here(a, l, TP_HLAST);
                 }
             }
         }
@@ -779,31 +790,33 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             if (lane == 0) cstore(hcur + XREC * g + (wid - W_SH), hsh[0]);
         }
         if (wid >= W_DN) {
-            // routed down bands; chunk ch (16 B) of band slot ch / 210 lands
+            // routed down bands; chunk ch (16 B) of slot ch / 210 + 1 lands
             // at byte 16 ch of S.down
-            const int nchunk = (K + 1) * BAND16;
-            const int c0 = BAND16 + WAVE * (wid - W_DN);
+            const int nchunk = K * BAND16;
+            const int c0 = WAVE * (wid - W_DN);
             const int ln = opaque(lane);
-            bool ok = true;
             // gate/up first: the down bands are not needed before the h
-            // exchange, so their loads wait until every rank's gate/up is issued
-            ok = lds_wait(S, &S.nready, K, true);
+            // exchange, so their loads wait until every rank's gate/up weights
+            // are in
+            bool ok = lds_wait(S, &S.nready, K, true) && lds_wait(S, &S.gucnt, K, true);
 #pragma unroll
             for (int i = 0; i < DN_LOADS; i++) {
                 const int cw = c0 + N_DN * WAVE * i;  // first chunk of this wave's load
-                if (cw >= nchunk) break;
-                const int shi = min((cw + WAVE - 1) / BAND16, K);
-                ok = ok && lds_wait(S, &S.nready, shi);
-                if (!ok) break;
+                if (!ok || cw >= nchunk) break;
                 const int ch = cw + ln;
                 if (ch < nchunk) {
-                    const int slot = ch / BAND16;
-                    const uint8_t *base = Ly.down_exps + (uint64_t)S.idx[slot - 1] * Ly.down_eb;
-                    lds_load16(base + (size_t)g * BAND + 16 * (ch - slot * BAND16), &S.down[4 * cw]);
+                    const int sl = ch / BAND16;  // slot - 1
+                    const uint8_t *base = Ly.down_exps + (uint64_t)S.idx[sl] * Ly.down_eb;
+                    lds_load16(base + (size_t)g * BAND + 16 * (ch - sl * BAND16), &S.down[4 * cw]);
                 }
             }
             __builtin_amdgcn_s_waitcnt(0);
             if (lane == 0) lds_add(&S.dncnt, 1);
+            // the next layer's routing-independent weights, now that this
+            // layer's are consumed (the shared gate/up was used before waves
+            // 9 and 10 loaded their bands)
+            if (wid >= W_PF && l + 1 < a.L && lds_wait(S, &S.dncnt, N_DN, true))
+                prefetch(S, load_layer(a, l + 1), g, E, wid, (l + 1) & 1);
         }
 
         // ---- P4: pre-decode this wave's down unit once every band is in
@@ -812,23 +825,50 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
         const bool extra = wid >= W_GU && wid < W_GU + 2 && wid - W_GU + NWV < NU;
         float4 (*xw)[WAVE] = reinterpret_cast<float4 (*)[WAVE]>(&S.gu[wid >= W_GU && wid < W_GU + 2 ? wid - W_GU : 0][0][0]);
         if (wid < NU && lds_wait(S, &S.dncnt, N_DN)) {
-            down_predecode(S, wid, w0);
-            if (extra) predecode_to_lds(S, wid - W_GU + NWV, xw);
+            if (tid == 0) trace_here(a, l, TP_DNIN);
+            down_predecode(S, wid, l & 1, w0);
+            if (extra) predecode_to_lds(S, wid - W_GU + NWV, l & 1, xw);
         }
 
         // ---- P5: every slot's h into LDS, polled: chunk c = (workgroup w,
         // q): float4 q of w's record holds slots 2q and 2q+1 (rows 2w, 2w+1)
-        if (!lds_get(&S.abort)) {
+        if (wid < N_HPOLL && !lds_get(&S.abort)) {
             const int NQ = (K + 2) >> 1;  // float4 chunks in use per record
             const auto hr = rsrc(hcur, G * XREC * 4);
             bool ok = true;
-            for (int c = tid; c < G * NQ; c += NT) {
-                const int w = c / NQ, q = c - w * NQ;
-                const bool hi = 2 * q + 1 <= K;
-                float4 v;
-                ok = ok && poll4(sy, hr, 4u * (uint32_t)(XREC * w + 4 * q), v, hi);
-                *reinterpret_cast<float2 *>(&S.h[2 * q * DI + GR * w]) = make_float2(v.x, v.y);
-                if (hi) *reinterpret_cast<float2 *>(&S.h[(2 * q + 1) * DI + GR * w]) = make_float2(v.z, v.w);
+            // up to two chunks a thread, polled together
+            const int c0 = tid, c1 = tid + N_HPOLL * WAVE;
+            const bool two = c1 < G * NQ;
+            const int w0 = c0 / NQ, q0 = c0 - w0 * NQ, w1 = c1 / NQ, q1 = c1 - w1 * NQ;
+            const bool hi0 = 2 * q0 + 1 <= K, hi1 = 2 * q1 + 1 <= K;
+            float4 v0, v1;
+            bool r0 = !(c0 < G * NQ), r1 = !two;
+            for (uint32_t it = 0; it < SPIN_LIMIT && !(r0 && r1); it++) {
+                if (!r0) {
+                    v0 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        hr, (int)(4 * (XREC * w0 + 4 * q0)), 0, AUX_COHERENT));
+                    r0 = !unwritten(v0.x) && !unwritten(v0.y) && !(hi0 && (unwritten(v0.z) || unwritten(v0.w)));
+                }
+                if (!r1) {
+                    v1 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        hr, (int)(4 * (XREC * w1 + 4 * q1)), 0, AUX_COHERENT));
+                    r1 = !unwritten(v1.x) && !unwritten(v1.y) && !(hi1 && (unwritten(v1.z) || unwritten(v1.w)));
+                }
+                if (r0 && r1) break;
+                if ((it & 63) == 63 && has_error(sy)) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+            if (!(r0 && r1)) {
+                if (!has_error(sy)) flag_error(sy, 1u);
+                ok = false;
+            }
+            if (c0 < G * NQ) {
+                *reinterpret_cast<float2 *>(&S.h[2 * q0 * DI + GR * w0]) = make_float2(v0.x, v0.y);
+                if (hi0) *reinterpret_cast<float2 *>(&S.h[(2 * q0 + 1) * DI + GR * w0]) = make_float2(v0.z, v0.w);
+            }
+            if (two) {
+                *reinterpret_cast<float2 *>(&S.h[2 * q1 * DI + GR * w1]) = make_float2(v1.x, v1.y);
+                if (hi1) *reinterpret_cast<float2 *>(&S.h[(2 * q1 + 1) * DI + GR * w1]) = make_float2(v1.z, v1.w);
             }
             if (!ok) S.abort = 1;
         }
@@ -849,7 +889,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
         // been consumed) by waves 4..15; combine in the reference order
         // (one_layer.cu:1443-1471) and publish the rows to the next layer and
         // the caller by wave 0
-        if (l + 1 < a.L) prefetch_fixed(S, load_layer(a, l + 1), g, E, wid);
+
         if (wid == 0 && lane < OR) {
             float d[NSLOT], wt[MAXK];
 #pragma unroll

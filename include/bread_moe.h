@@ -210,9 +210,9 @@ int bread_moe_decode_layers(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer
  * at d_buf[(workgroup * n_layers + layer) * 12 + point], points 0 layer
  * start, 1 input normalised, 2 own logit published, 3 every logit seen,
  * 4 rank-1 expert known, 5 routing done, 6 own down dots done, 7 every down
- * dot done, 8 every SwiGLU output seen, 9 output rows stored; 10 and 11 hold
- * the core clock (s_memtime) at points 3 and 5.  *grid_out receives the
- * launch's workgroup count.  NULL turns it off. */
+ * dot done, 8 every SwiGLU output seen, 9 output rows stored, 10 the last
+ * routed slot's SwiGLU outputs stored, 11 every routed down band loaded.
+ * *grid_out receives the launch's workgroup count.  NULL turns it off. */
 int bread_moe_ctx_set_trace(bread_moe_ctx_t *ctx, uint64_t *d_buf, size_t n_words, int *grid_out);
 
 /* out[t] = x[t] * (1/sqrt(mean(x[t]^2) + eps)) * w, fp32, n_tokens rows of n
