@@ -19,6 +19,10 @@ from ._lib import MoeLayer, MoeShape, check, lib
 QTYPE_Q8_0 = _lib.QTYPE_Q8_0
 QTYPE_Q4_K = _lib.QTYPE_Q4_K
 QTYPE_Q6_K = _lib.QTYPE_Q6_K
+PATH_AUTO = _lib.PATH_AUTO
+PATH_DECODE = _lib.PATH_DECODE
+PATH_GROUPED = _lib.PATH_GROUPED
+PATH_PER_TOKEN = _lib.PATH_PER_TOKEN
 
 
 def _p(t: torch.Tensor | None):
@@ -232,6 +236,10 @@ class MoeContext:
     @property
     def handle(self) -> ctypes.c_void_p:
         return self._h
+
+    def set_path(self, path: int) -> None:
+        """bread_moe_ctx_set_path: PATH_AUTO, PATH_DECODE, PATH_GROUPED or PATH_PER_TOKEN."""
+        check(lib.bread_moe_ctx_set_path(self._h, path), "bread_moe_ctx_set_path")
 
     def route(self, layer: MoeLayer, x: torch.Tensor, n_tokens: int, stream=None):
         K = self.shape.top_k

@@ -118,6 +118,24 @@ __device__ __forceinline__ uint32_t ld16_a2(const uint8_t *p)
     return (w >> (8u * (uint32_t)(a & 3u))) & 0xFFFFu;
 }
 
+// 8 bytes at a 2-byte aligned byte offset of a dword array (LDS), from
+// aligned dwords.
+__device__ __forceinline__ uint2 lds8_a2(const uint32_t *base, uint32_t off)
+{
+    const uint32_t a = off >> 2, sh = off & 3u;
+    const uint32_t w0 = base[a], w1 = base[a + 1], w2 = base[(off + 7) >> 2];
+    uint2 o;
+    o.x = __builtin_amdgcn_alignbyte(w1, w0, sh);
+    o.y = __builtin_amdgcn_alignbyte(w2, w1, sh);
+    return o;
+}
+
+// 16-bit value at a 2-byte aligned byte offset of a dword array (LDS).
+__device__ __forceinline__ uint32_t lds16_a2(const uint32_t *base, uint32_t off)
+{
+    return (base[off >> 2] >> (8u * (off & 3u))) & 0xFFFFu;
+}
+
 // ---------------------------------------------------------------------------
 // wave64 reductions (DPP inside 16-lane rows, cross-row by permute)
 // ---------------------------------------------------------------------------

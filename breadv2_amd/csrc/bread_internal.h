@@ -47,8 +47,20 @@ struct bread_decode_sync {
     bread_line error;  // non-zero: a bounded wait expired (sticky until checked)
 };
 
+// Workspace of the grouped (multi-token) path, sized for max_tokens.
+struct bread_grouped_ws {
+    void *xhi = nullptr, *xlo = nullptr;  // activations as hi/lo fp16 [max_tokens][H]
+    int *xexp = nullptr;                  // row scale exponents [max_tokens]
+    int *pair_tok = nullptr;              // token of each expert-sorted pair [max_tokens*(K+1)]
+    int *pos_of = nullptr;                // sorted position of pair (t, k) [max_tokens*K]
+    void *tiles = nullptr;                // M-tiles of the expert GEMMs
+    int *n_tiles = nullptr;
+    float *eo = nullptr;                  // expert outputs by pair [max_tokens*(K+1)][H]
+};
+
 struct bread_moe_ctx {
     bread_moe_shape_t shape;
+    int path;          // BREAD_PATH_*
     int max_tokens;
     int max_layers;
     int device;
@@ -71,6 +83,7 @@ struct bread_moe_ctx {
     int n_layers_uploaded;
     uint64_t *trace;   // optional decode timeline (device), trace_words entries
     size_t trace_words;
+    bread_grouped_ws gws;
 };
 
 struct bread_arena {
@@ -90,6 +103,12 @@ int bread_launch_route(bread_moe_ctx_t *ctx, const bread_moe_layer_t *L, const f
                        int n_tokens, int32_t *idx, float *w, float *gsh, hipStream_t st);
 int bread_launch_moe_multi(bread_moe_ctx_t *ctx, const bread_moe_layer_t *L, const float *x,
                            float *hidden, int n_tokens, hipStream_t st);
+int bread_launch_topk(const float *logits, int E, int K, int T, int32_t *idx, float *w, hipStream_t st);
+int bread_grouped_alloc(bread_moe_ctx_t *ctx);
+void bread_grouped_free(bread_moe_ctx_t *ctx);
+bool bread_grouped_supported(const bread_moe_shape_t &s, const bread_moe_layer_t *L);
+int bread_launch_moe_grouped(bread_moe_ctx_t *ctx, const bread_moe_layer_t *L, const float *x, float *hidden,
+                             int n_tokens, hipStream_t st);
 int bread_launch_moe_decode(bread_moe_ctx_t *ctx, const bread_moe_layer_t *L, const float *x,
                             float *hidden, hipStream_t st);
 int bread_launch_decode_layers(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layers, int n, float *hidden,

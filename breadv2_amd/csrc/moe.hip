@@ -11,6 +11,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <new>
+
 #include "bread_internal.h"
 #include "quant_dot.h"
 #include "route_dev.h"
@@ -115,7 +117,7 @@ extern "C" int bread_moe_ctx_create(const bread_moe_shape_t *shape, int max_toke
     if (rc) return rc;
     BREAD_REQUIRE(out && max_tokens > 0, BREAD_ERR_ARG, "out must be non-NULL and max_tokens > 0");
     *out = nullptr;
-    bread_moe_ctx_t *c = (bread_moe_ctx_t *)calloc(1, sizeof(bread_moe_ctx_t));
+    bread_moe_ctx_t *c = new (std::nothrow) bread_moe_ctx_t();
     BREAD_REQUIRE(c, BREAD_ERR_NOMEM, "host allocation");
     c->shape = *shape;
     c->max_tokens = max_tokens;
@@ -140,6 +142,10 @@ extern "C" int bread_moe_ctx_create(const bread_moe_shape_t *shape, int max_toke
         if (!c->h_layers) e = hipErrorOutOfMemory;
     }
     if (e == hipSuccess && bread_decode_max_blocks(&c->decode_max_blocks) != BREAD_OK) e = hipErrorUnknown;
+    if (e == hipSuccess) {
+        const int grc = bread_grouped_alloc(c);
+        if (grc != BREAD_OK) e = grc == BREAD_ERR_NOMEM ? hipErrorOutOfMemory : hipErrorUnknown;
+    }
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         bread_moe_ctx_destroy(c);
@@ -163,8 +169,9 @@ extern "C" int bread_moe_ctx_destroy(bread_moe_ctx_t *c)
     (void)hipFree(c->hbuf);
     (void)hipFree(c->dsync);
     (void)hipFree(c->d_layers);
+    bread_grouped_free(c);
     free(c->h_layers);
-    free(c);
+    delete c;
     return BREAD_OK;
 }
 
@@ -182,6 +189,14 @@ extern "C" int bread_moe_ctx_check(bread_moe_ctx_t *c, int *device_error)
         BREAD_HIP(hipDeviceSynchronize());
         return bread_fail(BREAD_ERR_DEVICE, "bread_moe_ctx_check", "a kernel flagged an error");
     }
+    return BREAD_OK;
+}
+
+extern "C" int bread_moe_ctx_set_path(bread_moe_ctx_t *c, int path)
+{
+    BREAD_REQUIRE(c, BREAD_ERR_ARG, "NULL context");
+    BREAD_REQUIRE(path >= BREAD_PATH_AUTO && path <= BREAD_PATH_PER_TOKEN, BREAD_ERR_ARG, "unknown path");
+    c->path = path;
     return BREAD_OK;
 }
 
@@ -311,7 +326,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, co
 // Launchers
 // ---------------------------------------------------------------------------
 
-static int launch_topk(const float *logits, int E, int K, int T, int32_t *idx, float *w, hipStream_t st)
+int bread_launch_topk(const float *logits, int E, int K, int T, int32_t *idx, float *w, hipStream_t st)
 {
     const int mv = (E + WAVE - 1) / WAVE;
     if (mv <= 4)
@@ -331,7 +346,7 @@ int bread_launch_route(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const flo
     hipLaunchKernelGGL(k_router, dim3((waves + 3) / 4), dim3(256), 0, st, L->router, L->shexp_gate, x, c->logits,
                        gsh, s.hidden, s.n_experts, T);
     BREAD_HIP(hipGetLastError());
-    return launch_topk(c->logits, s.n_experts, s.top_k, T, idx, w, st);
+    return bread_launch_topk(c->logits, s.n_experts, s.top_k, T, idx, w, st);
 }
 
 int bread_launch_moe_multi(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, float *hidden, int T,
@@ -401,8 +416,24 @@ extern "C" int bread_moe_forward(bread_moe_ctx_t *c, const bread_moe_layer_t *L,
     if (T == 0) return BREAD_OK;
     hipStream_t st = to_hip(stream);
     c->last_stream = st;
-    rc = (T == 1) ? bread_launch_moe_decode(c, L, x, hidden, st) : BREAD_ERR_SHAPE;
-    if (rc == BREAD_ERR_SHAPE) rc = bread_launch_moe_multi(c, L, x, hidden, T, st);
+    switch (c->path) {
+    case BREAD_PATH_DECODE:
+        BREAD_REQUIRE(T == 1, BREAD_ERR_SHAPE, "the decode path takes one token");
+        rc = bread_launch_moe_decode(c, L, x, hidden, st);
+        if (rc == BREAD_ERR_SHAPE) return bread_fail(rc, "bread_moe_forward", "shape not supported by the decode kernel");
+        break;
+    case BREAD_PATH_GROUPED:
+        rc = bread_launch_moe_grouped(c, L, x, hidden, T, st);
+        if (rc == BREAD_ERR_SHAPE) return bread_fail(rc, "bread_moe_forward", "shape not supported by the grouped path");
+        break;
+    case BREAD_PATH_PER_TOKEN:
+        rc = bread_launch_moe_multi(c, L, x, hidden, T, st);
+        break;
+    default:
+        rc = (T == 1) ? bread_launch_moe_decode(c, L, x, hidden, st) : BREAD_ERR_SHAPE;
+        if (rc == BREAD_ERR_SHAPE) rc = bread_launch_moe_grouped(c, L, x, hidden, T, st);
+        if (rc == BREAD_ERR_SHAPE) rc = bread_launch_moe_multi(c, L, x, hidden, T, st);
+    }
     if (rc) return rc;
     const int K = c->shape.top_k;
     if (idx) BREAD_HIP(hipMemcpyAsync(idx, c->idx, (size_t)T * K * sizeof(int32_t), hipMemcpyDeviceToDevice, st));

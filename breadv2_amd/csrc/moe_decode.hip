@@ -459,22 +459,6 @@ __device__ __forceinline__ void gu_compute(const Smem &S, const uint4 (*w)[WAVE]
 
 // ---------------------------------------------------------------- down
 
-// 8 bytes at a 2-byte aligned LDS byte offset, from aligned dwords.
-__device__ __forceinline__ uint2 lds8_a2(const uint32_t *base, uint32_t off)
-{
-    const uint32_t a = off >> 2, sh = off & 3u;
-    const uint32_t w0 = base[a], w1 = base[a + 1], w2 = base[(off + 7) >> 2];
-    uint2 o;
-    o.x = __builtin_amdgcn_alignbyte(w1, w0, sh);
-    o.y = __builtin_amdgcn_alignbyte(w2, w1, sh);
-    return o;
-}
-
-__device__ __forceinline__ uint32_t lds16_a2(const uint32_t *base, uint32_t off)
-{
-    return (base[off >> 2] >> (8u * (off & 3u))) & 0xFFFFu;
-}
-
 // Down unit u: slot u/2, rows 4*(u%2) .. +4 of the workgroup, 16 lanes a row;
 // a lane owns superblock b = (lane/8)%2, half n = (lane/4)%2 and l in
 // [8t, 8t+8), t = lane%4 (the Q6_K unit of quant_dot.h), i.e. the 32 weights

@@ -67,3 +67,18 @@ def normal_f32(n: int, seed: int, mean: float = 0.0, std: float = 1.0) -> np.nda
     """N(mean, std) via numpy's PCG64 (host-only inputs such as activations)."""
     rng = np.random.default_rng(seed)
     return (mean + std * rng.standard_normal(n)).astype(np.float32)
+
+
+def zipf_bias(n_experts: int, s: float, seed: int) -> np.ndarray:
+    """Router logit bias log p_rank(e) with p_r proportional to r**-s over a
+    seeded permutation of the experts (expert perm[r-1] has rank r).  The
+    bias enters through the router GEMV itself: the caller sets the last
+    activation feature of every token to 1 and the router's last column to
+    this bias, so logit_e = sum_{j<H-1} W[e][j] x[j] + bias_e."""
+    perm = np.random.default_rng(seed).permutation(n_experts)
+    r = np.arange(1, n_experts + 1, dtype=np.float64)
+    p = r ** -s
+    p /= p.sum()
+    bias = np.empty(n_experts, np.float64)
+    bias[perm] = np.log(p)
+    return bias.astype(np.float32)

@@ -149,6 +149,20 @@ int bread_moe_ctx_create(const bread_moe_shape_t *shape, int max_tokens,
                          bread_moe_ctx_t **out);
 int bread_moe_ctx_destroy(bread_moe_ctx_t *ctx);
 
+/* Which implementation bread_moe_forward runs.  AUTO picks by n_tokens and
+ * shape as described there; the others force one path and make
+ * bread_moe_forward return BREAD_ERR_SHAPE where it does not apply.  No
+ * counterpart in the reference (which has one path); for tests and
+ * benchmarks that compare the paths. */
+typedef enum {
+    BREAD_PATH_AUTO = 0,
+    BREAD_PATH_DECODE = 1,     /* persistent single-token kernel */
+    BREAD_PATH_GROUPED = 2,    /* expert-bucketed grouped GEMMs (MFMA) */
+    BREAD_PATH_PER_TOKEN = 3   /* one wave per (token, row) GEMV kernels */
+} bread_moe_path_t;
+
+int bread_moe_ctx_set_path(bread_moe_ctx_t *ctx, int path);
+
 /* Synchronises the context's last stream and returns BREAD_ERR_DEVICE (and
  * the kernel's error word in *device_error, if given) when a kernel flagged
  * a fault, e.g. a bounded wait that expired.  Clears the word. */
@@ -178,9 +192,12 @@ int bread_route_layer(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer, cons
  * reference order (shared first, then routed experts by rank).
  * d_x_normed fp32 [n_tokens][H] (the post-attention RMSNorm output),
  * d_hidden fp32 [n_tokens][H] in/out.  Optional outputs d_idx/d_w/d_gsh as in
- * bread_route (may be NULL).  n_tokens == 1 runs the persistent decode
- * kernel when the shape allows it (see bread_moe_decode_layers); other
- * shapes and larger batches run the multi-token path. */
+ * bread_route (may be NULL).  Path (bread_moe_ctx_set_path, default
+ * BREAD_PATH_AUTO): n_tokens == 1 runs the persistent decode kernel when the
+ * shape allows it (see bread_moe_decode_layers); larger batches run the
+ * grouped path (tokens bucketed by expert, expert GEMMs on the matrix cores
+ * with fp16 operands and fp32 accumulation; intermediate sizes <= 512 and
+ * 16-byte aligned Q6_K down weights); other shapes run the per-token path. */
 int bread_moe_forward(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer,
                       const float *d_x_normed, float *d_hidden, int n_tokens,
                       int32_t *d_idx, float *d_w, float *d_gsh, bread_stream_t stream);

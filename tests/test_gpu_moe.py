@@ -180,24 +180,35 @@ def test_decode_back_to_back_launches(full_layer):
 
 
 def test_decode_vs_multi_kernel_path(full_layer):
-    """The single-launch kernel and the multi-kernel path agree."""
+    """The single-launch kernel and the per-token kernels (both fp32) agree
+    to fp32 reordering; the grouped path (fp16 operands) to the layer
+    tolerance."""
     s, t, _ = full_layer
     ctx = B.MoeContext(s, max_tokens=2)
     x = xs(1, s.hidden, 8)
     h1 = torch.zeros(1, s.hidden, device=DEV)
     ctx.forward(t.desc(), dev(x), h1, 1)
+    ctx.set_path(api.PATH_PER_TOKEN)
     h2 = torch.zeros(2, s.hidden, device=DEV)
     ctx.forward(t.desc(), dev(np.repeat(x, 2, 0)), h2, 2)
+    ctx.set_path(api.PATH_GROUPED)
+    h3 = torch.zeros(2, s.hidden, device=DEV)
+    ctx.forward(t.desc(), dev(np.repeat(x, 2, 0)), h3, 2)
     torch.cuda.synchronize()
-    a, b = h1.cpu().numpy()[0], h2.cpu().numpy()
+    a, b, c = h1.cpu().numpy()[0], h2.cpu().numpy(), h3.cpu().numpy()
     assert np.array_equal(b[0], b[1])
     assert rel_l2(a, b[0]) < 1e-5
+    assert np.array_equal(c[0], c[1])
+    assert_moe_close(c[0], a)
 
 
+@pytest.mark.parametrize("path", [api.PATH_AUTO, api.PATH_PER_TOKEN])
 @pytest.mark.parametrize("T", [2, 8, 16])
-def test_multi_token_matches_oracle(full_layer, T):
+def test_multi_token_matches_oracle(full_layer, T, path):
+    """AUTO runs the grouped path at these sizes; PER_TOKEN the GEMV kernels."""
     s, t, hl = full_layer
     ctx = B.MoeContext(s, max_tokens=T)
+    ctx.set_path(path)
     x = xs(T, s.hidden, 300 + T)
     hidden = xs(T, s.hidden, 400 + T)
     got, gi, gw, _ = run_forward(ctx, t, x, hidden)
