@@ -35,6 +35,23 @@ def _s(stream) -> ctypes.c_void_p:
     return ctypes.c_void_p(stream.cuda_stream)
 
 
+_HIP = None
+
+
+def device_copy(dst: int, src: int, nbytes: int) -> None:
+    """Synchronous device-to-device copy between raw device pointers (HIP
+    runtime of the process, which torch has loaded)."""
+    global _HIP
+    if _HIP is None:
+        _HIP = ctypes.CDLL("libamdhip64.so")
+        _HIP.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        _HIP.hipMemcpy.restype = ctypes.c_int
+    torch.cuda.synchronize()
+    rc = _HIP.hipMemcpy(dst, src, nbytes, 3)  # hipMemcpyDeviceToDevice
+    if rc != 0:
+        raise RuntimeError(f"hipMemcpy failed: {rc}")
+
+
 def row_bytes(qtype: int, cols: int) -> int:
     if qtype == QTYPE_Q4_K:
         return cols // 256 * 144
@@ -211,6 +228,16 @@ class Arena:
               "bread_synth_normal_f32")
         check(lib.bread_synth_normal_f16(ctypes.c_void_p(d.shexp_gate), s.hidden, sd["shgate"], 0.0, shgate_std, st),
               "bread_synth_normal_f16")
+
+    def set_router_column(self, l: int, col: int, values) -> None:
+        """Overwrite column col of layer l's fp32 router [E][H] with values[E]
+        (e.g. a routing bias carried by a constant activation feature)."""
+        d = self.layer(l)
+        E, H = self.shape.n_experts, self.shape.hidden
+        r = torch.empty(E * H, dtype=torch.float32, device=torch.device("cuda", torch.cuda.current_device()))
+        device_copy(r.data_ptr(), d.router, E * H * 4)
+        r.view(E, H)[:, col] = torch.as_tensor(values, dtype=torch.float32).to(r.device)
+        device_copy(d.router, r.data_ptr(), E * H * 4)
 
     def close(self) -> None:
         if self._h:

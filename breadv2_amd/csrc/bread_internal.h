@@ -56,6 +56,8 @@ struct bread_grouped_ws {
     void *tiles = nullptr;                // M-tiles of the expert GEMMs
     int *n_tiles = nullptr;
     float *eo = nullptr;                  // expert outputs by pair [max_tokens*(K+1)][H]
+    void *hhi = nullptr, *hlo = nullptr;  // SwiGLU outputs as hi/lo fp16 by pair [max_tokens*(K+1)][Imax]
+    int *hexp = nullptr;                  // their row scale exponents [max_tokens*(K+1)]
 };
 
 struct bread_moe_ctx {

@@ -24,16 +24,23 @@
 // (Q4_K, dequant_q4k_cpu.c:117-118) or d * sc * (q - 32) (Q6_K, c = -1056 *
 // d * sc, dequant_q4k_cpu.c:160-165).
 //
+// Expert GEMMs use v_mfma_f32_32x32x16_f16 with the weights as the M side
+// (32 rows) and the M-tile's 32 (token, expert) pairs as the N side: each
+// dequantised weight fragment meets 32 tokens in one instruction, and each
+// activation fragment read from LDS serves 32 weight rows.
+//
 // Kernels per layer, stream-ordered:
 //   k_mt_xprep    one workgroup per token: row scale, hi/lo fp16 activations
 //                 in the gate/up operand order, shared-gate logit
 //   k_mt_router   router logits on fp32 MFMA (16 tokens x 16 experts per
-//                 workgroup, K split over 4 waves)
+//                 workgroup, K split over 16 waves)
 //   k_topk        softmax / top-k / renormalisation (moe.hip, route_dev.h)
 //   k_mt_bucket   one workgroup: expert histogram, token lists by expert,
-//                 M-tiles of 16 (token, expert) pairs
+//                 M-tiles of 32 pairs
 //   k_mt_gateup   per (M-tile, 128 rows): gate and up GEMMs, SwiGLU
-//   k_mt_down     per (M-tile, 256 rows): down GEMM
+//   k_mt_hprep    one wave per pair: row scale, hi/lo fp16 in the down
+//                 operand order
+//   k_mt_down     per (M-tile, 512 rows): down GEMM
 //   k_mt_combine  per token: shared expert, then routed experts in rank order
 // The shared expert is expert index E with every token, so both GEMMs treat
 // it like a routed expert with its own weights.
@@ -47,18 +54,19 @@
 
 namespace {
 
-constexpr int MT = 16;                           // (token, expert) pairs per M-tile
-constexpr int GU_WAVES = 4, GU_CB = 2;           // 16-row column blocks of gate (and up) per wave
-constexpr int GU_ROWS = GU_WAVES * GU_CB * 16;   // gate rows per gate/up workgroup
-constexpr int DN_WAVES = 8, DN_CB = 2;
-constexpr int DN_ROWS = DN_WAVES * DN_CB * 16;   // output rows per down workgroup
+constexpr int MT = 32;                           // (token, expert) pairs per M-tile
+constexpr int GU_WAVES = 8;                      // one 32-row gate or up block per wave
+constexpr int GU_ROWS = GU_WAVES / 2 * 32;       // SwiGLU rows per gate/up workgroup
+constexpr int DN_WAVES = 8, DN_BLOCKS = 2;       // 32-row down blocks per wave
+constexpr int DN_ROWS = DN_WAVES * DN_BLOCKS * 32;  // output rows per down workgroup
+constexpr int RT_WAVES = 16;                     // router K split
 constexpr int MAX_INTER = 512;                   // largest intermediate size the LDS plan holds
-constexpr int DN_BAND = 16 * (MAX_INTER / QK) * Q6K_BYTES;  // bytes of 16 down rows
 constexpr uint32_t MAGIC = 0x64646464u;          // fp16 0x64xx = 1024 + xx
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 struct MtTile {
     int e;   // expert (E = the shared expert)
@@ -67,15 +75,22 @@ struct MtTile {
     int pad;
 };
 
+// Device error word bit: a weight superblock whose dequantised values do
+// not fit fp16 (the grouped path's MFMA operand type).
+constexpr uint32_t DEV_ERR_RANGE = 4u;
+
 struct MtArgs {
     bread_moe_layer_t L;
+    uint32_t *err;           // device error word of the context
     int H, I, Ish, Imax, E, K, T;
     const uint4 *xhi, *xlo;  // [T][H/8] units of 8 fp16, gate/up operand order
     const int *xexp;         // [T] row scale exponents
     const int *pair_tok;     // [T*K + T] token of each sorted pair
     const MtTile *tiles;
     const int *n_tiles;
-    float *hbuf;             // [T*K + T][Imax] SwiGLU outputs by pair
+    float *h;                // [T*K + T][Imax] SwiGLU outputs by pair
+    const uint4 *hhi, *hlo;  // the same as hi/lo fp16 units in the down operand order
+    const int *hexp;         // [T*K + T] their row scale exponents
     float *eo;               // [T*K + T][H] expert outputs by pair
 };
 
@@ -87,6 +102,15 @@ __device__ __forceinline__ void lds_load16(const void *src, void *lds_wave_base)
 __device__ __forceinline__ uint32_t comp(const uint4 &q, int i)
 {
     return i == 0 ? q.x : (i == 1 ? q.y : (i == 2 ? q.z : q.w));
+}
+
+// s_waitcnt with vmcnt <= n (n < 16) and the other counters unconstrained
+// (gfx9 encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 16, "vmcnt");
+    __builtin_amdgcn_s_waitcnt(N | (7 << 4) | (15 << 8));
 }
 
 // Exponent e with max_abs * 2^-e in [2^13, 2^14); 0 for an all-zero or
@@ -136,46 +160,106 @@ __device__ __forceinline__ void bytes_to_w(uint32_t v, float d, float c, uint32_
     r1 = mix2(__builtin_amdgcn_perm(MAGIC, v, 0x07030702u), d, c);
 }
 
-__device__ __forceinline__ f32x4 mfma16(const uint4 &a, const uint4 &b, f32x4 acc)
+// D[32 weight rows][32 pairs] += W[32][16] * X[16][32].  Lane l holds W row
+// l%32 and X column l%32, K elements 8*(l/32) .. +7 of the step; D register
+// i holds row 8*(i/4) + 4*(l/32) + i%4 of column l%32.
+__device__ __forceinline__ f32x16 mfma32(const uint4 &w, const uint4 &x, f32x16 acc)
 {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), acc,
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, w), __builtin_bit_cast(half8, x), acc,
                                                   0, 0, 0);
 }
 
 // ---------------------------------------------------------------------------
-// Gate/up operand order (Q4_K).  Lane group g = lane/16 of a 16-row column
-// block reads qs bytes [32g, 32g+32) of each superblock row, i.e. sub-blocks
-// 2g (low nibbles) and 2g+1 (high nibbles).  K-step s (0..7) of a superblock
-// uses qs dword s of that range: B element j of the lane is superblock
-// element 64g + 4s + j (j < 4) or 64g + 32 + 4s + (j - 4) (j >= 4).  The
-// activations are stored in the same order: unit u = 32*sb + 4*s + g of a
-// token row holds those 8 elements.
+// Gate/up operand order (Q4_K).  Lane (row r = lane%32, group g = lane/32) of
+// a 32-row block reads qs bytes [64g, 64g+64) of each superblock row, i.e.
+// sub-block pairs p = 2g and 2g+1.  K-step s (0..15) of a superblock uses qs
+// dword s%8 of pair p = 2g + s/8: B element j of the lane is superblock
+// element 64p + 4(s%8) + j (j < 4, low nibbles, sub-block 2p) or
+// 64p + 32 + 4(s%8) + (j - 4) (j >= 4, high nibbles, sub-block 2p + 1).
+// The activations are stored in the same order: unit u = 32*sb + 2*s + g of
+// a token row holds those 8 elements.
 // ---------------------------------------------------------------------------
 
-struct Q4Sc {
-    float da, ca, db, cb;
+// Packed-fp16 form of the same weights, two per instruction:
+//   t = fma(1024 + q, sc, -1024 sc) = sc * q   (exact: |sc q| <= 945)
+//   w = fma(t, d, fp16(-dmin * m))             (one rounding, as above, plus
+//                                               the fp16 rounding of dmin * m)
+// Valid while d * 945 and dmin * 63 stay inside fp16's range (|d| < 64,
+// |dmin| < 1024), which fp16 weights need anyway; superblocks outside it
+// raise DEV_ERR_RANGE.
+struct Q4Pk {
+    half2v sc[4], nsc[4], m[4], d;
 };
 
-__device__ __forceinline__ Q4Sc q4k_lane_scales(const uint4 &hd, uint32_t g)
+__device__ __forceinline__ Q4Pk q4k_lane_pk(const uint4 &hd, uint32_t g)
 {
-    uint32_t sc0, m0, sc1, m1;
-    scale_min_k4(2 * g, hd.y, hd.z, hd.w, sc0, m0);
-    scale_min_k4(2 * g + 1, hd.y, hd.z, hd.w, sc1, m1);
-    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-    Q4Sc s;
-    s.da = d * (float)sc0;
-    s.ca = fmaf(-1024.f, s.da, -(dmin * (float)m0));
-    s.db = d * (float)sc1;
-    s.cb = fmaf(-1024.f, s.db, -(dmin * (float)m1));
+    Q4Pk s;
+    const float dmin = h2f(hd.x >> 16);
+    const _Float16 d16 = __builtin_bit_cast(_Float16, (uint16_t)(hd.x & 0xFFFFu));
+    s.d = half2v{d16, d16};
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        uint32_t sc, m;
+        scale_min_k4(4 * g + q, hd.y, hd.z, hd.w, sc, m);
+        const _Float16 scf = (_Float16)(float)sc, nscf = (_Float16)(-1024.f * (float)sc);
+        const _Float16 mf = (_Float16)(-(dmin * (float)m));
+        s.sc[q] = half2v{scf, scf};
+        s.nsc[q] = half2v{nscf, nscf};
+        s.m[q] = half2v{mf, mf};
+    }
     return s;
 }
 
-__device__ __forceinline__ uint4 q4k_frag(uint32_t v, const Q4Sc &s)
+__device__ __forceinline__ uint32_t pk_w(uint32_t qb, const Q4Pk &s, int q)
 {
-    uint4 r;
-    bytes_to_w(v & 0x0F0F0F0Fu, s.da, s.ca, r.x, r.y);
-    bytes_to_w((v >> 4) & 0x0F0F0F0Fu, s.db, s.cb, r.z, r.w);
-    return r;
+    const half2v t = __builtin_elementwise_fma(__builtin_bit_cast(half2v, qb), s.sc[q], s.nsc[q]);
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(t, s.d, s.m[q]));
+}
+
+__device__ __forceinline__ bool q4k_pk_ok(const uint4 &hd)
+{
+    const float d = fabsf(h2f(hd.x)), dmin = fabsf(h2f(hd.x >> 16));
+    return d < 64.f && dmin < 1024.f;  // false for NaN
+}
+
+// ---------------------------------------------------------------------------
+// Down operand order (Q6_K).  Lane (row r, group g) of a 32-row block takes
+// half g (elements 128g .. 128g+127) of each superblock row; K-step t (0..15)
+// of the half covers its elements 8t .. 8t+7 (natural order): low nibbles
+// of ql bytes 8t.. (t < 8) or high nibbles of ql bytes 8(t-8).. (t >= 8),
+// with qh bits 2*(t/4) of qh bytes 8(t%4).. and scale sc[8g + t/2]
+// (dequant_q4k_cpu.c:155-170).  Activation unit ((16b + t)*2 + g) of a row
+// holds elements 256b + 128g + 8t .. +7.
+//
+// The lane's bytes are 2-byte aligned (superblocks are 210 bytes), so each
+// range is loaded as whole dwords from the aligned-down address and shifted
+// with v_alignbyte.  Every dword loaded holds a byte of the superblock or of
+// the next one in the same expert block (an expert block ends 16-byte
+// aligned, so a superblock starting at a multiple of 4 is never its last).
+// ---------------------------------------------------------------------------
+
+struct Q6Raw {
+    uint4 ql[4];
+    uint32_t ql4;
+    uint4 qh[2];
+    uint32_t qh2;
+    uint4 sc;
+    uint32_t sc1;
+};
+
+__device__ __forceinline__ void q6k_load(const uint8_t *sb, int g, Q6Raw &R)
+{
+    const uintptr_t base = reinterpret_cast<uintptr_t>(sb) & ~(uintptr_t)3;
+    const uint8_t *p = reinterpret_cast<const uint8_t *>(base);
+    const uint8_t *ql = p + 64 * g, *qh = p + 128 + 32 * g, *sc = p + 192;
+#pragma unroll
+    for (int i = 0; i < 4; i++) R.ql[i] = *reinterpret_cast<const uint4 *>(ql + 16 * i);
+    R.ql4 = *reinterpret_cast<const uint32_t *>(ql + 64);
+    R.qh[0] = *reinterpret_cast<const uint4 *>(qh);
+    R.qh[1] = *reinterpret_cast<const uint4 *>(qh + 16);
+    R.qh2 = *reinterpret_cast<const uint32_t *>(qh + 32);
+    R.sc = *reinterpret_cast<const uint4 *>(sc);
+    R.sc1 = *reinterpret_cast<const uint32_t *>(sc + 16);
 }
 
 // ---------------------------------------------------------------------------
@@ -215,8 +299,8 @@ __global__ __launch_bounds__(256) void k_mt_xprep(const float *__restrict__ x, c
     }
     const int nu = H / 8;
     for (int u = threadIdx.x; u < nu; u += 256) {
-        const int sb = u >> 5, s = (u >> 2) & 7, g = u & 3;
-        const int b = QK * sb + 64 * g + 4 * s;
+        const int sb = u >> 5, s = (u >> 1) & 15, g = u & 1;
+        const int b = QK * sb + 64 * (2 * g + (s >> 3)) + 4 * (s & 7);
         const float4 lo4 = *reinterpret_cast<const float4 *>(xt + b);
         const float4 hi4 = *reinterpret_cast<const float4 *>(xt + b + 32);
         const float v[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
@@ -228,31 +312,45 @@ __global__ __launch_bounds__(256) void k_mt_xprep(const float *__restrict__ x, c
 }
 
 // logits[t][e] = router row e . x[t] (one_layer.cu:964-971), fp32 products
-// and sums.  Wave w covers K range [w*H/4, (w+1)*H/4); lane (r, g) feeds
-// token t0 + r and expert e0 + r, 4 consecutive K each step.
-__global__ __launch_bounds__(256) void k_mt_router(const float *__restrict__ router, const float *__restrict__ x,
-                                                   float *__restrict__ logits, int H, int E, int T)
+// and sums.  Wave w covers K range [w*H/16, (w+1)*H/16); lane (r, g) feeds
+// token t0 + r and expert e0 + r, 4 consecutive K each 16-element chunk;
+// all of a wave's loads are issued before its MFMAs.  The 16 partial tiles
+// are summed in wave order.
+__global__ __launch_bounds__(RT_WAVES * WAVE) void k_mt_router(const float *__restrict__ router,
+                                                               const float *__restrict__ x,
+                                                               float *__restrict__ logits, int H, int E, int T)
 {
-    __shared__ f32x4 part[3][WAVE];
+    __shared__ f32x4 part[RT_WAVES][WAVE];
     const int w = wave_id(), lane = lane_id();
     const int r = lane & 15, g = lane >> 4;
     const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
-    const float *xr = x + (size_t)min(t0 + r, T - 1) * H;
-    const float *wr = router + (size_t)min(e0 + r, E - 1) * H;
-    const int kq = H / 4;
+    const int kq = H / RT_WAVES, nch = kq / 16;
+    const float *xr = x + (size_t)min(t0 + r, T - 1) * H + w * kq + 4 * g;
+    const float *wr = router + (size_t)min(e0 + r, E - 1) * H + w * kq + 4 * g;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int k = w * kq + 4 * g; k < (w + 1) * kq; k += 16) {
-        const float4 a = *reinterpret_cast<const float4 *>(xr + k);
-        const float4 b = *reinterpret_cast<const float4 *>(wr + k);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc, 0, 0, 0);
+    for (int c0 = 0; c0 < nch; c0 += 8) {
+        float4 a[8], b[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (c0 + u < nch) {
+                a[u] = *reinterpret_cast<const float4 *>(xr + 16 * (c0 + u));
+                b[u] = *reinterpret_cast<const float4 *>(wr + 16 * (c0 + u));
+            }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (c0 + u < nch) {
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].x, b[u].x, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].y, b[u].y, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].z, b[u].z, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].w, b[u].w, acc, 0, 0, 0);
+            }
     }
-    if (w > 0) part[w - 1][lane] = acc;
+    part[w][lane] = acc;
     __syncthreads();
     if (w != 0) return;
-    const f32x4 s = ((acc + part[0][lane]) + part[1][lane]) + part[2][lane];
+    f32x4 s = part[0][lane];
+#pragma unroll
+    for (int i = 1; i < RT_WAVES; i++) s += part[i][lane];
     const int e = e0 + r;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -340,16 +438,19 @@ __global__ __launch_bounds__(1024) void k_mt_bucket(const int32_t *__restrict__ 
 }
 
 // ---------------------------------------------------------------------------
-// Gate/up: tile (M-tile, 128 gate rows).  Wave w owns gate and up rows
-// n0 + 32w + [0, 32) as two 16-row column blocks each; the tile's 16
-// activation rows are staged per superblock in LDS (LDS-direct loads,
-// double-buffered) and shared by the 4 waves; each wave dequantises its own
-// weights in registers, prefetching the next superblock.
+// Gate/up: tile (M-tile, 128 rows).  Waves 0..3 own gate rows n0 + 32w +
+// [0, 32), waves 4..7 the same rows of up, one 32-row block per wave.  The
+// tile's 32 activation rows are staged per superblock (32 KB, hi and lo) in
+// two LDS buffers by LDS-direct loads one superblock ahead; each wave loads
+// its raw weight bytes one superblock ahead into registers and dequantises
+// them there.  One barrier per superblock; two workgroups (16 waves) per CU.
+// At the end the up waves pass their results through LDS to the gate waves
+// (same lane layout), which apply the SwiGLU (layer_ops.cu:214-220).
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(256, 2) void k_mt_gateup(const MtArgs a)
+__global__ __launch_bounds__(GU_WAVES * WAVE, 2) void k_mt_gateup(const MtArgs a)
 {
-    __shared__ uint4 sA[2][2][512];  // [buffer][hi, lo][unit (s, g, m)]
+    __shared__ uint4 sA[2][2][1024];  // [buffer][hi, lo][unit (s, g, n)]
     __shared__ int stok[MT], sexp[MT];
     const int tile = blockIdx.x;
     if (tile >= *a.n_tiles) return;
@@ -359,7 +460,9 @@ __global__ __launch_bounds__(256, 2) void k_mt_gateup(const MtArgs a)
     const int n0 = blockIdx.y * GU_ROWS;
     if (n0 >= I) return;
     const int tid = threadIdx.x, w = wave_id(), lane = lane_id();
-    const int g = lane >> 4, n = lane & 15;
+    const bool up = w >= GU_WAVES / 2;
+    const int wr = up ? w - GU_WAVES / 2 : w;
+    const int g = lane >> 5, r = lane & 31;
     if (tid < MT) {
         const int tok = a.pair_tok[tl.p0 + min(tid, tl.nr - 1)];
         stok[tid] = tok;
@@ -369,104 +472,156 @@ __global__ __launch_bounds__(256, 2) void k_mt_gateup(const MtArgs a)
 
     const int HU = a.H / 8, nsb = a.H / QK;
     const uint64_t rb = (uint64_t)nsb * Q4K_BYTES;
-    const uint8_t *gb = sh ? (const uint8_t *)a.L.gate_shexp
-                           : (const uint8_t *)a.L.gate_exps + (uint64_t)tl.e * a.L.gate_expert_bytes;
-    const uint8_t *ub = sh ? (const uint8_t *)a.L.up_shexp
-                           : (const uint8_t *)a.L.up_exps + (uint64_t)tl.e * a.L.up_expert_bytes;
-    const uint8_t *rows[4];  // gate block 0, gate block 1, up block 0, up block 1
-#pragma unroll
-    for (int c = 0; c < 4; c++)
-        rows[c] = (c < 2 ? gb : ub) + (uint64_t)(n0 + 16 * (GU_CB * w + (c & 1)) + n) * rb;
-    const uint4 *ahi = a.xhi + (size_t)stok[n] * HU + 4 * w + g;
-    const uint4 *alo = a.xlo + (size_t)stok[n] * HU + 4 * w + g;
+    const uint8_t *base = up ? (sh ? (const uint8_t *)a.L.up_shexp
+                                   : (const uint8_t *)a.L.up_exps + (uint64_t)tl.e * a.L.up_expert_bytes)
+                             : (sh ? (const uint8_t *)a.L.gate_shexp
+                                   : (const uint8_t *)a.L.gate_exps + (uint64_t)tl.e * a.L.gate_expert_bytes);
+    const int row0 = n0 + 32 * wr;
+    const uint8_t *wrow = base + (uint64_t)(row0 + r) * rb;
+    // unit (s, g, n) of a buffer: lane (n = r, g) of wave w stages s = w + 8i
+    const uint4 *ahi = a.xhi + (size_t)stok[r] * HU + 2 * w + g;
+    const uint4 *alo = a.xlo + (size_t)stok[r] * HU + 2 * w + g;
 
-    // unit (s, g, m) of buffer: lane (m = n, g) of wave w loads s = w and w + 4
-    auto stage = [&](int sb, int buf) {
-        lds_load16(ahi + 32 * sb, &sA[buf][0][64 * w]);
-        lds_load16(ahi + 32 * sb + 16, &sA[buf][0][64 * w + 256]);
-        lds_load16(alo + 32 * sb, &sA[buf][1][64 * w]);
-        lds_load16(alo + 32 * sb + 16, &sA[buf][1][64 * w + 256]);
-    };
-    auto load_b = [&](int sb, uint4 (&B)[4][3]) {
+    auto stage = [&](int sb, int st) {
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const uint8_t *p = rows[c] + (uint64_t)sb * Q4K_BYTES;
-            B[c][0] = ld_b128(p);
-            B[c][1] = ld_b128(p + 16 + 32 * g);
-            B[c][2] = ld_b128(p + 32 + 32 * g);
+        for (int i = 0; i < 16 / GU_WAVES; i++) {
+            lds_load16(ahi + 32 * sb + 2 * GU_WAVES * i, &sA[st][0][64 * (w + GU_WAVES * i)]);
+            lds_load16(alo + 32 * sb + 2 * GU_WAVES * i, &sA[st][1][64 * (w + GU_WAVES * i)]);
         }
     };
-    f32x4 acc[4];
+    auto load_b = [&](int sb, uint4 (&B)[5]) {
+        const uint8_t *p = wrow + (uint64_t)sb * Q4K_BYTES;
+        B[0] = ld_b128(p);
 #pragma unroll
-    for (int c = 0; c < 4; c++) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-    auto compute = [&](int buf, const uint4 (&B)[4][3]) {
-        Q4Sc sc[4];
+        for (int i = 0; i < 4; i++) B[1 + i] = ld_b128(p + 16 + 64 * g + 16 * i);
+    };
+    f32x16 acc;
 #pragma unroll
-        for (int c = 0; c < 4; c++) sc[c] = q4k_lane_scales(B[c][0], (uint32_t)g);
+    for (int i = 0; i < 16; i++) acc[i] = 0.f;
+    // K-step s: activation fragments one step ahead of their MFMAs; the
+    // weight fragment from qs dword s%8 of pair 2g + s/8
+    auto ksteps = [&](int st, const uint4 (&B)[5], auto &&frag) {
+        uint4 xa[2][2];
+        xa[0][0] = sA[st][0][lane];
+        xa[0][1] = sA[st][1][lane];
 #pragma unroll
-        for (int s = 0; s < 8; s++) {
-            const uint4 xh = sA[buf][0][(4 * s + g) * 16 + n];
-            const uint4 xl = sA[buf][1][(4 * s + g) * 16 + n];
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const uint4 bw = q4k_frag(comp(B[c][1 + (s >> 2)], s & 3), sc[c]);
-                acc[c] = mfma16(xh, bw, acc[c]);
-                acc[c] = mfma16(xl, bw, acc[c]);
+        for (int s = 0; s < 16; s++) {
+            if (s + 1 < 16) {
+                xa[(s + 1) & 1][0] = sA[st][0][64 * (s + 1) + lane];
+                xa[(s + 1) & 1][1] = sA[st][1][64 * (s + 1) + lane];
             }
+            __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of this step's work
+            const int pp = s >> 3, ds = s & 7;
+            const uint4 bw = frag(comp(B[1 + 2 * pp + (ds >> 2)], ds & 3), 2 * pp);
+            acc = mfma32(bw, xa[s & 1][0], acc);
+            acc = mfma32(bw, xa[s & 1][1], acc);
         }
     };
+    auto compute = [&](int st, const uint4 (&B)[5]) {
+        if (__builtin_amdgcn_ballot_w64(!q4k_pk_ok(B[0])) != 0 && lane == 0)
+            __hip_atomic_fetch_or(a.err, DEV_ERR_RANGE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const Q4Pk pk = q4k_lane_pk(B[0], (uint32_t)g);
+        ksteps(st, B, [&](uint32_t v, int q) {
+            const uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+            uint4 r;
+            r.x = pk_w(__builtin_amdgcn_perm(MAGIC, lo, 0x07010700u), pk, q);
+            r.y = pk_w(__builtin_amdgcn_perm(MAGIC, lo, 0x07030702u), pk, q);
+            r.z = pk_w(__builtin_amdgcn_perm(MAGIC, hi, 0x07010700u), pk, q + 1);
+            r.w = pk_w(__builtin_amdgcn_perm(MAGIC, hi, 0x07030702u), pk, q + 1);
+            return r;
+        });
+    };
 
-    uint4 B0[4][3], B1[4][3];
-    stage(0, 0);
+    // Iteration k: wait for weights and activations of k (issued in
+    // iteration k-1), barrier (everyone is done with buffer (k+1)%2), issue
+    // k+1, compute k.
+    uint4 B0[5], B1[5];
     load_b(0, B0);
+    stage(0, 0);
     for (int sb = 0; sb < nsb; sb += 2) {
-        // superblock sb from buffer 0 / B0
-        __builtin_amdgcn_s_waitcnt(0);
+        wait_vmcnt<0>();
         __syncthreads();
         if (sb + 1 < nsb) {
-            stage(sb + 1, 1);
             load_b(sb + 1, B1);
+            stage(sb + 1, 1);
         }
         compute(0, B0);
         if (sb + 1 >= nsb) break;
-        // superblock sb + 1 from buffer 1 / B1
-        __builtin_amdgcn_s_waitcnt(0);
+        wait_vmcnt<0>();
         __syncthreads();
         if (sb + 2 < nsb) {
-            stage(sb + 2, 0);
             load_b(sb + 2, B0);
+            stage(sb + 2, 0);
         }
         compute(1, B1);
     }
 
-    float *hrow = a.hbuf + n0 + 16 * GU_CB * w + n;
+    const int e = sexp[r];
+    float *xch = reinterpret_cast<float *>(&sA[0][0][0]);  // [wave 0..3][16][64] up results
+    __syncthreads();
+    if (up) {
 #pragma unroll
-    for (int cb = 0; cb < GU_CB; cb++)
+        for (int i = 0; i < 16; i++) xch[(wr * 16 + i) * WAVE + lane] = ldexpf(acc[i], e);
+    }
+    __syncthreads();
+    if (!up && r < tl.nr) {
+        float *hp = a.h + (size_t)(tl.p0 + r) * a.Imax + row0 + 4 * g;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = 4 * g + i;
-            if (m < tl.nr) {
-                const float gv = ldexpf(acc[cb][i], sexp[m]);
-                const float uv = ldexpf(acc[2 + cb][i], sexp[m]);
-                hrow[(size_t)(tl.p0 + m) * a.Imax + 16 * cb] = silu_mul(gv, uv);
-            }
+        for (int j = 0; j < 4; j++) {
+            float4 o;
+            o.x = silu_mul(ldexpf(acc[4 * j + 0], e), xch[(wr * 16 + 4 * j + 0) * WAVE + lane]);
+            o.y = silu_mul(ldexpf(acc[4 * j + 1], e), xch[(wr * 16 + 4 * j + 1) * WAVE + lane]);
+            o.z = silu_mul(ldexpf(acc[4 * j + 2], e), xch[(wr * 16 + 4 * j + 2) * WAVE + lane]);
+            o.w = silu_mul(ldexpf(acc[4 * j + 3], e), xch[(wr * 16 + 4 * j + 3) * WAVE + lane]);
+            *reinterpret_cast<float4 *>(hp + 8 * j) = o;
         }
+    }
+}
+
+// One wave per pair row p (rows T*K .. T*K+T-1 are the shared expert's):
+// the SwiGLU row scaled by a power of two and split into hi/lo fp16, unit
+// ((16b + t)*2 + g) of the row holding elements 256b + 128g + 8t .. +7.
+__global__ __launch_bounds__(256) void k_mt_hprep(const float *__restrict__ h, int n_rows, int n_routed, int I,
+                                                  int Ish, int Imax, uint4 *__restrict__ hhi,
+                                                  uint4 *__restrict__ hlo, int *__restrict__ hexp)
+{
+    const int p = blockIdx.x * 4 + (int)(threadIdx.x / WAVE);
+    if (p >= n_rows) return;
+    const int lane = lane_id();
+    const int n = (p < n_routed ? I : Ish) / 8;
+    const float *hr = h + (size_t)p * Imax;
+    float mx = 0.f;
+    for (int v = lane; v < n; v += WAVE) {
+        const float4 a = *reinterpret_cast<const float4 *>(hr + 8 * v);
+        const float4 b = *reinterpret_cast<const float4 *>(hr + 8 * v + 4);
+        mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                             fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
+    }
+    const int e = row_exp(wave_max(mx));
+    if (lane == 0) hexp[p] = e;
+    for (int v = lane; v < n; v += WAVE) {
+        const float4 a = *reinterpret_cast<const float4 *>(hr + 8 * v);
+        const float4 b = *reinterpret_cast<const float4 *>(hr + 8 * v + 4);
+        const float x8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        uint4 hi, lo;
+        split8(x8, e, hi, lo);
+        const int u = (16 * (v >> 5) + (v & 15)) * 2 + ((v >> 4) & 1);
+        hhi[(size_t)p * (Imax / 8) + u] = hi;
+        hlo[(size_t)p * (Imax / 8) + u] = lo;
+    }
 }
 
 // ---------------------------------------------------------------------------
-// Down: tile (M-tile, 256 output rows).  Wave w owns rows n0 + 32w + [0, 32)
-// as two 16-row column blocks, each a contiguous band of the expert's Q6_K
-// rows staged in LDS (16-byte aligned: 16 rows are 16 * 210 * I/256 bytes);
-// the tile's SwiGLU rows are scaled, split and staged once for all waves.
-// Operand order: K-step s covers elements [32s, 32s + 32) and lane group g
-// elements 32s + 8g + [0, 8) (natural order), from the ql/qh bytes of
-// quant_dot.h's Q6_K lane unit.
+// Down: tile (M-tile, 512 output rows).  Wave w owns rows n0 + 64w + [0, 64)
+// as two 32-row blocks.  The tile's SwiGLU rows, already split by
+// k_mt_hprep, are staged once by LDS-direct loads (hi and lo fp16, 64 KB for
+// I = 512); each wave walks its (block, superblock) items loading the next
+// item's raw Q6_K bytes into registers while dequantising the current one.
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(512, 1) void k_mt_down(const MtArgs a)
+__global__ __launch_bounds__(DN_WAVES * WAVE, 2) void k_mt_down(const MtArgs a)
 {
-    __shared__ uint4 sA[2][(MAX_INTER / 32) * 64];   // [hi, lo][unit (s, g, m)]
-    __shared__ uint32_t sB[DN_WAVES][DN_CB][DN_BAND / 4];
+    __shared__ uint4 sA[2][(MAX_INTER / 8) * MT];  // [hi, lo][unit ((16b + t)*2 + g)*32 + n]
     __shared__ int sexp[MT];
     const int tile = blockIdx.x;
     if (tile >= *a.n_tiles) return;
@@ -475,97 +630,121 @@ __global__ __launch_bounds__(512, 1) void k_mt_down(const MtArgs a)
     const int I = sh ? a.Ish : a.I;
     const int n0 = blockIdx.y * DN_ROWS;
     const int tid = threadIdx.x, w = wave_id(), lane = lane_id();
-    const int rbd = (I / QK) * Q6K_BYTES;
+    const int g = lane >> 5, r = lane & 31;
+    const int nb = I / QK;
+    const uint64_t rbd = (uint64_t)nb * Q6K_BYTES;
     const uint8_t *db = sh ? (const uint8_t *)a.L.down_shexp
                            : (const uint8_t *)a.L.down_exps + (uint64_t)tl.e * a.L.down_expert_bytes;
+    const int row0 = n0 + 32 * DN_BLOCKS * w;
+    const int nblk = max(0, min(DN_BLOCKS, (a.H - row0) / 32));
+    const int items = nblk * nb;
+    auto item_ptr = [&](int it) {
+        return db + (uint64_t)(row0 + 32 * (it / nb) + r) * rbd + (uint64_t)(it % nb) * Q6K_BYTES;
+    };
 
-    // weight bands first, so they load while the activations are prepared
-#pragma unroll
-    for (int cb = 0; cb < DN_CB; cb++) {
-        const uint8_t *band = db + (uint64_t)(n0 + 16 * (DN_CB * w + cb)) * rbd;
-        for (int k = 0; k < rbd; k += WAVE)
-            if (k + lane < rbd) lds_load16(band + 16 * (k + lane), &sB[w][cb][4 * k]);
-    }
+    Q6Raw R0, R1;
+    if (items > 0) q6k_load(item_ptr(0), g, R0);
 
     {
-        const int m = tid >> 5, seg = tid & 31;
-        const float *hr = a.hbuf + (size_t)(tl.p0 + min(m, tl.nr - 1)) * a.Imax;
-        const int per = I / 32;
-        float mx = 0.f;
-        for (int j = 0; j < per; j += 4) {
-            const float4 v = *reinterpret_cast<const float4 *>(hr + seg * per + j);
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        // the tile's activation units: LDS unit ((16b + t)*2 + g)*32 + n
+        // holds unit (16b + t)*2 + g of pair row p0 + n; wave w loads LDS
+        // units 64q + lane for q = w, w + DN_WAVES, ...
+        const int n = lane & 31, hu = a.Imax / 8;
+        const size_t prow = (size_t)(tl.p0 + min(n, tl.nr - 1)) * hu + (lane >> 5);
+        for (int q = w; q < I / 16; q += DN_WAVES) {
+            lds_load16(a.hhi + prow + 2 * q, &sA[0][64 * q]);
+            lds_load16(a.hlo + prow + 2 * q, &sA[1][64 * q]);
         }
-#pragma unroll
-        for (int o = 16; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-        const int e = row_exp(mx);
-        if (seg == 0) sexp[m] = e;
-        for (int j = 0; j < per; j += 8) {
-            const int k0 = seg * per + j;
-            const float4 p = *reinterpret_cast<const float4 *>(hr + k0);
-            const float4 q = *reinterpret_cast<const float4 *>(hr + k0 + 4);
-            const float v[8] = {p.x, p.y, p.z, p.w, q.x, q.y, q.z, q.w};
-            uint4 h, l;
-            split8(v, e, h, l);
-            const int unit = ((k0 >> 5) * 4 + ((k0 >> 3) & 3)) * 16 + m;
-            sA[0][unit] = h;
-            sA[1][unit] = l;
-        }
+        if (tid < MT) sexp[tid] = a.hexp[tl.p0 + min(tid, tl.nr - 1)];
     }
-    __builtin_amdgcn_s_waitcnt(0);
+    wait_vmcnt<0>();
     __syncthreads();
 
-    const int g = lane >> 4, n = lane & 15;
-    const uint32_t i2 = (uint32_t)g >> 1;
+    f32x16 acc;
 #pragma unroll
-    for (int cb = 0; cb < DN_CB; cb++) {
-        const uint32_t *band = sB[w][cb];
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int b = 0; b < I / QK; b++) {
-            const uint32_t o = (uint32_t)(n * rbd + b * Q6K_BYTES);
+    for (int i = 0; i < 16; i++) acc[i] = 0.f;
+    auto compute = [&](int it, const Q6Raw &R) {
+        const uint32_t sh8 = (uint32_t)(reinterpret_cast<uintptr_t>(item_ptr(it)) & 3u);
+        const uint32_t qw[17] = {R.ql[0].x, R.ql[0].y, R.ql[0].z, R.ql[0].w, R.ql[1].x, R.ql[1].y,
+                                 R.ql[1].z, R.ql[1].w, R.ql[2].x, R.ql[2].y, R.ql[2].z, R.ql[2].w,
+                                 R.ql[3].x, R.ql[3].y, R.ql[3].z, R.ql[3].w, R.ql4};
+        const uint32_t hw[9] = {R.qh[0].x, R.qh[0].y, R.qh[0].z, R.qh[0].w, R.qh[1].x,
+                                R.qh[1].y, R.qh[1].z, R.qh[1].w, R.qh2};
+        const uint32_t sw[5] = {R.sc.x, R.sc.y, R.sc.z, R.sc.w, R.sc1};
+        const uint32_t s0 = __builtin_amdgcn_alignbyte(sw[2 * g + 1], sw[2 * g], sh8);      // sc[8g .. 8g+3]
+        const uint32_t s1 = __builtin_amdgcn_alignbyte(sw[2 * g + 2], sw[2 * g + 1], sh8);  // sc[8g+4 .. 8g+7]
+        const float d = h2f(sw[4] >> (8 * sh8));
+        const int b = it % nb;
+        bool bad = false;  // |d sc| * 32 beyond fp16's range
+        // K-steps t and t + 8 use the same ql bytes (low and high nibbles)
+        // and the same qh bytes (bits 2(t/4) and 2(t/4) + 4)
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const uint2 ql0 = lds8_a2(band, o + 64 * h + 8 * g);
-                const uint2 ql1 = lds8_a2(band, o + 64 * h + 32 + 8 * g);
-                const uint2 qh = lds8_a2(band, o + 128 + 32 * h + 8 * g);
-                const uint2 scw = lds8_a2(band, o + 192 + 8 * h);
-                const float d = h2f(lds16_a2(band, o + 208));
-                uint32_t qa[4], qb[4];
-                q6k_unpack(ql0.x, ql1.x, qh.x, qa);
-                q6k_unpack(ql0.y, ql1.y, qh.y, qb);
+        for (int t = 0; t < 8; t++) {
+            const uint32_t l0 = __builtin_amdgcn_alignbyte(qw[2 * t + 1], qw[2 * t], sh8);
+            const uint32_t l1 = __builtin_amdgcn_alignbyte(qw[2 * t + 2], qw[2 * t + 1], sh8);
+            const uint32_t h0 = __builtin_amdgcn_alignbyte(hw[2 * (t & 3) + 1], hw[2 * (t & 3)], sh8);
+            const uint32_t h1 = __builtin_amdgcn_alignbyte(hw[2 * (t & 3) + 2], hw[2 * (t & 3) + 1], sh8);
 #pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    const float ds = d * q6k_scale(scw, i2 + 2 * t);
-                    const float c = -1056.f * ds;
-                    uint4 bw;
-                    bytes_to_w(qa[t], ds, c, bw.x, bw.y);
-                    bytes_to_w(qb[t], ds, c, bw.z, bw.w);
-                    const int s = 8 * b + 4 * h + t;
-                    acc = mfma16(sA[0][(4 * s + g) * 16 + n], bw, acc);
-                    acc = mfma16(sA[1][(4 * s + g) * 16 + n], bw, acc);
-                }
+            for (int hi = 0; hi < 2; hi++) {
+                const int tt = t + 8 * hi;
+                const int hs = 2 * (tt >> 2);
+                const uint32_t scw = hi ? s1 : s0;
+                const float ds = d * (float)(int8_t)byte_of(scw, (uint32_t)((t >> 1) & 3));
+                const float c = -1056.f * ds;
+                bad |= !(fabsf(ds) < 2047.f);
+                const uint32_t n0v = (hi ? l0 >> 4 : l0) & 0x0F0F0F0Fu;
+                const uint32_t n1v = (hi ? l1 >> 4 : l1) & 0x0F0F0F0Fu;
+                const uint32_t q0 = n0v | (((h0 >> hs) & 0x03030303u) << 4);
+                const uint32_t q1 = n1v | (((h1 >> hs) & 0x03030303u) << 4);
+                uint4 bw;
+                bytes_to_w(q0, ds, c, bw.x, bw.y);
+                bytes_to_w(q1, ds, c, bw.z, bw.w);
+                const int unit = (16 * b + tt) * 64 + lane;
+                acc = mfma32(bw, sA[0][unit], acc);
+                acc = mfma32(bw, sA[1][unit], acc);
             }
         }
-        const int r = n0 + 16 * (DN_CB * w + cb) + n;
+        if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0)
+            __hip_atomic_fetch_or(a.err, DEV_ERR_RANGE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (b == nb - 1) {
+            if (r < tl.nr) {
+                const int e = sexp[r];
+                float *op = a.eo + (size_t)(tl.p0 + r) * a.H + row0 + 32 * (it / nb) + 4 * g;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = 4 * g + i;
-            if (m < tl.nr) a.eo[(size_t)(tl.p0 + m) * a.H + r] = ldexpf(acc[i], sexp[m]);
+                for (int j = 0; j < 4; j++) {
+                    float4 o;
+                    o.x = ldexpf(acc[4 * j + 0], e);
+                    o.y = ldexpf(acc[4 * j + 1], e);
+                    o.z = ldexpf(acc[4 * j + 2], e);
+                    o.w = ldexpf(acc[4 * j + 3], e);
+                    *reinterpret_cast<float4 *>(op + 8 * j) = o;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[i] = 0.f;
         }
+    };
+
+    for (int it = 0; it < items; it += 2) {
+        if (it + 1 < items) q6k_load(item_ptr(it + 1), g, R1);
+        compute(it, R0);
+        if (it + 1 >= items) break;
+        if (it + 2 < items) q6k_load(item_ptr(it + 2), g, R0);
+        compute(it + 1, R1);
     }
 }
 
 // hidden[t] += sigmoid(gsh[t]) * shared(t), then += w_k * expert_k(t) for
-// k = 0..K-1 (one_layer.cu:1447-1449, 1469), one float4 per thread.
+// k = 0..K-1 (one_layer.cu:1447-1449, 1469), one float4 per thread;
+// blockIdx.x = token, blockIdx.y = 1024-column chunk.
 __global__ __launch_bounds__(256) void k_mt_combine(const float *__restrict__ eo, const int *__restrict__ pos_of,
                                                     const float *__restrict__ w, const float *__restrict__ gsh,
                                                     float *__restrict__ hidden, int H, int K, int T)
 {
 #pragma clang fp contract(off)
-    const int h4 = H / 4;
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (int64_t)T * h4) return;
-    const int t = (int)(i / h4), c = (int)(i % h4) * 4;
+    const int t = blockIdx.x;
+    const int c = 4 * (blockIdx.y * blockDim.x + threadIdx.x);
+    if (c >= H) return;
     float4 acc = *reinterpret_cast<const float4 *>(hidden + (size_t)t * H + c);
     const float sg = sigmoidf_ref(gsh[t]);
     const float4 s = *reinterpret_cast<const float4 *>(eo + ((size_t)T * K + t) * H + c);
@@ -573,6 +752,7 @@ __global__ __launch_bounds__(256) void k_mt_combine(const float *__restrict__ eo
     acc.y = acc.y + sg * s.y;
     acc.z = acc.z + sg * s.z;
     acc.w = acc.w + sg * s.w;
+#pragma unroll 8
     for (int k = 0; k < K; k++) {
         const int p = pos_of[t * K + k];
         if (p < 0) continue;
@@ -613,6 +793,10 @@ int bread_grouped_alloc(bread_moe_ctx_t *c)
     if (e == hipSuccess) e = hipMalloc(&g.tiles, (size_t)max_tiles(s, c->max_tokens) * sizeof(MtTile));
     if (e == hipSuccess) e = hipMalloc((void **)&g.n_tiles, sizeof(int));
     if (e == hipSuccess) e = hipMalloc((void **)&g.eo, P * H * sizeof(float));
+    const size_t Imax = (size_t)(s.expert_inter > s.shared_inter ? s.expert_inter : s.shared_inter);
+    if (e == hipSuccess) e = hipMalloc(&g.hhi, P * Imax * 2);
+    if (e == hipSuccess) e = hipMalloc(&g.hlo, P * Imax * 2);
+    if (e == hipSuccess) e = hipMalloc((void **)&g.hexp, P * sizeof(int));
     return e == hipSuccess ? BREAD_OK : (e == hipErrorOutOfMemory ? BREAD_ERR_NOMEM : BREAD_ERR_HIP);
 }
 
@@ -627,13 +811,16 @@ void bread_grouped_free(bread_moe_ctx_t *c)
     (void)hipFree(g.tiles);
     (void)hipFree(g.n_tiles);
     (void)hipFree(g.eo);
+    (void)hipFree(g.hhi);
+    (void)hipFree(g.hlo);
+    (void)hipFree(g.hexp);
     g = bread_grouped_ws{};
 }
 
 bool bread_grouped_supported(const bread_moe_shape_t &s, const bread_moe_layer_t *L)
 {
     if (s.expert_inter > MAX_INTER || s.shared_inter > MAX_INTER) return false;
-    // down bands are loaded 16 bytes a lane
+    // Q6_K expert blocks must end 16-byte aligned (see the down operand order)
     const uintptr_t a16 = (uintptr_t)L->down_exps | (uintptr_t)L->down_shexp | L->down_expert_bytes;
     return (a16 & 15) == 0;
 }
@@ -651,8 +838,8 @@ int bread_launch_moe_grouped(bread_moe_ctx_t *c, const bread_moe_layer_t *L, con
     hipLaunchKernelGGL(k_mt_xprep, dim3(T), dim3(256), 0, st, x, (const uint16_t *)L->shexp_gate, H,
                        (uint4 *)g.xhi, (uint4 *)g.xlo, g.xexp, c->gsh);
     BREAD_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_mt_router, dim3((T + 15) / 16, (E + 15) / 16), dim3(256), 0, st, (const float *)L->router, x,
-                       c->logits, H, E, T);
+    hipLaunchKernelGGL(k_mt_router, dim3((T + 15) / 16, (E + 15) / 16), dim3(RT_WAVES * WAVE), 0, st,
+                       (const float *)L->router, x, c->logits, H, E, T);
     BREAD_HIP(hipGetLastError());
     int rc = bread_launch_topk(c->logits, E, K, T, c->idx, c->w, st);
     if (rc) return rc;
@@ -661,6 +848,7 @@ int bread_launch_moe_grouped(bread_moe_ctx_t *c, const bread_moe_layer_t *L, con
     BREAD_HIP(hipGetLastError());
     MtArgs a;
     a.L = *L;
+    a.err = &c->dsync->error.v;
     a.H = H;
     a.I = s.expert_inter;
     a.Ish = s.shared_inter;
@@ -674,16 +862,22 @@ int bread_launch_moe_grouped(bread_moe_ctx_t *c, const bread_moe_layer_t *L, con
     a.pair_tok = g.pair_tok;
     a.tiles = (const MtTile *)g.tiles;
     a.n_tiles = g.n_tiles;
-    a.hbuf = c->h;
+    a.h = c->h;
+    a.hhi = (const uint4 *)g.hhi;
+    a.hlo = (const uint4 *)g.hlo;
+    a.hexp = g.hexp;
     a.eo = g.eo;
     const int nt = max_tiles(s, T);
-    hipLaunchKernelGGL(k_mt_gateup, dim3(nt, (Imax + GU_ROWS - 1) / GU_ROWS), dim3(GU_WAVES * WAVE), 0, st, a);
+    hipLaunchKernelGGL(k_mt_gateup, dim3(nt, Imax / GU_ROWS), dim3(GU_WAVES * WAVE), 0, st, a);
     BREAD_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_mt_down, dim3(nt, H / DN_ROWS), dim3(DN_WAVES * WAVE), 0, st, a);
+    const int rows = T * (K + 1);
+    hipLaunchKernelGGL(k_mt_hprep, dim3((rows + 3) / 4), dim3(256), 0, st, c->h, rows, T * K, s.expert_inter,
+                       s.shared_inter, Imax, (uint4 *)g.hhi, (uint4 *)g.hlo, g.hexp);
     BREAD_HIP(hipGetLastError());
-    const int64_t n4 = (int64_t)T * (H / 4);
-    hipLaunchKernelGGL(k_mt_combine, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, g.eo, g.pos_of, c->w,
-                       c->gsh, hidden, H, K, T);
+    hipLaunchKernelGGL(k_mt_down, dim3(nt, (H + DN_ROWS - 1) / DN_ROWS), dim3(DN_WAVES * WAVE), 0, st, a);
+    BREAD_HIP(hipGetLastError());
+    hipLaunchKernelGGL(k_mt_combine, dim3(T, (H / 4 + 255) / 256), dim3(256), 0, st, g.eo, g.pos_of, c->w, c->gsh,
+                       hidden, H, K, T);
     BREAD_HIP(hipGetLastError());
     return BREAD_OK;
 }

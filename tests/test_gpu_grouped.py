@@ -15,7 +15,7 @@ import pytest
 import torch
 
 import breadv2_amd as B
-from breadv2_amd import api, synth
+from breadv2_amd import _lib, api, synth
 from oracle import oracle as O
 
 from helpers import MAX_ABS_TOL, REL_L2_TOL, assert_moe_close, host_layer, max_abs, rel_l2, scale_layer_d
@@ -198,3 +198,46 @@ def test_grouped_null_shared_gate(full_layer):
     got = run(s, lt, x, hidden)
     assert np.all(got[3] == 0.0)
     check(hl, x, hidden, got)
+
+
+def _gate_d(t, s, expert: int, d: float):
+    """Set d of every Q4_K superblock of one expert's gate matrix."""
+    g = t.gate_exps.cpu().numpy().reshape(s.n_experts, -1)
+    blocks = g[expert].reshape(-1, 144)
+    blocks[:, 0:2] = np.array([d], np.float16).view(np.uint8)
+    g[expert] = blocks.reshape(-1)
+    t.gate_exps.copy_(torch.from_numpy(g.reshape(-1)))
+    torch.cuda.synchronize()
+
+
+def test_grouped_large_scales_near_fp16_limit():
+    """d = 32: dequantised gate weights up to 32 * 63 * 15 = 30240, inside
+    fp16's range; the packed-fp16 dequant stays exact in sc * q."""
+    s = api.shape(hidden=512, expert_inter=256, shared_inter=256, n_experts=16, top_k=2)
+    t = api.synth_layer_tensors(s, seed=91, layer=0)
+    _gate_d(t, s, 3, 32.0)
+    hl = host_layer(t)
+    x = tokens(64, s.hidden, 92, zipf=False)
+    hidden = np.zeros_like(x)
+    got = run(s, t, x, hidden)
+    assert np.any(got[1] == 3), "expert 3 not routed; pick another seed"
+    check(hl, x, hidden, got)
+
+
+def test_grouped_weights_beyond_fp16_flag_device_error():
+    """d = 100 puts dequantised weights beyond fp16's range (the grouped
+    path's operand type): the call completes and bread_moe_ctx_check reports
+    BREAD_ERR_DEVICE with the range bit (4) set."""
+    s = api.shape(hidden=512, expert_inter=256, shared_inter=256, n_experts=16, top_k=2)
+    t = api.synth_layer_tensors(s, seed=91, layer=0)
+    _gate_d(t, s, 3, 100.0)
+    x = tokens(64, s.hidden, 92, zipf=False)
+    ctx = B.MoeContext(s, max_tokens=64)
+    ctx.set_path(api.PATH_GROUPED)
+    idx, _, _ = ctx.forward(t.desc(), dev(x), dev(np.zeros_like(x)), 64, want_routing=True)
+    torch.cuda.synchronize()
+    assert np.any(idx.cpu().numpy() == 3)
+    with pytest.raises(B.BreadError) as ei:
+        ctx.check_device()
+    assert ei.value.status == _lib.ERR_DEVICE
+    ctx.check_device()  # cleared
