@@ -11,7 +11,9 @@ decode token, one kernel launch:
 with l cycling over the 40 resident layers, each step reading the previous
 step's output (a real decode dependency, no overlap between steps).
 config.stack reports configs[2] as well: one decode token through all 40
-layers in a single launch, 128 tokens.
+layers in a single launch, 128 tokens.  multi_token reports configs[3] and
+configs[4] (batched decode B = 8/16/64 with Zipf routing, 512-token prefill
+chunks with uniform and Zipf routing) on the grouped path.
 
 value = decode MoE-layer tokens per second (steps / s).
 roofline: the single-launch MoE kernel, expert-weight bytes per launch
@@ -90,6 +92,69 @@ def cpu_baseline(arena, s, seconds: float):
     return out, threads, cores
 
 
+MT_CASES = [("config4: batched decode / verify, B=8, Zipf(1.1) routing", 8, True),
+            ("config4: batched decode / verify, B=16, Zipf(1.1) routing", 16, True),
+            ("config4: batched decode / verify, B=64, Zipf(1.1) routing", 64, True),
+            ("config5: prefill chunk, 512 tokens, uniform routing", 512, False),
+            ("config5: prefill chunk, 512 tokens, Zipf(1.1) routing", 512, True)]
+MFMA_F16_PEAK_TFS = 2500.0
+
+
+def multi_token(arena, s, steps: int, stream):
+    """Configs 4 and 5 on the grouped path.  Zipf cases use layers 32..39 with
+    the router's last column set to a Zipf(1.1) bias (tokens carry a 1 in
+    their last feature); uniform cases layers 24..31.  Each case cycles its 8
+    layers (~4.2 GB of experts, beyond the Infinity Cache), x ~ N(0,1)."""
+    import numpy as np
+    import torch
+
+    import breadv2_amd as B
+    from breadv2_amd import api, synth
+
+    H, E = s.hidden, s.n_experts
+    for l in range(32, 40):
+        arena.set_router_column(l, H - 1, synth.zipf_bias(E, 1.1, seed=1000 + l))
+    out = []
+    for name, T, zipf in MT_CASES:
+        layers = [arena.layer(l + (32 if zipf else 24)) for l in range(8)]
+        ctx = B.MoeContext(s, max_tokens=T)
+        ctx.set_path(api.PATH_GROUPED)
+        g = torch.Generator(device="cuda:0").manual_seed(T)
+        x = torch.randn(T, H, device="cuda:0", generator=g)
+        if zipf:
+            x[:, -1] = 1.0
+        hid = torch.zeros(T, H, device="cuda:0")
+        distinct = []
+        with torch.cuda.stream(stream):
+            for i in range(8):
+                idx, _, _ = ctx.forward(layers[i], x, hid, T, want_routing=True, stream=stream)
+                distinct.append(int(np.unique(idx.cpu().numpy()).size))
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for i in range(steps):
+                ctx.forward(layers[i % 8], x, hid, T, stream=stream)
+            e1.record(stream)
+            torch.cuda.synchronize()
+        if ctx.check_device():
+            raise RuntimeError("grouped path flagged a device error")
+        us = e0.elapsed_time(e1) * 1e3 / steps
+        U = sum(distinct) / len(distinct)
+        nbytes = U * EXPERT_BYTES + EXPERT_BYTES + 2_097_152 + 4_096 + 2 * T * H * 4
+        flops = 9 * T * 6_291_456 + T * 1_048_576
+        out.append({
+            "workload": name, "tokens": T, "us_per_layer": round(us, 1), "tok_s": round(T / us * 1e6, 1),
+            "distinct_experts": round(U, 1), "algorithmic_bytes": int(nbytes),
+            "hbm_gbs": round(nbytes / us / 1e3, 1), "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            "algorithmic_flops": flops, "tflops": round(flops / us / 1e6, 2),
+            "mfma_util": round(flops / us / 1e6 / MFMA_F16_PEAK_TFS, 4),
+        })
+        log(f"{name}: {us:.1f} us/layer, {T / us * 1e6:.0f} tok/s, U={U:.1f}")
+        ctx.close()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -100,6 +165,10 @@ def main() -> int:
     ap.add_argument("--stack-tokens", type=int, default=128,
                     help="config 3: decode tokens through the whole resident stack, one launch per token")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--mt-steps", type=int, default=40,
+                    help="configs 4/5: timed grouped-path layers per case (0 skips them)")
+    ap.add_argument("--only-mt", action="store_true",
+                    help="profiling aid: run only the configs 4/5 cases and print their JSON")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 512 MiB device copy (known bytes) to calibrate rocprofv3 FETCH/WRITE_SIZE")
     args = ap.parse_args()
@@ -128,6 +197,10 @@ def main() -> int:
     descs = [arena.layer(l) for l in range(L)]
     ctx = B.MoeContext(s, max_tokens=1)
     stream = torch.cuda.Stream()
+    if args.only_mt:
+        print(json.dumps({"multi_token": multi_token(arena, s, args.mt_steps, stream)}), flush=True)
+        arena.close()
+        return 0
     h = torch.randn(1, s.hidden, device="cuda:0", generator=torch.Generator("cuda:0").manual_seed(1))
 
     def step(i):
@@ -245,6 +318,14 @@ def main() -> int:
             "layer_tok_s": round(L * 1e6 / stack_us, 1),
             "expert_gbs": round(L * LAYER_EXPERT_BYTES / (stack_us * 1e-6) / 1e9, 1),
             "frac": round(L * LAYER_EXPERT_BYTES / (stack_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        }
+    if args.mt_steps > 0 and L >= 40:
+        result["multi_token"] = {
+            "path": "grouped (tokens bucketed by expert, fp16 MFMA expert GEMMs, fp32 accumulate)",
+            "mfma_peak_tflops": MFMA_F16_PEAK_TFS,
+            "flops_note": "algorithmic: 9 x 6,291,456 per token (8 routed + shared) + router 1,048,576; "
+                          "executed MFMA work is higher (32-pair tiles padded, activations as hi+lo fp16)",
+            "cases": multi_token(arena, s, args.mt_steps, stream),
         }
     if not args.no_cpu:
         res, threads, cores = cpu_baseline(arena, s, args.cpu_seconds)

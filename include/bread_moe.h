@@ -165,7 +165,11 @@ int bread_moe_ctx_set_path(bread_moe_ctx_t *ctx, int path);
 
 /* Synchronises the context's last stream and returns BREAD_ERR_DEVICE (and
  * the kernel's error word in *device_error, if given) when a kernel flagged
- * a fault, e.g. a bounded wait that expired.  Clears the word. */
+ * a fault.  Bits: 1 = the decode kernel's bounded wait for hidden or SwiGLU
+ * values expired, 2 = its wait for router logits expired (both: a launch that
+ * could not get every CU), 4 = the grouped path met a weight superblock whose
+ * dequantised values exceed fp16's range (Q4_K d >= 64 or dmin >= 1024,
+ * Q6_K |d*sc| >= 2047).  Clears the word. */
 int bread_moe_ctx_check(bread_moe_ctx_t *ctx, int *device_error);
 
 /* Routing for n_tokens tokens on the device: router GEMV (fp32), softmax,
