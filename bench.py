@@ -155,6 +155,41 @@ def multi_token(arena, s, steps: int, stream):
     return out
 
 
+def lm_head(steps: int):
+    """SURVEY's next row 4: the lm_head (248,320 x 2048) through bread_matvec
+    with the reference's fp16 I/O (main.cu:297-319), Q4_K and Q6_K weights,
+    two copies alternated so reads come from HBM."""
+    import torch
+
+    from breadv2_amd import api
+
+    R, C = 248_320, 2048
+    out = []
+    for qt, name, bpr in ((api.QTYPE_Q4_K, "Q4_K", C // 256 * 144), (api.QTYPE_Q6_K, "Q6_K", C // 256 * 210)):
+        ws = [torch.empty(R * bpr, dtype=torch.uint8, device="cuda:0") for _ in range(2)]
+        for i, w in enumerate(ws):
+            (api.synth_q4k if qt == api.QTYPE_Q4_K else api.synth_q6k)(w, R * C // 256, 31 + i)
+        x = torch.randn(C, device="cuda:0").to(torch.float16)
+        y = torch.empty(R, device="cuda:0", dtype=torch.float16)
+        for i in range(4):
+            api.bread_matvec(ws[i % 2], x, y, R, C, qt)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            api.bread_matvec(ws[i % 2], x, y, R, C, qt)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / steps
+        nb = R * bpr + 2 * (C + R)
+        out.append({"qtype": name, "rows": R, "cols": C, "us": round(us, 1), "bytes": nb,
+                    "gbs": round(nb / us / 1e3, 1), "frac": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)})
+        log(f"lm_head {name}: {us:.1f} us, {nb / us / 1e3:.0f} GB/s")
+        del ws
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -327,6 +362,8 @@ def main() -> int:
                           "executed MFMA work is higher (32-pair tiles padded, activations as hi+lo fp16)",
             "cases": multi_token(arena, s, args.mt_steps, stream),
         }
+    if args.mt_steps > 0:
+        result["lm_head"] = {"entry": "bread_matvec (fp16 x/y)", "cases": lm_head(20)}
     if not args.no_cpu:
         res, threads, cores = cpu_baseline(arena, s, args.cpu_seconds)
         v, n, el = res[threads]

@@ -6,6 +6,8 @@
 // fp32 accumulate, DPP wave reduction.  Replaces kernels.cu:150-308, whose
 // 256-thread blocks read one element per thread with two barriers per
 // superblock.
+#include <type_traits>
+
 #include "bread_internal.h"
 #include "quant_dot.h"
 
@@ -36,6 +38,109 @@ __global__ __launch_bounds__(256) void k_matvec(const uint8_t *__restrict__ w, c
             p = q80_row_partial(row, cols / Q80_ELEMS, x, lane);
         p = wave_sum(p);
         if (lane == 0) store_y(y, r, p);
+    }
+}
+
+// ---- Long matvecs (the lm_head: 248,320 rows): each wave holds its lanes'
+// slices of x in registers for all its rows (lane l always reads superblocks
+// l/8 + 8j, j < NBL, of a row: cols = 2048 * NBL) and streams two rows per
+// iteration, so x is read once per wave instead of once per row.
+
+template <typename XT>
+struct XQ4 {
+    float xl[16], xh[16], sl, sh;
+    __device__ __forceinline__ void load(const XT *x, int b, int c)
+    {
+        const int base = b * QK + 64 * (c >> 1) + 16 * (c & 1);
+        load_x16(x, base, xl);
+        load_x16(x, base + 32, xh);
+        sl = 0.f;
+        sh = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            sl += xl[k];
+            sh += xh[k];
+        }
+    }
+};
+
+template <typename XT>
+struct XQ6 {
+    float xs[4][8], X[4];
+    __device__ __forceinline__ void load(const XT *x, int b, int c)
+    {
+        const int n = c >> 2, t = c & 3;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            load_x8(x, b * QK + 128 * n + 32 * s + 8 * t, xs[s]);
+            X[s] = 0.f;
+#pragma unroll
+            for (int k = 0; k < 8; k++) X[s] += xs[s][k];
+        }
+    }
+};
+
+template <int QT, typename XT, typename YT, int NBL>
+__global__ __launch_bounds__(256) void k_matvec_xr(const uint8_t *__restrict__ w, const XT *__restrict__ x,
+                                                   YT *__restrict__ y, int rows, uint64_t row_bytes)
+{
+    constexpr int RPI = 4;  // rows per iteration
+    const int lane = lane_id();
+    const int c = lane & 7, b0 = lane >> 3;
+    const int wv = (int)((blockIdx.x * blockDim.x + threadIdx.x) / WAVE);
+    const int nw = (int)(gridDim.x * blockDim.x / WAVE);
+    typename std::conditional<QT == BREAD_QTYPE_Q4_K, XQ4<XT>, XQ6<XT>>::type xr[NBL];
+#pragma unroll
+    for (int j = 0; j < NBL; j++) xr[j].load(x, b0 + 8 * j, c);
+    for (int r0 = wv * RPI; r0 < rows; r0 += nw * RPI) {
+        float p[RPI];
+        if constexpr (QT == BREAD_QTYPE_Q4_K) {
+            uint4 hd[RPI][NBL], q[RPI][NBL];
+#pragma unroll
+            for (int u = 0; u < RPI; u++)
+#pragma unroll
+                for (int j = 0; j < NBL; j++) {
+                    const uint8_t *blk = w + (size_t)min(r0 + u, rows - 1) * row_bytes + (size_t)(b0 + 8 * j) * Q4K_BYTES;
+                    hd[u][j] = ld_b128(blk);
+                    q[u][j] = ld_b128(blk + 16 + 16 * c);
+                }
+#pragma unroll
+            for (int u = 0; u < RPI; u++) {
+                p[u] = 0.f;
+#pragma unroll
+                for (int j = 0; j < NBL; j++)
+                    p[u] += q4k_chunk_dot_sx(hd[u][j], q[u][j], (uint32_t)(c >> 1), xr[j].xl, xr[j].xh, xr[j].sl,
+                                             xr[j].sh);
+            }
+        } else {
+            const int n = c >> 2, t = c & 3;
+            uint2 ql0[RPI][NBL], ql1[RPI][NBL], qh[RPI][NBL], scw[RPI][NBL];
+            uint32_t dd[RPI][NBL];
+#pragma unroll
+            for (int u = 0; u < RPI; u++)
+#pragma unroll
+                for (int j = 0; j < NBL; j++) {
+                    const uint8_t *blk = w + (size_t)min(r0 + u, rows - 1) * row_bytes + (size_t)(b0 + 8 * j) * Q6K_BYTES;
+                    ql0[u][j] = ld8_a2(blk + 64 * n + 8 * t);
+                    ql1[u][j] = ld8_a2(blk + 64 * n + 32 + 8 * t);
+                    qh[u][j] = ld8_a2(blk + 128 + 32 * n + 8 * t);
+                    scw[u][j] = ld8_a2(blk + 192 + 8 * n);
+                    dd[u][j] = ld16_a2(blk + 208);
+                }
+#pragma unroll
+            for (int u = 0; u < RPI; u++) {
+                p[u] = 0.f;
+#pragma unroll
+                for (int j = 0; j < NBL; j++)
+                    p[u] += q6k_unit_dot_sx(ql0[u][j], ql1[u][j], qh[u][j], scw[u][j], (uint32_t)t >> 1,
+                                            h2f(dd[u][j]), xr[j].xs, xr[j].X);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < RPI; u++) {
+            const float v = wave_sum(p[u]);
+            if (lane == 0 && r0 + u < rows) store_y(y, r0 + u, v);
+        }
     }
 }
 
@@ -152,6 +257,21 @@ int launch_matvec(const void *w, const XT *x, YT *y, int rows, int cols, int qty
     int blocks = (rows + waves_per_block - 1) / waves_per_block;
     if (blocks > 65536) blocks = 65536;
     const uint8_t *wb = (const uint8_t *)w;
+    // long matvecs with 2048 or 4096 columns: x held in registers, >= 4 rows
+    // per wave (16 waves per CU)
+    constexpr int XR_WAVES = 256 * 16;
+    if (rows >= 4 * XR_WAVES && (cols == 2048 || cols == 4096) && qtype != BREAD_QTYPE_Q8_0) {
+        const dim3 g(XR_WAVES / 4), b(256);
+        if (qtype == BREAD_QTYPE_Q4_K) {
+            if (cols == 2048) hipLaunchKernelGGL((k_matvec_xr<BREAD_QTYPE_Q4_K, XT, YT, 1>), g, b, 0, st, wb, x, y, rows, rb);
+            else hipLaunchKernelGGL((k_matvec_xr<BREAD_QTYPE_Q4_K, XT, YT, 2>), g, b, 0, st, wb, x, y, rows, rb);
+        } else {
+            if (cols == 2048) hipLaunchKernelGGL((k_matvec_xr<BREAD_QTYPE_Q6_K, XT, YT, 1>), g, b, 0, st, wb, x, y, rows, rb);
+            else hipLaunchKernelGGL((k_matvec_xr<BREAD_QTYPE_Q6_K, XT, YT, 2>), g, b, 0, st, wb, x, y, rows, rb);
+        }
+        BREAD_HIP(hipGetLastError());
+        return BREAD_OK;
+    }
     switch (qtype) {
     case BREAD_QTYPE_Q4_K:
         hipLaunchKernelGGL((k_matvec<BREAD_QTYPE_Q4_K, XT, YT>), dim3(blocks), dim3(256), 0, st, wb, x, y, rows, cols, rb);

@@ -138,6 +138,26 @@ __device__ __forceinline__ float q6k_unit_dot(uint2 ql0, uint2 ql1, uint2 qh, ui
     return d * r;
 }
 
+// q6k_unit_dot with the activation sums X[s] = sum_k xs[s][k] precomputed.
+__device__ __forceinline__ float q6k_unit_dot_sx(uint2 ql0, uint2 ql1, uint2 qh, uint2 scw, uint32_t i, float d,
+                                                 const float (&xs)[4][8], const float (&X)[4])
+{
+    float A[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < 2; w++) {
+        uint32_t q[4];
+        q6k_unpack(w ? ql0.y : ql0.x, w ? ql1.y : ql1.x, w ? qh.y : qh.x, q);
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) A[s] = fmaf((float)byte_of(q[s], k), xs[s][4 * w + k], A[s]);
+    }
+    float r = 0.f;
+#pragma unroll
+    for (int s = 0; s < 4; s++) r = fmaf(q6k_scale(scw, i + 2 * s), fmaf(-32.f, X[s], A[s]), r);
+    return d * r;
+}
+
 template <typename XT>
 __device__ __forceinline__ float q6k_row_partial(const uint8_t *row, int nb, const XT *x, int lane)
 {

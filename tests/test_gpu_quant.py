@@ -135,10 +135,13 @@ def abs_bound(w, qtype, x, rows, cols):
 @pytest.mark.parametrize(
     "qtype,rows,cols",
     [(Q4K, 512, 2048), (Q4K, 1, 256), (Q4K, 37, 4352), (Q4K, 300, 16384), (Q6K, 2048, 512), (Q6K, 5, 256),
-     (Q6K, 33, 2304), (Q80, 100, 2048), (Q80, 3, 32), (Q80, 17, 2080)],
+     (Q6K, 33, 2304), (Q80, 100, 2048), (Q80, 3, 32), (Q80, 17, 2080),
+     (Q4K, 20001, 2048), (Q4K, 16385, 4096), (Q6K, 20001, 2048), (Q6K, 16385, 4096)],
 )
 def test_matvec_f32_parity(qtype, rows, cols):
-    """Config 1 is the first case (512 x 2048 Q4_K, x ~ N(0,1))."""
+    """Config 1 is the first case (512 x 2048 Q4_K, x ~ N(0,1)).  Row counts
+    >= 16384 with 2048 or 4096 columns take the long-matvec kernel (x held in
+    registers, two rows per iteration; odd counts exercise its tail)."""
     w = weights(qtype, rows, cols, seed=rows * 7 + cols)
     x = np.random.default_rng(rows + cols).standard_normal(cols).astype(np.float32)
     y = torch.empty(rows, dtype=torch.float32, device=DEV)
@@ -151,10 +154,12 @@ def test_matvec_f32_parity(qtype, rows, cols):
     assert np.linalg.norm(got - ref) <= 1e-5 * np.linalg.norm(ref)
 
 
-@pytest.mark.parametrize("qtype,rows,cols", [(Q4K, 512, 2048), (Q6K, 2048, 512), (Q80, 64, 2048), (Q4K, 9, 768)])
+@pytest.mark.parametrize("qtype,rows,cols", [(Q4K, 512, 2048), (Q6K, 2048, 512), (Q80, 64, 2048), (Q4K, 9, 768),
+                                             (Q4K, 20001, 2048), (Q6K, 16385, 4096)])
 def test_matvec_f16_io(qtype, rows, cols):
     """bread_matvec fp16 I/O: equal to the oracle's fp16-rounded result up to
-    one ulp (the fp32 sums differ only in order)."""
+    one ulp plus the fp32 summation-order bound of test_matvec_f32_parity
+    (which dominates for results near zero, where the fp16 ulp is tiny)."""
     w = weights(qtype, rows, cols, seed=3 + rows)
     x16 = np.random.default_rng(9).standard_normal(cols).astype(np.float16)
     y = torch.empty(rows, dtype=torch.float16, device=DEV)
@@ -164,7 +169,8 @@ def test_matvec_f16_io(qtype, rows, cols):
     g32 = got.astype(np.float32)
     r32 = ref.astype(np.float32)
     ulp = np.spacing(np.abs(ref)).astype(np.float32)
-    assert np.all(np.abs(g32 - r32) <= ulp + 1e-6)
+    order = 2 * cols * 2.0**-24 * abs_bound(w, qtype, x16.astype(np.float32), rows, cols)
+    assert np.all(np.abs(g32 - r32) <= ulp + order + 1e-6)
     assert np.max(np.abs(g32 - r32)) < 0.05 * max(1.0, float(np.max(np.abs(r32))))
 
 
