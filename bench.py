@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
 """bench.py — MoE-layer decode at batch 1 on one MI355X.
 
-Workload (timed over the configs[2] arena so the
+Workload (the headline config, batch-1 decode of one MoE layer, timed over
+the 40-layer arena of the stack config so the
 working set is ~21 GB, far above the 256 MB Infinity Cache): all 256 experts
 of 40 layers resident in HBM (Qwen3.5-35B-A3B shape: hidden 2048, expert and
 shared intermediate 512, 256 experts, top-8, Q4_K gate/up, Q6_K down, fp32
@@ -156,7 +157,7 @@ def multi_token(arena, s, steps: int, stream):
 
 
 def lm_head(steps: int):
-    """SURVEY's next row 4: the lm_head (248,320 x 2048) through bread_matvec
+    """The lm_head (248,320 x 2048) through bread_matvec
     with the reference's fp16 I/O (main.cu:297-319), Q4_K and Q6_K weights,
     two copies alternated so reads come from HBM."""
     import torch
@@ -211,7 +212,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build measures one GPU: the MoE decode layer is single-GPU "
-                                   "(expert-parallel sharding is design-only, see DESIGN.md); run with --gpus 1"}))
+                                   "(expert-parallel sharding is a design, not built); run with --gpus 1"}))
         return 2
 
     import torch

@@ -7,6 +7,7 @@ without the built library raises: there is no CPU fallback.
 from ._lib import BreadError, MoeLayer, MoeShape, lib, status_str  # noqa: F401
 from .api import (  # noqa: F401
     Arena,
+    Gguf,
     LayerTensors,
     MoeContext,
     bread_dequant_rows,

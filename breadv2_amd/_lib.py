@@ -49,6 +49,7 @@ ERR_HIP = -5
 ERR_NOMEM = -6
 ERR_CAPACITY = -7
 ERR_DEVICE = -8
+ERR_FORMAT = -9
 
 
 class BreadError(RuntimeError):
@@ -92,6 +93,19 @@ class MoeLayer(ctypes.Structure):
     ]
 
 
+class GgufTensor(ctypes.Structure):
+    _fields_ = [
+        ("name", c_char_p),
+        ("type", ctypes.c_uint32),
+        ("n_dims", ctypes.c_uint32),
+        ("dims", c_uint64 * 4),
+        ("offset", c_uint64),
+        ("size", c_uint64),
+        ("n_elems", c_uint64),
+        ("data", c_void_p),
+    ]
+
+
 # name -> (restype, argtypes); mirrors include/bread_moe.h one to one.
 SIGNATURES = {
     "bread_status_str": (c_char_p, [c_int]),
@@ -126,6 +140,18 @@ SIGNATURES = {
     "bread_synth_q6k": (c_int, [c_void_p, c_uint64, c_uint64, c_void_p]),
     "bread_synth_normal_f32": (c_int, [c_void_p, c_uint64, c_uint64, c_float, c_float, c_void_p]),
     "bread_synth_normal_f16": (c_int, [c_void_p, c_uint64, c_uint64, c_float, c_float, c_void_p]),
+    "bread_gguf_open": (c_int, [c_char_p, POINTER(c_void_p)]),
+    "bread_gguf_close": (c_int, [c_void_p]),
+    "bread_gguf_info": (c_int, [c_void_p, POINTER(ctypes.c_uint32), POINTER(c_uint64), POINTER(c_uint64),
+                                POINTER(c_uint64), POINTER(ctypes.c_uint32)]),
+    "bread_gguf_tensor": (c_int, [c_void_p, c_uint64, POINTER(GgufTensor)]),
+    "bread_gguf_find": (c_int, [c_void_p, c_char_p, POINTER(GgufTensor)]),
+    "bread_gguf_kv_int": (c_int, [c_void_p, c_char_p, POINTER(ctypes.c_int64)]),
+    "bread_gguf_kv_float": (c_int, [c_void_p, c_char_p, POINTER(ctypes.c_double)]),
+    "bread_gguf_kv_str": (c_int, [c_void_p, c_char_p, c_char_p, ctypes.c_size_t]),
+    "bread_ggml_type_size": (c_uint64, [ctypes.c_uint32, c_uint64]),
+    "bread_gguf_moe_shape": (c_int, [c_void_p, c_int, POINTER(MoeShape)]),
+    "bread_arena_load_gguf": (c_int, [c_void_p, c_int, c_void_p, c_int]),
 }
 
 

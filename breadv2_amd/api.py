@@ -189,6 +189,68 @@ def synth_layer_tensors(s: MoeShape, seed: int, layer: int = 0, router_std: floa
     return t
 
 
+class Gguf:
+    """A parsed GGUF v2/v3 file (bread_gguf_*): metadata and tensor index over
+    a read-only mapping; weights are read when loaded into an Arena."""
+
+    def __init__(self, path: str):
+        self._h = ctypes.c_void_p()
+        check(lib.bread_gguf_open(path.encode(), ctypes.byref(self._h)), "bread_gguf_open")
+
+    def info(self) -> dict:
+        v, a = ctypes.c_uint32(), ctypes.c_uint32()
+        nt, nk, off = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+        check(lib.bread_gguf_info(self._h, ctypes.byref(v), ctypes.byref(nt), ctypes.byref(nk), ctypes.byref(off),
+                                  ctypes.byref(a)), "bread_gguf_info")
+        return {"version": v.value, "n_tensors": nt.value, "n_kv": nk.value, "data_offset": off.value,
+                "alignment": a.value}
+
+    @staticmethod
+    def _t(t: _lib.GgufTensor) -> dict:
+        return {"name": t.name.decode(), "type": t.type, "dims": list(t.dims[: t.n_dims]), "offset": t.offset,
+                "size": t.size, "n_elems": t.n_elems, "data": t.data}
+
+    def tensor(self, i: int) -> dict:
+        t = _lib.GgufTensor()
+        check(lib.bread_gguf_tensor(self._h, i, ctypes.byref(t)), "bread_gguf_tensor")
+        return self._t(t)
+
+    def tensors(self) -> list:
+        return [self.tensor(i) for i in range(self.info()["n_tensors"])]
+
+    def find(self, name: str):
+        t = _lib.GgufTensor()
+        return self._t(t) if lib.bread_gguf_find(self._h, name.encode(), ctypes.byref(t)) == 0 else None
+
+    def kv_int(self, key: str):
+        v = ctypes.c_int64()
+        return v.value if lib.bread_gguf_kv_int(self._h, key.encode(), ctypes.byref(v)) == 0 else None
+
+    def kv_float(self, key: str):
+        v = ctypes.c_double()
+        return v.value if lib.bread_gguf_kv_float(self._h, key.encode(), ctypes.byref(v)) == 0 else None
+
+    def kv_str(self, key: str):
+        b = ctypes.create_string_buffer(4096)
+        return b.value.decode() if lib.bread_gguf_kv_str(self._h, key.encode(), b, 4096) == 0 else None
+
+    def moe_shape(self, layer: int) -> MoeShape:
+        sh = MoeShape()
+        check(lib.bread_gguf_moe_shape(self._h, layer, ctypes.byref(sh)), "bread_gguf_moe_shape")
+        return sh
+
+    def close(self) -> None:
+        if self._h:
+            lib.bread_gguf_close(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Arena:
     """All experts of n_layers layers resident in HBM (bread_arena_*)."""
 
@@ -226,8 +288,13 @@ class Arena:
         q(lib.bread_synth_q6k, d.down_shexp, b["down_sh"] // 210, sd["down_sh"])
         check(lib.bread_synth_normal_f32(ctypes.c_void_p(d.router), E * s.hidden, sd["router"], 0.0, router_std, st),
               "bread_synth_normal_f32")
-        check(lib.bread_synth_normal_f16(ctypes.c_void_p(d.shexp_gate), s.hidden, sd["shgate"], 0.0, shgate_std, st),
-              "bread_synth_normal_f16")
+        if d.shexp_gate:
+            check(lib.bread_synth_normal_f16(ctypes.c_void_p(d.shexp_gate), s.hidden, sd["shgate"], 0.0, shgate_std,
+                                             st), "bread_synth_normal_f16")
+
+    def load_gguf(self, l: int, g: "Gguf", gguf_layer: int) -> None:
+        """bread_arena_load_gguf: block gguf_layer's MoE tensors into layer l."""
+        check(lib.bread_arena_load_gguf(self._h, l, g._h, gguf_layer), "bread_arena_load_gguf")
 
     def set_router_column(self, l: int, col: int, values) -> None:
         """Overwrite column col of layer l's fp32 router [E][H] with values[E]

@@ -88,14 +88,21 @@ struct bread_moe_ctx {
     bread_grouped_ws gws;
 };
 
+// Per-layer arena flags: which optional tensors the layer holds.
+enum : int {
+    BREAD_ARENA_HAS_SHGATE = 1,  // fp16 shared-gate vector (otherwise logit 0)
+    BREAD_ARENA_HAS_NORM = 2,    // fp32 post-attention norm weight (otherwise unit)
+};
+
 struct bread_arena {
     bread_moe_shape_t shape;
     int n_layers;
     int device;
     uint64_t layer_bytes;
-    uint64_t off_gate, off_up, off_down, off_gate_sh, off_up_sh, off_down_sh, off_router, off_shgate;
+    uint64_t off_gate, off_up, off_down, off_gate_sh, off_up_sh, off_down_sh, off_router, off_shgate, off_norm;
     uint64_t gate_expert_bytes, up_expert_bytes, down_expert_bytes;
     uint8_t **layers;  // n_layers device allocations
+    int *flags;        // n_layers x BREAD_ARENA_HAS_*
 };
 
 int bread_validate_layer(const bread_moe_shape_t *s, const bread_moe_layer_t *L);

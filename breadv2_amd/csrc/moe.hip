@@ -53,6 +53,7 @@ extern "C" const char *bread_status_str(int status)
     case BREAD_ERR_NOMEM: return "out of memory";
     case BREAD_ERR_CAPACITY: return "more tokens than the context holds";
     case BREAD_ERR_DEVICE: return "device-side fault flagged by a kernel";
+    case BREAD_ERR_FORMAT: return "malformed model file";
     }
     return "unknown status";
 }

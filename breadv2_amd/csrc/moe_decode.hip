@@ -584,7 +584,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
     __shared__ Smem S;
     const int g = (int)blockIdx.x;
     const int tid = (int)threadIdx.x;
-    const int wid = wave_id(), lane = lane_id();
+    const int wid = wave_id();
     const int K = a.K, E = a.E;
     const int NU = 2 * (K + 1);   // down units
     bread_decode_sync *sy = a.sync;

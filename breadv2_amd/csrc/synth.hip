@@ -207,10 +207,13 @@ extern "C" int bread_arena_create(const bread_moe_shape_t *s, int n_layers, brea
     a->off_down_sh = o; o = align256(o + H * (Ish / QK) * Q6K_BYTES);
     a->off_router = o; o = align256(o + E * H * 4);
     a->off_shgate = o; o = align256(o + H * 2);
+    a->off_norm = o; o = align256(o + H * 4);
     a->layer_bytes = o;
     a->layers = (uint8_t **)calloc((size_t)n_layers, sizeof(uint8_t *));
+    a->flags = (int *)calloc((size_t)n_layers, sizeof(int));
     hipError_t e = hipGetDevice(&a->device);
-    if (!a->layers) e = hipErrorOutOfMemory;
+    if (!a->layers || !a->flags) e = hipErrorOutOfMemory;
+    for (int l = 0; l < n_layers && a->flags; l++) a->flags[l] = BREAD_ARENA_HAS_SHGATE;
     for (int l = 0; l < n_layers && e == hipSuccess; l++) e = hipMalloc((void **)&a->layers[l], a->layer_bytes);
     if (e != hipSuccess) {
         bread_arena_destroy(a);
@@ -227,6 +230,7 @@ extern "C" int bread_arena_destroy(bread_arena_t *a)
     if (a->layers)
         for (int l = 0; l < a->n_layers; l++) (void)hipFree(a->layers[l]);
     free(a->layers);
+    free(a->flags);
     free(a);
     return BREAD_OK;
 }
@@ -255,6 +259,7 @@ extern "C" int bread_arena_layer(const bread_arena_t *a, int layer, bread_moe_la
     L->gate_shexp_type = L->up_shexp_type = BREAD_QTYPE_Q4_K;
     L->down_shexp_type = BREAD_QTYPE_Q6_K;
     L->router = (const float *)(b + a->off_router);
-    L->shexp_gate = (const uint16_t *)(b + a->off_shgate);
+    L->shexp_gate = (a->flags[layer] & BREAD_ARENA_HAS_SHGATE) ? (const uint16_t *)(b + a->off_shgate) : nullptr;
+    L->post_norm_w = (a->flags[layer] & BREAD_ARENA_HAS_NORM) ? (const float *)(b + a->off_norm) : nullptr;
     return BREAD_OK;
 }

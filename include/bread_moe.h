@@ -57,7 +57,8 @@ typedef enum {
     BREAD_ERR_HIP = -5,        /* a HIP runtime call failed */
     BREAD_ERR_NOMEM = -6,      /* device or host allocation failed */
     BREAD_ERR_CAPACITY = -7,   /* more tokens than the context was created for */
-    BREAD_ERR_DEVICE = -8      /* a kernel reported a fault (see bread_moe_ctx_check) */
+    BREAD_ERR_DEVICE = -8,     /* a kernel reported a fault (see bread_moe_ctx_check) */
+    BREAD_ERR_FORMAT = -9      /* a model file is malformed (bread_gguf_open) */
 } bread_status_t;
 
 /* Text for a status code (static storage). */
@@ -255,10 +256,69 @@ typedef struct bread_arena bread_arena_t;
 
 int bread_arena_create(const bread_moe_shape_t *shape, int n_layers, bread_arena_t **out);
 int bread_arena_destroy(bread_arena_t *arena);
-/* Descriptor of layer `layer` (device pointers into the arena). */
+/* Descriptor of layer `layer` (device pointers into the arena); shexp_gate
+ * and post_norm_w are NULL when the layer holds no such tensor (a layer
+ * loaded from a file without them). */
 int bread_arena_layer(const bread_arena_t *arena, int layer, bread_moe_layer_t *out);
 /* Bytes of one layer's allocation. */
 uint64_t bread_arena_layer_bytes(const bread_arena_t *arena);
+
+/* ------------------------------------------------------------------ */
+/* GGUF model files                                                    */
+/* ------------------------------------------------------------------ */
+
+/* A parsed GGUF v2/v3 file: header, metadata and tensor index over a
+ * read-only mapping of the file (weights are not read until loaded).
+ * Replaces gguf_open / gguf_find_tensor / gguf_tensor_by_idx (gguf.c:306-411,
+ * gguf.h:100-127); a malformed file (bad magic or version, truncated
+ * records, tensor data beyond the end) returns BREAD_ERR_FORMAT instead of
+ * exiting. */
+typedef struct bread_gguf bread_gguf_t;
+
+typedef struct {
+    const char *name;     /* owned by the file handle */
+    uint32_t type;        /* ggml type id (0 F32, 1 F16, 8 Q8_0, 12 Q4_K, 14 Q6_K, ...) */
+    uint32_t n_dims;
+    uint64_t dims[4];     /* dims[0] innermost (columns) */
+    uint64_t offset;      /* from the start of the data section */
+    uint64_t size;        /* bytes (0 for a type this build has no size for) */
+    uint64_t n_elems;
+    const void *data;     /* host pointer into the mapping */
+} bread_gguf_tensor_t;
+
+int bread_gguf_open(const char *path, bread_gguf_t **out);
+int bread_gguf_close(bread_gguf_t *file);
+int bread_gguf_info(const bread_gguf_t *file, uint32_t *version, uint64_t *n_tensors, uint64_t *n_kv,
+                    uint64_t *data_offset, uint32_t *alignment);
+int bread_gguf_tensor(const bread_gguf_t *file, uint64_t index, bread_gguf_tensor_t *out);
+/* BREAD_ERR_ARG (without recording an error) when no tensor has this name. */
+int bread_gguf_find(const bread_gguf_t *file, const char *name, bread_gguf_tensor_t *out);
+/* Scalar metadata: integers and bools (any width, signed sign-extended),
+ * floats (f32/f64) and strings (copied NUL-terminated, cut to buf_len - 1
+ * bytes); BREAD_ERR_ARG when absent or of another kind.  Arrays are parsed
+ * and skipped. */
+int bread_gguf_kv_int(const bread_gguf_t *file, const char *key, int64_t *value);
+int bread_gguf_kv_float(const bread_gguf_t *file, const char *key, double *value);
+int bread_gguf_kv_str(const bread_gguf_t *file, const char *key, char *buf, size_t buf_len);
+/* Bytes of n_elems elements of a ggml type (ggml_tensor_nbytes, gguf.c:140);
+ * 0 for unknown types or a count that is not a whole number of blocks. */
+uint64_t bread_ggml_type_size(uint32_t type, uint64_t n_elems);
+
+/* MoE shape of block `layer` from its tensors (loader.c:160-206): hidden and
+ * expert intermediate from ffn_gate_exps [H, I, E], shared intermediate from
+ * ffn_gate_shexp, top_k from <arch>.expert_used_count and rms_eps from
+ * <arch>.attention.layer_norm_rms_epsilon when present (else 8 and 1e-6,
+ * bread.h). */
+int bread_gguf_moe_shape(const bread_gguf_t *file, int layer, bread_moe_shape_t *shape);
+
+/* Copies block `gguf_layer`'s MoE tensors into arena layer `arena_layer`:
+ * blk.N.ffn_{gate,up,down}_exps (Q4_K, Q4_K, Q6_K; experts at stride
+ * tensor.size / n_experts, loader.c:188-190), ffn_{gate,up,down}_shexp,
+ * ffn_gate_inp (F32 router) and, when present, ffn_gate_inp_shexp (F16) and
+ * post_attention_norm (F32), which bread_arena_layer then exposes as
+ * shexp_gate and post_norm_w.  Types and dimensions must match the arena's
+ * shape (BREAD_ERR_QTYPE / BREAD_ERR_SHAPE).  Synchronous. */
+int bread_arena_load_gguf(bread_arena_t *arena, int arena_layer, const bread_gguf_t *file, int gguf_layer);
 
 /* ------------------------------------------------------------------ */
 /* Seeded synthetic weights (bench and test inputs)                    */

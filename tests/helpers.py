@@ -71,8 +71,8 @@ def arena_host_layer(s, d) -> "O.HostLayer":
 def assert_moe_close(got, ref, base=None):
     """The north-star tolerance on a MoE-layer output: relative L2 < 1e-3 and
     max-abs < 1e-2.  `base` (the residual added before the layer) is removed
-    first so the check is on the layer's own contribution.  At BASELINE's
-    synthetic weight scale (d ~ U(1e-3, 1e-2), 6-bit scales) outputs reach
+    first so the check is on the layer's own contribution.  At the
+    benchmark's synthetic weight scale (d ~ U(1e-3, 1e-2), 6-bit scales) outputs reach
     1e5..1e6, where one fp32 ulp is 0.01..0.1, so the max-abs bound is applied
     to the output divided by its RMS; the unit-scale tests apply it raw."""
     got = np.asarray(got, np.float64)
@@ -89,7 +89,7 @@ def assert_moe_close(got, ref, base=None):
 
 def scale_layer_d(t, shift: int = 6) -> None:
     """Divide every superblock scale (d, dmin of Q4_K; d of Q6_K) of a device
-    layer by 2**shift in place (exact in fp16 for BASELINE's range), so the
+    layer by 2**shift in place (exact in fp16 for the synthetic scale range), so the
     layer's outputs are of order one."""
     import torch
 

@@ -38,7 +38,7 @@ def test_binding_covers_every_declared_symbol():
 
 
 def test_status_strings():
-    for code in range(-8, 1):
+    for code in range(-9, 1):
         assert B.status_str(code) and B.status_str(code) != "unknown status"
     assert B.status_str(-99) == "unknown status"
 
