@@ -366,6 +366,24 @@ class MoeContext:
                                     _p(gsh), _s(stream)), "bread_moe_forward")
         return idx, w, gsh
 
+    def forward_f16(self, layer: MoeLayer, hidden: torch.Tensor, normed: torch.Tensor, n_tokens: int,
+                    norm_w=None, want_routing: bool = False, stream=None):
+        """bread_moe_forward_f16: the MoE block on fp16 hidden / normed
+        [n_tokens][H] (one_layer.cu:1800-1986).  norm_w: a float32 device
+        tensor or raw device pointer (e.g. layer.post_norm_w); None takes
+        `normed` as the input instead of computing it."""
+        assert hidden.dtype == torch.float16 and normed.dtype == torch.float16
+        K = self.shape.top_k
+        idx = w = gsh = None
+        if want_routing:
+            idx = torch.empty((n_tokens, K), dtype=torch.int32, device=hidden.device)
+            w = torch.empty((n_tokens, K), dtype=torch.float32, device=hidden.device)
+            gsh = torch.empty((n_tokens,), dtype=torch.float32, device=hidden.device)
+        nw = norm_w if isinstance(norm_w, int) or norm_w is None else norm_w.data_ptr()
+        check(lib.bread_moe_forward_f16(self._h, ctypes.byref(layer), nw, _p(hidden), _p(normed), n_tokens, _p(idx),
+                                        _p(w), _p(gsh), _s(stream)), "bread_moe_forward_f16")
+        return idx, w, gsh
+
     def decode_layers(self, layers, hidden: torch.Tensor, want_routing: bool = False, stream=None):
         """bread_moe_decode_layers: one token through len(layers) layers,
         h <- h + MoE_l(RMSNorm(h) * w_l), in one launch."""

@@ -74,6 +74,7 @@ struct bread_moe_ctx {
     float *w;          // [max_tokens][K]
     float *gsh;        // [max_tokens]
     float *h;          // [max_tokens][K+1][Imax] SwiGLU outputs, slot 0 = shared
+    float *x32, *h32;  // [max_tokens][H] fp32 input and residual of the fp16-stream entry
     uint64_t *tlogits; // decode router logits, (epoch tag << 32) | fp32 bits, one per 64 B
     float *xbuf;       // decode layer outputs by parity, one 128 B record per workgroup
     float *hbuf;       // decode SwiGLU outputs by layer mod 3, one 128 B record per workgroup

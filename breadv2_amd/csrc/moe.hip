@@ -132,6 +132,8 @@ extern "C" int bread_moe_ctx_create(const bread_moe_shape_t *shape, int max_toke
     if (e == hipSuccess) e = hipMalloc((void **)&c->w, T * K * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->gsh, T * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->h, T * (K + 1) * Imax * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->x32, T * shape->hidden * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->h32, T * shape->hidden * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->tlogits, bread_decode_tlogit_words() * sizeof(uint64_t));
     if (e == hipSuccess) e = hipMalloc((void **)&c->xbuf, bread_decode_xbuf_floats() * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->hbuf, bread_decode_hbuf_floats() * sizeof(float));
@@ -165,6 +167,8 @@ extern "C" int bread_moe_ctx_destroy(bread_moe_ctx_t *c)
     (void)hipFree(c->w);
     (void)hipFree(c->gsh);
     (void)hipFree(c->h);
+    (void)hipFree(c->x32);
+    (void)hipFree(c->h32);
     (void)hipFree(c->tlogits);
     (void)hipFree(c->xbuf);
     (void)hipFree(c->hbuf);
@@ -323,6 +327,95 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, co
     for (int i = threadIdx.x; i < n; i += blockDim.x) ot[i] = xt[i] * inv * (w ? w[i] : 1.0f);
 }
 
+// The fp16 residual stream of one_layer_forward, in: per token, the fp32
+// residual copy h32 = hidden and the MoE input x32.  With norm_w, x32 is the
+// fp16-rounded post-attention RMSNorm output, also written to `normed` as
+// one_layer.cu:1812-1815 writes d_normed2 (x * rms * w in that order,
+// rms = 1/sqrt(mean(x^2) + eps)); without, `normed` is read.  H % 8 == 0.
+__global__ __launch_bounds__(256) void k_f16_in(const uint16_t *__restrict__ hidden, uint16_t *__restrict__ normed,
+                                                const float *__restrict__ norm_w, float *__restrict__ x32,
+                                                float *__restrict__ h32, int H, float eps)
+{
+    __shared__ float part[4];
+    const size_t base = (size_t)blockIdx.x * H;
+    const uint4 *hv = reinterpret_cast<const uint4 *>(hidden + base);
+    uint4 *nv = reinterpret_cast<uint4 *>(normed + base);
+    float4 *xo = reinterpret_cast<float4 *>(x32 + base);
+    float4 *ho = reinterpret_cast<float4 *>(h32 + base);
+    const int n8 = H / 8;
+    float inv = 1.0f;
+    if (norm_w) {
+        float ss = 0.f;
+        for (int v = threadIdx.x; v < n8; v += 256) {
+            const uint4 q = hv[v];
+            const uint32_t p[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float a = h2f(p[k]), b = h2f(p[k] >> 16);
+                ss = fmaf(a, a, ss);
+                ss = fmaf(b, b, ss);
+            }
+        }
+        ss = wave_sum(ss);
+        if (lane_id() == 0) part[threadIdx.x / WAVE] = ss;
+        __syncthreads();
+        inv = 1.0f / sqrtf((part[0] + part[1] + part[2] + part[3]) / (float)H + eps);
+    }
+    for (int v = threadIdx.x; v < n8; v += 256) {
+        const uint4 q = hv[v];
+        const uint32_t p[4] = {q.x, q.y, q.z, q.w};
+        float hf[8], xf[8];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            hf[2 * k] = h2f(p[k]);
+            hf[2 * k + 1] = h2f(p[k] >> 16);
+        }
+        uint4 n;
+        if (norm_w) {
+            const float4 w0 = reinterpret_cast<const float4 *>(norm_w)[2 * v];
+            const float4 w1 = reinterpret_cast<const float4 *>(norm_w)[2 * v + 1];
+            const float wf[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            uint32_t o[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t lo = f2h(hf[2 * k] * inv * wf[2 * k]);
+                const uint32_t hi = f2h(hf[2 * k + 1] * inv * wf[2 * k + 1]);
+                o[k] = lo | (hi << 16);
+            }
+            n = make_uint4(o[0], o[1], o[2], o[3]);
+            nv[v] = n;
+        } else {
+            n = nv[v];
+        }
+        const uint32_t np[4] = {n.x, n.y, n.z, n.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            xf[2 * k] = h2f(np[k]);
+            xf[2 * k + 1] = h2f(np[k] >> 16);
+        }
+        xo[2 * v] = make_float4(xf[0], xf[1], xf[2], xf[3]);
+        xo[2 * v + 1] = make_float4(xf[4], xf[5], xf[6], xf[7]);
+        ho[2 * v] = make_float4(hf[0], hf[1], hf[2], hf[3]);
+        ho[2 * v + 1] = make_float4(hf[4], hf[5], hf[6], hf[7]);
+    }
+}
+
+// ... and out: hidden = fp16(h32), round to nearest even, 8 values a thread.
+__global__ __launch_bounds__(256) void k_f16_out(const float *__restrict__ h32, uint16_t *__restrict__ hidden,
+                                                 size_t n8)
+{
+    const size_t v = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (v >= n8) return;
+    const float4 a = reinterpret_cast<const float4 *>(h32)[2 * v];
+    const float4 b = reinterpret_cast<const float4 *>(h32)[2 * v + 1];
+    uint4 o;
+    o.x = f2h(a.x) | ((uint32_t)f2h(a.y) << 16);
+    o.y = f2h(a.z) | ((uint32_t)f2h(a.w) << 16);
+    o.z = f2h(b.x) | ((uint32_t)f2h(b.y) << 16);
+    o.w = f2h(b.z) | ((uint32_t)f2h(b.w) << 16);
+    reinterpret_cast<uint4 *>(hidden)[v] = o;
+}
+
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
@@ -440,6 +533,34 @@ extern "C" int bread_moe_forward(bread_moe_ctx_t *c, const bread_moe_layer_t *L,
     if (idx) BREAD_HIP(hipMemcpyAsync(idx, c->idx, (size_t)T * K * sizeof(int32_t), hipMemcpyDeviceToDevice, st));
     if (w) BREAD_HIP(hipMemcpyAsync(w, c->w, (size_t)T * K * sizeof(float), hipMemcpyDeviceToDevice, st));
     if (gsh) BREAD_HIP(hipMemcpyAsync(gsh, c->gsh, (size_t)T * sizeof(float), hipMemcpyDeviceToDevice, st));
+    return BREAD_OK;
+}
+
+// The MoE block of one_layer_forward on its fp16 residual stream
+// (one_layer.cu:1800-1986): norm in, bread_moe_forward in fp32, one rounding out.
+extern "C" int bread_moe_forward_f16(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *norm_w,
+                                     uint16_t *hidden, uint16_t *normed, int T, int32_t *idx, float *w,
+                                     float *gsh, bread_stream_t stream)
+{
+    BREAD_REQUIRE(c && hidden && normed, BREAD_ERR_ARG, "NULL context, hidden or normed");
+    BREAD_REQUIRE(T >= 0, BREAD_ERR_ARG, "n_tokens < 0");
+    BREAD_REQUIRE(T <= c->max_tokens, BREAD_ERR_CAPACITY, "n_tokens > max_tokens of the context");
+    BREAD_REQUIRE((((uintptr_t)hidden | (uintptr_t)normed | (uintptr_t)norm_w) & 15) == 0, BREAD_ERR_ALIGN,
+                  "hidden, normed and norm_w must be 16-byte aligned");
+    int rc = bread_validate_layer(&c->shape, L);
+    if (rc) return rc;
+    if (T == 0) return BREAD_OK;
+    const int H = c->shape.hidden;
+    hipStream_t st = to_hip(stream);
+    bread_clear_stale_error();
+    hipLaunchKernelGGL(k_f16_in, dim3(T), dim3(256), 0, st, hidden, normed, norm_w, c->x32, c->h32, H,
+                       c->shape.rms_eps);
+    BREAD_HIP(hipGetLastError());
+    rc = bread_moe_forward(c, L, c->x32, c->h32, T, idx, w, gsh, stream);
+    if (rc) return rc;
+    const size_t n8 = (size_t)T * H / 8;
+    hipLaunchKernelGGL(k_f16_out, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, c->h32, hidden, n8);
+    BREAD_HIP(hipGetLastError());
     return BREAD_OK;
 }
 

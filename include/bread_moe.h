@@ -207,6 +207,22 @@ int bread_moe_forward(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer,
                       const float *d_x_normed, float *d_hidden, int n_tokens,
                       int32_t *d_idx, float *d_w, float *d_gsh, bread_stream_t stream);
 
+/* The MoE block of one_layer_forward on the reference's fp16 residual stream
+ * (one_layer.cu:1800-1986, the d_hidden / d_normed2 interface of :1812-1815).
+ * hidden and normed are fp16 [n_tokens][H], 16-byte aligned.
+ *   norm_w != NULL (fp32 [H]): normed[t] = fp16(hidden[t] * rms * norm_w),
+ *     rms = 1/sqrt(mean(hidden[t]^2) + shape.rms_eps), written to `normed` as
+ *     the reference writes d_normed2;  norm_w == NULL: `normed` is the input.
+ *   hidden[t] = fp16(float(hidden[t]) + MoE(float(normed[t])))
+ * The block runs in fp32 exactly as bread_moe_forward (same paths) and is
+ * rounded to fp16 once; the reference rounds after the shared expert and
+ * after each routed expert, and keeps gate/up/SwiGLU/down results in fp16.
+ * Values beyond fp16's range become +-Inf, as in the reference.  Optional
+ * routing outputs as in bread_moe_forward. */
+int bread_moe_forward_f16(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer, const float *norm_w,
+                          uint16_t *hidden, uint16_t *normed, int n_tokens,
+                          int32_t *d_idx, float *d_w, float *d_gsh, bread_stream_t stream);
+
 /* One decode token through a stack of MoE layers in a single launch:
  *   for l < n_layers:  x = RMSNorm(hidden) * layers[l].post_norm_w  (eps = shape.rms_eps);
  *                      hidden += MoE_l(x)
