@@ -191,6 +191,69 @@ def lm_head(steps: int):
     return out
 
 
+VERIFY_B = (5, 9, 17)
+
+
+def verify(arena, s, rounds: int, stream):
+    """Speculative verification at the MoE boundary: a round of B tokens (the
+    confirmed token and B - 1 drafts) through all 40 resident layers with one
+    grouped call per layer (bread_moe_stack_forward), then the greedy head
+    (output RMSNorm, Q4_K lm_head 248,320 x 2048 through bread_matvec per
+    token, device argmax).  Compared with the reference's order: B rounds of
+    one token (the decode stack launch, then the head)."""
+    import torch
+
+    import breadv2_amd as B
+    from breadv2_amd import api
+
+    H, V = s.hidden, 248_320
+    layers = [arena.layer(l) for l in range(arena.n_layers)]
+    w = torch.empty(V * H // 256 * 144, dtype=torch.uint8, device="cuda:0")
+    api.synth_q4k(w, V * H // 256, 77)
+    nw = torch.ones(H, device="cuda:0")
+    ctx = B.MoeContext(s, max_tokens=max(VERIFY_B))
+    g = torch.Generator(device="cuda:0").manual_seed(5)
+    out = []
+    with torch.cuda.stream(stream):
+        for Bn in VERIFY_B:
+            h0 = torch.randn(Bn, H, device="cuda:0", generator=g)
+
+            def batched():
+                h = h0.clone()
+                ctx.stack_forward(layers, h, Bn, stream=stream)
+                ctx.greedy_head(h, nw, w, api.QTYPE_Q4_K, V, Bn, stream=stream)
+
+            def sequential():
+                for t in range(Bn):
+                    h = h0[t:t + 1].clone()
+                    ctx.stack_forward(layers, h, 1, stream=stream)
+                    ctx.greedy_head(h, nw, w, api.QTYPE_Q4_K, V, 1, stream=stream)
+
+            res = {}
+            for name, fn in (("batched", batched), ("token_by_token", sequential)):
+                fn()
+                torch.cuda.synchronize()
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(rounds):
+                    fn()
+                e1.record(stream)
+                torch.cuda.synchronize()
+                res[name] = e0.elapsed_time(e1) * 1e3 / rounds
+            if ctx.check_device():
+                raise RuntimeError("verify round flagged a device error")
+            out.append({"tokens_per_round": Bn, "drafts": Bn - 1, "layers": len(layers),
+                        "us_per_round": round(res["batched"], 1),
+                        "us_per_round_token_by_token": round(res["token_by_token"], 1),
+                        "speedup": round(res["token_by_token"] / res["batched"], 2),
+                        "verified_tok_s": round(Bn / res["batched"] * 1e6, 1)})
+            log(f"verify B={Bn}: {res['batched']:.0f} us/round vs {res['token_by_token']:.0f} token by token")
+    ctx.close()
+    del w
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -365,6 +428,11 @@ def main() -> int:
         }
     if args.mt_steps > 0:
         result["lm_head"] = {"entry": "bread_matvec (fp16 x/y)", "cases": lm_head(20)}
+    if args.mt_steps > 0 and L >= 40:
+        result["verify"] = {
+            "entry": "bread_moe_stack_forward + bread_moe_greedy_head per round of B tokens",
+            "cases": verify(arena, s, 5, stream),
+        }
     if not args.no_cpu:
         res, threads, cores = cpu_baseline(arena, s, args.cpu_seconds)
         v, n, el = res[threads]

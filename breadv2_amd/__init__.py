@@ -10,6 +10,7 @@ from .api import (  # noqa: F401
     Gguf,
     LayerTensors,
     MoeContext,
+    argmax_f16,
     bread_dequant_rows,
     bread_matvec,
     bread_matvec_f32,
@@ -18,5 +19,6 @@ from .api import (  # noqa: F401
     row_bytes,
     shape,
     shape_bytes,
+    spec_accept,
     synth_layer_tensors,
 )

@@ -131,6 +131,19 @@ SIGNATURES = {
         c_int,
         [c_void_p, POINTER(MoeLayer), c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p],
     ),
+    "bread_moe_stack_forward": (
+        c_int,
+        [c_void_p, POINTER(MoeLayer), c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p],
+    ),
+    "bread_moe_greedy_head": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p],
+    ),
+    "bread_argmax_f16": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p]),
+    "bread_spec_accept": (
+        c_int,
+        [POINTER(c_int32), POINTER(c_int32), c_int, c_int32, c_int, POINTER(c_int), POINTER(c_int32)],
+    ),
     "bread_moe_decode_layers": (
         c_int, [c_void_p, POINTER(MoeLayer), c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "bread_moe_ctx_set_trace": (c_int, [c_void_p, c_void_p, ctypes.c_size_t, POINTER(c_int)]),

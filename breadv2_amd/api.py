@@ -189,6 +189,28 @@ def synth_layer_tensors(s: MoeShape, seed: int, layer: int = 0, router_std: floa
     return t
 
 
+def argmax_f16(logits: torch.Tensor, stream=None) -> torch.Tensor:
+    """bread_argmax_f16 over the rows of a 2-d fp16 device tensor."""
+    assert logits.dtype == torch.float16 and logits.dim() == 2 and logits.is_contiguous()
+    out = torch.empty((logits.shape[0],), dtype=torch.int32, device=logits.device)
+    check(lib.bread_argmax_f16(_p(logits), logits.shape[1], logits.shape[0], _p(out), _s(stream)),
+          "bread_argmax_f16")
+    return out
+
+
+def spec_accept(pred, draft, eos: int, max_accept: int):
+    """bread_spec_accept on host lists: (n_accept, next token)."""
+    pred = list(pred)
+    draft = list(draft)
+    assert len(pred) == len(draft) + 1
+    pa = (ctypes.c_int32 * len(pred))(*pred)
+    da = (ctypes.c_int32 * max(1, len(draft)))(*draft)
+    na, nx = ctypes.c_int(), ctypes.c_int32()
+    check(lib.bread_spec_accept(pa, da, len(draft), eos, max_accept, ctypes.byref(na), ctypes.byref(nx)),
+          "bread_spec_accept")
+    return na.value, nx.value
+
+
 class Gguf:
     """A parsed GGUF v2/v3 file (bread_gguf_*): metadata and tensor index over
     a read-only mapping; weights are read when loaded into an Arena."""
@@ -398,6 +420,31 @@ class MoeContext:
         check(lib.bread_moe_decode_layers(self._h, arr, n, _p(hidden), _p(idx), _p(w), _p(gsh), _s(stream)),
               "bread_moe_decode_layers")
         return idx, w, gsh
+
+    def stack_forward(self, layers, hidden: torch.Tensor, n_tokens: int, want_routing: bool = False, stream=None):
+        """bread_moe_stack_forward: n_tokens tokens through len(layers) MoE
+        layers, h <- h + MoE_l(RMSNorm(h) * w_l), one grouped call per layer."""
+        n = len(layers)
+        arr = (MoeLayer * n)(*layers)
+        K = self.shape.top_k
+        idx = w = gsh = None
+        if want_routing:
+            idx = torch.empty((n, n_tokens, K), dtype=torch.int32, device=hidden.device)
+            w = torch.empty((n, n_tokens, K), dtype=torch.float32, device=hidden.device)
+            gsh = torch.empty((n, n_tokens), dtype=torch.float32, device=hidden.device)
+        check(lib.bread_moe_stack_forward(self._h, arr, n, _p(hidden), n_tokens, _p(idx), _p(w), _p(gsh),
+                                          _s(stream)), "bread_moe_stack_forward")
+        return idx, w, gsh
+
+    def greedy_head(self, hidden: torch.Tensor, norm_w: torch.Tensor | None, w_out: torch.Tensor, qtype: int,
+                    vocab: int, n_tokens: int, stream=None):
+        """bread_moe_greedy_head: (tokens int32 [n_tokens], fp16 logits
+        [n_tokens][vocab]) of the output norm + lm_head + greedy argmax."""
+        logits = torch.empty((n_tokens, vocab), dtype=torch.float16, device=hidden.device)
+        tokens = torch.empty((n_tokens,), dtype=torch.int32, device=hidden.device)
+        check(lib.bread_moe_greedy_head(self._h, _p(hidden), _p(norm_w), _p(w_out), qtype, vocab, n_tokens,
+                                        _p(logits), _p(tokens), _s(stream)), "bread_moe_greedy_head")
+        return tokens, logits
 
     def set_trace(self, buf: torch.Tensor | None) -> int:
         """Record the decode kernel's timeline into buf (int64 device tensor)."""

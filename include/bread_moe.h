@@ -223,6 +223,47 @@ int bread_moe_forward_f16(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer, 
                           uint16_t *hidden, uint16_t *normed, int n_tokens,
                           int32_t *d_idx, float *d_w, float *d_gsh, bread_stream_t stream);
 
+/* ------------------------------------------------------------------ */
+/* Batched speculative verification                                     */
+/* ------------------------------------------------------------------ */
+
+/* n_tokens tokens through a stack of MoE layers:
+ *   for l < n_layers:  x = RMSNorm(hidden) * layers[l].post_norm_w  (NULL: unit);
+ *                      hidden += MoE_l(x)
+ * one bread_moe_forward per layer for all tokens (the grouped path), or one
+ * bread_moe_decode_layers launch for a single token.  Replaces the
+ * token-by-token verification of main_speculative.cu:477-497 (one
+ * bread_step per draft token) at the MoE boundary: the B = K + 1 tokens of a
+ * round share each layer's expert reads.  d_hidden fp32 [n_tokens][H] in/out;
+ * optional routing outputs [n_layers][n_tokens][K] / [n_layers][n_tokens]. */
+int bread_moe_stack_forward(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layers, int n_layers,
+                            float *d_hidden, int n_tokens, int32_t *d_idx, float *d_w, float *d_gsh,
+                            bread_stream_t stream);
+
+/* Greedy prediction per token (main.cu:282-335, bc_output_norm / bc_logits /
+ * bc_greedy): x = fp16(RMSNorm(hidden) * norm_w), logits = bread_matvec(w_out,
+ * x) as fp16 [n_tokens][vocab], tokens[t] = greedy_sample's argmax (first
+ * index of the largest logit; NaN logits skipped; 0 when logits[0] is NaN).
+ * hidden fp32 [n_tokens][H]; vocab a multiple of 8; all device buffers. */
+int bread_moe_greedy_head(bread_moe_ctx_t *ctx, const float *d_hidden, const float *d_norm_w,
+                          const void *d_w_out, int qtype, int vocab, int n_tokens, uint16_t *d_logits,
+                          int32_t *d_tokens, bread_stream_t stream);
+
+/* greedy_sample's argmax (main.cu:326-335) over n_tokens rows of n fp16
+ * logits, on the device. */
+int bread_argmax_f16(const uint16_t *d_logits, int n, int n_tokens, int32_t *d_out, bread_stream_t stream);
+
+/* The acceptance rule of main_speculative.cu:477-497, on host arrays.
+ * pred[i] is the target's greedy prediction after token i of the round
+ * (i = 0: the last confirmed token, i >= 1: draft i-1), n_draft + 1 entries.
+ * Drafts are accepted while equal to the running prediction and not eos, at
+ * most max_accept (>= 1: the tokens the caller may still output).  *next is
+ * the prediction at the first mismatch or after the last draft (the bonus
+ * token and the next round's seed); when the budget ends the run it is the
+ * last accepted draft, since the reference stops stepping there. */
+int bread_spec_accept(const int32_t *pred, const int32_t *draft, int n_draft, int32_t eos, int max_accept,
+                      int *n_accept, int32_t *next);
+
 /* One decode token through a stack of MoE layers in a single launch:
  *   for l < n_layers:  x = RMSNorm(hidden) * layers[l].post_norm_w  (eps = shape.rms_eps);
  *                      hidden += MoE_l(x)

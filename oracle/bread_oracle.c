@@ -551,6 +551,44 @@ void oracle_moe_forward(const oracle_shape_t *s, const oracle_layer_t *L, const 
     }
 }
 
+/* main.cu:326-335 */
+int oracle_greedy_f16(const uint16_t *logits, int n)
+{
+    int best_id = 0;
+    float best_val = oracle_h2f(logits[0]);
+    for (int i = 1; i < n; i++) {
+        const float v = oracle_h2f(logits[i]);
+        if (v > best_val) {
+            best_val = v;
+            best_id = i;
+        }
+    }
+    return best_id;
+}
+
+/* main_speculative.cu:474-510, the body of the verification loop. */
+int oracle_spec_round(const int32_t *pred, const int32_t *draft, int n_drafted, int32_t eos, int total_gen,
+                      int max_tokens, int32_t *next, int *out_gen)
+{
+    int step = 0;                       /* bread_step calls made so far */
+    int32_t target_pred = pred[step++]; /* bread_step(confirmed_tok) */
+    int n_accept = 0;
+    for (int i = 0; i < n_drafted; i++) {
+        if (target_pred == draft[i] && target_pred != eos) {
+            n_accept++;
+            total_gen++;
+            if (total_gen >= max_tokens) break;
+            target_pred = pred[step++]; /* bread_step(draft[i]) */
+        } else {
+            break;
+        }
+    }
+    if (total_gen < max_tokens && target_pred != eos) total_gen++; /* bonus token */
+    *next = target_pred;
+    *out_gen = total_gen;
+    return n_accept;
+}
+
 int oracle_online_cores(void)
 {
     return (int)sysconf(_SC_NPROCESSORS_ONLN);

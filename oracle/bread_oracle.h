@@ -106,6 +106,19 @@ void oracle_moe_forward(const oracle_shape_t *s, const oracle_layer_t *L, const 
                         float *hidden, int n_tokens, int *idx, float *w, float *gsh,
                         int nthreads);
 
+/* greedy_sample (main.cu:326-335): argmax over n fp16 logits, best starts at
+ * logits[0] and moves only on a strictly greater value. */
+int oracle_greedy_f16(const uint16_t *logits, int n);
+
+/* One verification round of main_speculative.cu:468-510 with bread_step
+ * replaced by a lookup: pred[i] is the target's prediction after token i of
+ * the round (0: the confirmed token, i >= 1: draft i-1).  total_gen and
+ * max_tokens are the loop's counters; returns the accepted count, sets
+ * *next (confirmed_tok after the round) and *out_gen (total_gen after it,
+ * bonus token included). */
+int oracle_spec_round(const int32_t *pred, const int32_t *draft, int n_drafted, int32_t eos, int total_gen,
+                      int max_tokens, int32_t *next, int *out_gen);
+
 /* Online core count and affinity-mask size, for the baseline report. */
 int oracle_online_cores(void);
 int oracle_affinity_cores(void);

@@ -61,6 +61,10 @@ _lib.oracle_moe_token_mt.argtypes = [POINTER(OShape), POINTER(OLayer), c_void_p,
                                      c_void_p, c_int]
 _lib.oracle_moe_forward.argtypes = [POINTER(OShape), POINTER(OLayer), c_void_p, c_void_p, c_int, c_void_p,
                                     c_void_p, c_void_p, c_int]
+_lib.oracle_greedy_f16.restype = c_int
+_lib.oracle_greedy_f16.argtypes = [c_void_p, c_int]
+_lib.oracle_spec_round.restype = c_int
+_lib.oracle_spec_round.argtypes = [c_void_p, c_void_p, c_int, ctypes.c_int32, c_int, c_int, c_void_p, c_void_p]
 _lib.oracle_online_cores.restype = c_int
 _lib.oracle_affinity_cores.restype = c_int
 
@@ -234,3 +238,20 @@ def ref_dequant_lib():
     lib.dequant_q4k_block_cpu.argtypes = [c_void_p, c_void_p]
     lib.dequant_q6k_block_cpu.argtypes = [c_void_p, c_void_p]
     return lib
+
+
+def greedy_f16(logits16: np.ndarray) -> int:
+    """greedy_sample (main.cu:326-335) over one row of fp16 logits."""
+    a = np.ascontiguousarray(logits16, np.float16)
+    return int(_lib.oracle_greedy_f16(_ptr(a.view(np.uint16)), a.size))
+
+
+def spec_round(pred, draft, eos: int, total_gen: int, max_tokens: int):
+    """One verification round (main_speculative.cu:474-510): returns
+    (n_accept, next confirmed token, total_gen after the round)."""
+    p = np.ascontiguousarray(pred, np.int32)
+    d = np.ascontiguousarray(draft if len(draft) else [0], np.int32)
+    nx = np.zeros(1, np.int32)
+    g = np.zeros(1, np.int32)
+    a = _lib.oracle_spec_round(_ptr(p), _ptr(d), len(draft), eos, total_gen, max_tokens, _ptr(nx), _ptr(g))
+    return int(a), int(nx[0]), int(g[0])
