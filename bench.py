@@ -118,8 +118,8 @@ def multi_token(arena, s, steps: int, stream):
     out = []
     for name, T, zipf in MT_CASES:
         layers = [arena.layer(l + (32 if zipf else 24)) for l in range(8)]
-        ctx = B.MoeContext(s, max_tokens=T)
-        ctx.set_path(api.PATH_GROUPED)
+        ctx = B.MoeContext(s, max_tokens=T)  # automatic path choice
+        path = "small-batch" if T <= B.lib.bread_small_auto_tokens() else "grouped"
         g = torch.Generator(device="cuda:0").manual_seed(T)
         x = torch.randn(T, H, device="cuda:0", generator=g)
         if zipf:
@@ -145,11 +145,12 @@ def multi_token(arena, s, steps: int, stream):
         nbytes = U * EXPERT_BYTES + EXPERT_BYTES + 2_097_152 + 4_096 + 2 * T * H * 4
         flops = 9 * T * 6_291_456 + T * 1_048_576
         out.append({
-            "workload": name, "tokens": T, "us_per_layer": round(us, 1), "tok_s": round(T / us * 1e6, 1),
+            "workload": name, "path": path, "tokens": T, "us_per_layer": round(us, 1),
+            "tok_s": round(T / us * 1e6, 1),
             "distinct_experts": round(U, 1), "algorithmic_bytes": int(nbytes),
             "hbm_gbs": round(nbytes / us / 1e3, 1), "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
             "algorithmic_flops": flops, "tflops": round(flops / us / 1e6, 2),
-            "mfma_util": round(flops / us / 1e6 / MFMA_F16_PEAK_TFS, 4),
+            "mfma_util": round(flops / us / 1e6 / MFMA_F16_PEAK_TFS, 4) if path == "grouped" else None,
         })
         log(f"{name}: {us:.1f} us/layer, {T / us * 1e6:.0f} tok/s, U={U:.1f}")
         ctx.close()
@@ -420,7 +421,8 @@ def main() -> int:
         }
     if args.mt_steps > 0 and L >= 40:
         result["multi_token"] = {
-            "path": "grouped (tokens bucketed by expert, fp16 MFMA expert GEMMs, fp32 accumulate)",
+            "path": "automatic: small-batch (2..8 tokens: selected experts' rows over the whole GPU, fp32 dots) or "
+                    "grouped (tokens bucketed by expert, fp16 MFMA expert GEMMs, fp32 accumulate)",
             "mfma_peak_tflops": MFMA_F16_PEAK_TFS,
             "flops_note": "algorithmic: 9 x 6,291,456 per token (8 routed + shared) + router 1,048,576; "
                           "executed MFMA work is higher (32-pair tiles padded, activations as hi+lo fp16)",

@@ -33,6 +33,7 @@ PATH_AUTO = 0
 PATH_DECODE = 1
 PATH_GROUPED = 2
 PATH_PER_TOKEN = 3
+PATH_SMALL = 4
 
 QK_K = 256
 Q4K_BLOCK_BYTES = 144
@@ -148,6 +149,7 @@ SIGNATURES = {
         c_int, [c_void_p, POINTER(MoeLayer), c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "bread_moe_ctx_set_trace": (c_int, [c_void_p, c_void_p, ctypes.c_size_t, POINTER(c_int)]),
     "bread_moe_ctx_set_path": (c_int, [c_void_p, c_int]),
+    "bread_small_auto_tokens": (c_int, []),
     "bread_rmsnorm_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_void_p]),
     "bread_arena_create": (c_int, [POINTER(MoeShape), c_int, POINTER(c_void_p)]),
     "bread_arena_destroy": (c_int, [c_void_p]),

@@ -23,6 +23,7 @@ PATH_AUTO = _lib.PATH_AUTO
 PATH_DECODE = _lib.PATH_DECODE
 PATH_GROUPED = _lib.PATH_GROUPED
 PATH_PER_TOKEN = _lib.PATH_PER_TOKEN
+PATH_SMALL = _lib.PATH_SMALL
 
 
 def _p(t: torch.Tensor | None):
@@ -354,7 +355,7 @@ class MoeContext:
         return self._h
 
     def set_path(self, path: int) -> None:
-        """bread_moe_ctx_set_path: PATH_AUTO, PATH_DECODE, PATH_GROUPED or PATH_PER_TOKEN."""
+        """bread_moe_ctx_set_path: PATH_AUTO, PATH_DECODE, PATH_GROUPED, PATH_PER_TOKEN or PATH_SMALL."""
         check(lib.bread_moe_ctx_set_path(self._h, path), "bread_moe_ctx_set_path")
 
     def route(self, layer: MoeLayer, x: torch.Tensor, n_tokens: int, stream=None):

@@ -60,6 +60,14 @@ struct bread_grouped_ws {
     int *hexp = nullptr;                  // their row scale exponents [max_tokens*(K+1)]
 };
 
+struct bread_small_ws {
+    int32_t *slot_expert = nullptr;  // expert of each slot (-1: shared) [min(T K, E) + 1]
+    int32_t *slot_cnt = nullptr;     // pairs of each slot
+    int32_t *slot_pair = nullptr;    // pair ids of each slot in token order [slots][T]
+    int32_t *n_slots = nullptr;
+    float *eo = nullptr;             // expert outputs by pair [T (K+1)][H]
+};
+
 struct bread_moe_ctx {
     bread_moe_shape_t shape;
     int path;          // BREAD_PATH_*
@@ -87,6 +95,7 @@ struct bread_moe_ctx {
     uint64_t *trace;   // optional decode timeline (device), trace_words entries
     size_t trace_words;
     bread_grouped_ws gws;
+    bread_small_ws sws;
 };
 
 // Per-layer arena flags: which optional tensors the layer holds.
@@ -119,6 +128,12 @@ void bread_grouped_free(bread_moe_ctx_t *ctx);
 bool bread_grouped_supported(const bread_moe_shape_t &s, const bread_moe_layer_t *L);
 int bread_launch_moe_grouped(bread_moe_ctx_t *ctx, const bread_moe_layer_t *L, const float *x, float *hidden,
                              int n_tokens, hipStream_t st);
+int bread_small_alloc(bread_moe_ctx_t *ctx);
+void bread_small_free(bread_moe_ctx_t *ctx);
+bool bread_small_supported(const bread_moe_shape_t &s, const bread_moe_layer_t *L);
+int bread_small_max_tokens();
+int bread_launch_moe_small(bread_moe_ctx_t *ctx, const bread_moe_layer_t *L, const float *x, float *hidden,
+                           int n_tokens, hipStream_t st);
 int bread_launch_moe_decode(bread_moe_ctx_t *ctx, const bread_moe_layer_t *L, const float *x,
                             float *hidden, hipStream_t st);
 int bread_launch_decode_layers(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layers, int n, float *hidden,

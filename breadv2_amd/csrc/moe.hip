@@ -149,6 +149,10 @@ extern "C" int bread_moe_ctx_create(const bread_moe_shape_t *shape, int max_toke
         const int grc = bread_grouped_alloc(c);
         if (grc != BREAD_OK) e = grc == BREAD_ERR_NOMEM ? hipErrorOutOfMemory : hipErrorUnknown;
     }
+    if (e == hipSuccess) {
+        const int src = bread_small_alloc(c);
+        if (src != BREAD_OK) e = src == BREAD_ERR_NOMEM ? hipErrorOutOfMemory : hipErrorUnknown;
+    }
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         bread_moe_ctx_destroy(c);
@@ -175,6 +179,7 @@ extern "C" int bread_moe_ctx_destroy(bread_moe_ctx_t *c)
     (void)hipFree(c->dsync);
     (void)hipFree(c->d_layers);
     bread_grouped_free(c);
+    bread_small_free(c);
     free(c->h_layers);
     delete c;
     return BREAD_OK;
@@ -200,7 +205,7 @@ extern "C" int bread_moe_ctx_check(bread_moe_ctx_t *c, int *device_error)
 extern "C" int bread_moe_ctx_set_path(bread_moe_ctx_t *c, int path)
 {
     BREAD_REQUIRE(c, BREAD_ERR_ARG, "NULL context");
-    BREAD_REQUIRE(path >= BREAD_PATH_AUTO && path <= BREAD_PATH_PER_TOKEN, BREAD_ERR_ARG, "unknown path");
+    BREAD_REQUIRE(path >= BREAD_PATH_AUTO && path <= BREAD_PATH_SMALL, BREAD_ERR_ARG, "unknown path");
     c->path = path;
     return BREAD_OK;
 }
@@ -523,8 +528,13 @@ extern "C" int bread_moe_forward(bread_moe_ctx_t *c, const bread_moe_layer_t *L,
     case BREAD_PATH_PER_TOKEN:
         rc = bread_launch_moe_multi(c, L, x, hidden, T, st);
         break;
+    case BREAD_PATH_SMALL:
+        rc = bread_launch_moe_small(c, L, x, hidden, T, st);
+        if (rc == BREAD_ERR_SHAPE) return bread_fail(rc, "bread_moe_forward", "shape not supported by the small-batch path");
+        break;
     default:
         rc = (T == 1) ? bread_launch_moe_decode(c, L, x, hidden, st) : BREAD_ERR_SHAPE;
+        if (rc == BREAD_ERR_SHAPE && T <= bread_small_auto_tokens()) rc = bread_launch_moe_small(c, L, x, hidden, T, st);
         if (rc == BREAD_ERR_SHAPE) rc = bread_launch_moe_grouped(c, L, x, hidden, T, st);
         if (rc == BREAD_ERR_SHAPE) rc = bread_launch_moe_multi(c, L, x, hidden, T, st);
     }

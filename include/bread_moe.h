@@ -159,10 +159,13 @@ typedef enum {
     BREAD_PATH_AUTO = 0,
     BREAD_PATH_DECODE = 1,     /* persistent single-token kernel */
     BREAD_PATH_GROUPED = 2,    /* expert-bucketed grouped GEMMs (MFMA) */
-    BREAD_PATH_PER_TOKEN = 3   /* one wave per (token, row) GEMV kernels */
+    BREAD_PATH_PER_TOKEN = 3,  /* one wave per (token, row) GEMV kernels */
+    BREAD_PATH_SMALL = 4       /* 2..32 tokens: selected experts' rows over the whole GPU, fp32 dots */
 } bread_moe_path_t;
 
 int bread_moe_ctx_set_path(bread_moe_ctx_t *ctx, int path);
+/* Largest n_tokens the automatic choice sends to the small-batch path. */
+int bread_small_auto_tokens(void);
 
 /* Synchronises the context's last stream and returns BREAD_ERR_DEVICE (and
  * the kernel's error word in *device_error, if given) when a kernel flagged
@@ -199,7 +202,10 @@ int bread_route_layer(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer, cons
  * d_hidden fp32 [n_tokens][H] in/out.  Optional outputs d_idx/d_w/d_gsh as in
  * bread_route (may be NULL).  Path (bread_moe_ctx_set_path, default
  * BREAD_PATH_AUTO): n_tokens == 1 runs the persistent decode kernel when the
- * shape allows it (see bread_moe_decode_layers); larger batches run the
+ * shape allows it (see bread_moe_decode_layers); small batches (up to
+ * bread_small_auto_tokens()) run the small-batch path (each selected expert's
+ * rows streamed once over the whole GPU and dotted with the tokens that chose
+ * it, fp32; H <= 2048, intermediate sizes 256 or 512); larger batches run the
  * grouped path (tokens bucketed by expert, expert GEMMs on the matrix cores
  * with fp16 operands and fp32 accumulation; intermediate sizes <= 512 and
  * 16-byte aligned Q6_K down weights); other shapes run the per-token path. */
