@@ -448,16 +448,31 @@ __global__ __launch_bounds__(1024) void k_mt_bucket(const int32_t *__restrict__ 
 // (same lane layout), which apply the SwiGLU (layer_ops.cu:214-220).
 // ---------------------------------------------------------------------------
 
+// Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its
+// own L2.  The C chunks (row blocks) of one M-tile read the same activation
+// rows, so they are given linear ids L with the same L mod 8: one L2 fetches
+// the tile's activations for all of them.  L = 8 q + x gives tile
+// 8 (q / C) + x and chunk q mod C, a bijection onto the tiles padded to a
+// multiple of 8.
+__device__ __forceinline__ void xcd_tile(int C, int &tile, int &chunk)
+{
+    const int L = (int)blockIdx.x;
+    const int q = L >> 3;
+    tile = (q / C) * 8 + (L & 7);
+    chunk = q % C;
+}
+
 __global__ __launch_bounds__(GU_WAVES * WAVE, 2) void k_mt_gateup(const MtArgs a)
 {
     __shared__ uint4 sA[2][2][1024];  // [buffer][hi, lo][unit (s, g, n)]
     __shared__ int stok[MT], sexp[MT];
-    const int tile = blockIdx.x;
+    int tile, chunk;
+    xcd_tile(a.Imax / GU_ROWS, tile, chunk);
     if (tile >= *a.n_tiles) return;
     const MtTile tl = a.tiles[tile];
     const bool sh = tl.e == a.E;
     const int I = sh ? a.Ish : a.I;
-    const int n0 = blockIdx.y * GU_ROWS;
+    const int n0 = chunk * GU_ROWS;
     if (n0 >= I) return;
     const int tid = threadIdx.x, w = wave_id(), lane = lane_id();
     const bool up = w >= GU_WAVES / 2;
@@ -623,12 +638,13 @@ __global__ __launch_bounds__(DN_WAVES * WAVE, 2) void k_mt_down(const MtArgs a)
 {
     __shared__ uint4 sA[2][(MAX_INTER / 8) * MT];  // [hi, lo][unit ((16b + t)*2 + g)*32 + n]
     __shared__ int sexp[MT];
-    const int tile = blockIdx.x;
+    int tile, chunk;
+    xcd_tile((a.H + DN_ROWS - 1) / DN_ROWS, tile, chunk);
     if (tile >= *a.n_tiles) return;
     const MtTile tl = a.tiles[tile];
     const bool sh = tl.e == a.E;
     const int I = sh ? a.Ish : a.I;
-    const int n0 = blockIdx.y * DN_ROWS;
+    const int n0 = chunk * DN_ROWS;
     const int tid = threadIdx.x, w = wave_id(), lane = lane_id();
     const int g = lane >> 5, r = lane & 31;
     const int nb = I / QK;
@@ -868,13 +884,14 @@ int bread_launch_moe_grouped(bread_moe_ctx_t *c, const bread_moe_layer_t *L, con
     a.hexp = g.hexp;
     a.eo = g.eo;
     const int nt = max_tiles(s, T);
-    hipLaunchKernelGGL(k_mt_gateup, dim3(nt, Imax / GU_ROWS), dim3(GU_WAVES * WAVE), 0, st, a);
+    const int nt8 = (nt + 7) / 8 * 8;  // tiles padded for the XCD-aware mapping
+    hipLaunchKernelGGL(k_mt_gateup, dim3(nt8 * (Imax / GU_ROWS)), dim3(GU_WAVES * WAVE), 0, st, a);
     BREAD_HIP(hipGetLastError());
     const int rows = T * (K + 1);
     hipLaunchKernelGGL(k_mt_hprep, dim3((rows + 3) / 4), dim3(256), 0, st, c->h, rows, T * K, s.expert_inter,
                        s.shared_inter, Imax, (uint4 *)g.hhi, (uint4 *)g.hlo, g.hexp);
     BREAD_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_mt_down, dim3(nt, (H + DN_ROWS - 1) / DN_ROWS), dim3(DN_WAVES * WAVE), 0, st, a);
+    hipLaunchKernelGGL(k_mt_down, dim3(nt8 * ((H + DN_ROWS - 1) / DN_ROWS)), dim3(DN_WAVES * WAVE), 0, st, a);
     BREAD_HIP(hipGetLastError());
     hipLaunchKernelGGL(k_mt_combine, dim3(T, (H / 4 + 255) / 256), dim3(256), 0, st, g.eo, g.pos_of, c->w, c->gsh,
                        hidden, H, K, T);
