@@ -61,9 +61,9 @@ struct bread_grouped_ws {
 };
 
 struct bread_small_ws {
-    int32_t *slot_expert = nullptr;  // expert of each slot (-1: shared) [min(T K, E) + 1]
-    int32_t *slot_cnt = nullptr;     // pairs of each slot
-    int32_t *slot_pair = nullptr;    // pair ids of each slot in token order [slots][T]
+    int32_t *slot_expert = nullptr;  // expert of each slot (-1: shared)
+    int32_t *slot_cnt = nullptr;     // pairs of each slot (at most 4)
+    int32_t *slot_pair = nullptr;    // pair ids of each slot in token order [slots][4]
     int32_t *n_slots = nullptr;
     float *eo = nullptr;             // expert outputs by pair [T (K+1)][H]
 };

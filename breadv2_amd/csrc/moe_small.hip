@@ -1,5 +1,6 @@
-// moe_small.hip — the small-batch MoE path (2 <= n_tokens <= 32: batched
-// decode, speculative-verify rounds).
+// moe_small.hip — the small-batch MoE path (2 <= n_tokens <= 32; the
+// automatic choice uses it up to 8: batched decode, speculative-verify
+// rounds).
 //
 // Per token the result is the MoE block of one_layer_forward
 // (one_layer.cu:1800-1986; CPU form 1413-1471), computed in fp32 like the
@@ -7,31 +8,32 @@
 // tokens, so matrix-core tiles would run mostly empty and the time goes to
 // latency: this path streams each selected expert's rows once over the whole
 // GPU and dots every row with the few tokens that chose the expert, on the
-// vector ALUs.  Waves work independently (no LDS staging, no barriers): a
-// wave requests all of its weight rows at once, then reads each token's
-// activations straight into registers (the first row brings them into the
-// CU's L1, the others hit there) and reduces with DPP.
+// vector ALUs.
 //
 // Kernels per layer, stream-ordered:
-//   k_sb_route    one router row a wave held in registers, dotted with every
+//   k_sb_router   one router row a wave held in registers, dotted with every
 //                 token (the next token's activations requested while the
-//                 current one is summed; the extra row E is the fp16
-//                 shared-gate vector); the workgroup that finishes last runs
-//                 softmax / top-k per token and numbers the experts chosen by
-//                 any token into slots in expert order (slot 0 is the shared
-//                 expert with every token), each slot with its (token, rank)
-//                 pairs in token order.
+//                 current one is summed); the extra row E is the fp16
+//                 shared-gate vector.
+//   k_sb_select   one workgroup: softmax / top-k per token, then slots: an
+//                 expert's tokens in chunks of at most SB_CH (the shared
+//                 expert's chunks first, with every token, then the chosen
+//                 experts in expert order), each with its (token, rank) pairs
+//                 in token order.  Chunks spread a hot expert over more
+//                 workgroups.
 //   k_sb_gateup   grid (slot, 32-row chunk): 8 lanes per gate/up row pair,
-//                 one superblock a lane, dotted with the slot's tokens, then
-//                 SwiGLU.
-//   k_sb_down     grid (slot, 128-row chunk): a wave takes 32 rows, 8 lanes
-//                 per Q6_K superblock with a row's superblocks in adjacent
-//                 lanes, and dots them with the slot's SwiGLU rows.
+//                 one Q4_K superblock a lane, dotted with the slot's tokens
+//                 (staged in LDS), then SwiGLU.
+//   k_sb_down     grid (slot, 128-row chunk): the rows staged in LDS by
+//                 16-byte loads, 16 lanes per row (8 per Q6_K superblock),
+//                 dotted with the slot's SwiGLU rows (staged in LDS).
 //   k_sb_combine  per token, the reference order: shared expert first, then
 //                 the routed experts by rank.
 // Pair p = t * (K + 1) + k' (k' = 0 shared, 1 + rank) indexes the SwiGLU rows
 // and the expert outputs, so the combine does not depend on the slot order.
-// Every sum has a fixed order: repeated calls are bit-identical.
+// In each workgroup the pair ids are loaded first, then the activations,
+// then the weights: a wait for a load also waits for every load issued
+// before it.  Every sum has a fixed order: repeated calls are bit-identical.
 #include "bread_internal.h"
 #include "quant_dot.h"
 #include "route_dev.h"
@@ -59,17 +61,17 @@ struct SbLayer {
 };
 
 // Marks a register as changed here, so code that depends on it stays at its
-// use: keeps the compiler from hoisting every row group's dequantisation out
-// of the staging loop, which would hold them all in registers at once.
+// use: keeps the compiler from hoisting the code conversions out of the token
+// loops, which would hold every converted weight in registers at once.
 __device__ __forceinline__ void pin(uint32_t &v)
 {
     asm volatile("" : "+v"(v));
 }
 
 struct SbSlots {
-    const int32_t *expert;  // [S]: expert id, -1 for the shared expert (slot 0)
-    const int32_t *cnt;     // [S]: pairs in the slot
-    const int32_t *pair;    // [S][T]: pair ids in token order
+    const int32_t *expert;  // [S]: expert id, -1 for the shared expert's slots
+    const int32_t *cnt;     // [S]: pairs in the slot (<= SB_CH)
+    const int32_t *pair;    // [S][SB_CH]: pair ids in token order
     const int32_t *n;       // slots in use
 };
 
