@@ -87,6 +87,8 @@ constexpr int W_SH = 9;                  // waves 9, 10: shared gate/up
 constexpr int W_DN = 9;                  // waves 9..15: routed down bands
 constexpr int N_DN = NWV - W_DN;         // 7
 constexpr int DN_LOADS = (MAXK * BAND16 + N_DN * WAVE - 1) / (N_DN * WAVE);  // 4
+constexpr int W_XQ = 4;                  // waves 4..11 convert x to fixed point (quant_x)
+constexpr int N_XQ = 8;
 constexpr int W_PF = 12;                 // waves 12..15 prefetch routing-independent weights, never poll
 constexpr int N_XPOLL = 8;               // waves 0..7 poll the previous layer's output, 4 columns a thread
 constexpr int N_HPOLL = W_PF;            // waves 0..11 poll the SwiGLU outputs
@@ -106,6 +108,8 @@ static_assert(NBH == 8 && DI / QK == 2, "lane layouts assume H = 2048 and I = 51
 static_assert(BAND % 16 == 0, "down bands are loaded in 16-byte chunks");
 static_assert(NPOLL * WAVE == 256 && 4 * N_XPOLL * WAVE == DH, "pollers: one logit a lane; four columns a thread");
 static_assert(W_GU + MAXK == W_SH && W_SH + 2 <= NWV, "wave roles");
+static_assert(N_XQ * WAVE * 4 == DH && W_XQ >= NPOLL && W_XQ + N_XQ <= NWV,
+              "fixed-point x: non-polling waves, four columns a thread");
 static_assert(G * ((MAXK + 2) / 2) <= 2 * N_HPOLL * WAVE, "h poll: at most two chunks a thread");
 
 // Trace points recorded per (workgroup, layer) when a trace buffer is given.
@@ -156,6 +160,10 @@ struct DecArgs {
 
 struct Smem {
     float x[DH];                       // normalised input of the layer
+    uint32_t xqh[DH / 4];              // x in 16-bit block fixed point: high bytes, 4 columns a word
+    uint32_t xql[DH / 4];              // low bytes
+    float xqs[DH / 32];                // block scales (32 columns)
+    float xsum[DH / 16];               // fp32 sums of 16-column runs of x
     float nw[DH];                      // RMSNorm weights (prefetched)
     float h[NSLOT * DI];               // SwiGLU outputs of every slot
     uint32_t down[MAXK * BAND / 4];    // routed down bands, slot k at (k - 1) * BAND
@@ -177,6 +185,7 @@ struct Smem {
     int lgcnt;                         // polling waves done with the logits
     int dncnt;                         // down waves whose bands are in LDS
     int gucnt;                         // routed gate/up waves whose weights are in LDS
+    int xqcnt;                         // waves done converting their part of x (quant_x)
     int abort;                         // a wait failed: the workgroup leaves
 };
 // more than half of a CU's 160 KB, so the dispatcher puts one workgroup per CU
@@ -427,32 +436,61 @@ __device__ __forceinline__ void gu_issue(const uint8_t *gbase, const uint8_t *ub
     }
 }
 
+// x of the layer in 16-bit block fixed point for the gate/up integer dots
+// (q4k_chunk_dot_q16): per 32-column block b, s_b = max|x| / 32511 and
+// x_i ~= s_b * q_i with q_i = rint(x_i / s_b) = 256 hi_i + lo_i, hi in
+// [-127, 127], lo in [-128, 127]; the error is at most s_b / 2 (relative
+// 1.5e-5 of the block maximum).  Also the fp32 sum of every 16-column run
+// (the Q4_K min term).  Thread t (0..511) converts columns 4t..4t+3; eight
+// threads share a block, four a run.
+__device__ __forceinline__ void quant_x(Smem &S, int t)
+{
+    const float4 v = *reinterpret_cast<const float4 *>(&S.x[4 * t]);
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    m = fmaxf(m, dpp_f<0xB1>(m));   // quad_perm [1,0,3,2]
+    m = fmaxf(m, dpp_f<0x4E>(m));   // quad_perm [2,3,0,1]
+    m = fmaxf(m, dpp_f<0x141>(m));  // row_half_mirror: the 8-lane block
+    const float inv = m > 0.f ? 32511.0f / m : 0.f;
+    const float xv[4] = {v.x, v.y, v.z, v.w};
+    uint32_t hw = 0, lw = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int q = __float2int_rn(xv[k] * inv);
+        const int hi = (q + 128) >> 8;
+        const int lo = q - 256 * hi;
+        hw |= ((uint32_t)hi & 0xFFu) << (8 * k);
+        lw |= ((uint32_t)lo & 0xFFu) << (8 * k);
+    }
+    S.xqh[t] = hw;
+    S.xql[t] = lw;
+    if ((t & 7) == 0) S.xqs[t >> 3] = m / 32511.0f;
+    float r = (v.x + v.y) + (v.z + v.w);
+    r += dpp_f<0xB1>(r);
+    r += dpp_f<0x4E>(r);
+    if ((t & 3) == 0) S.xsum[t >> 2] = r;
+}
+
 // Gate/up + SwiGLU of the N rows staged by gu_issue (the wave's own loads
-// must have landed); every lane gets the results.
+// must have landed); every lane gets the results.  The dots run on the
+// fixed-point x of quant_x with integer products (q4k_chunk_dot_q16).
 template <int N>
 __device__ __forceinline__ void gu_compute(const Smem &S, const uint4 (*w)[WAVE], float (&out)[N])
 {
     const int lane = opaque(lane_id());
     const int base = gu_base(lane);
     const uint32_t j = (uint32_t)(lane & 7) >> 1;
-    float xl[16], xh[16];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const float4 lo = *reinterpret_cast<const float4 *>(&S.x[base + 4 * q]);
-        const float4 hi = *reinterpret_cast<const float4 *>(&S.x[base + 32 + 4 * q]);
-        xl[4 * q] = lo.x; xl[4 * q + 1] = lo.y; xl[4 * q + 2] = lo.z; xl[4 * q + 3] = lo.w;
-        xh[4 * q] = hi.x; xh[4 * q + 1] = hi.y; xh[4 * q + 2] = hi.z; xh[4 * q + 3] = hi.w;
-    }
-    float sxl = 0.f, sxh = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        sxl += xl[i];
-        sxh += xh[i];
-    }
+    const uint4 lh = *reinterpret_cast<const uint4 *>(&S.xqh[base >> 2]);
+    const uint4 ll = *reinterpret_cast<const uint4 *>(&S.xql[base >> 2]);
+    const uint4 hh = *reinterpret_cast<const uint4 *>(&S.xqh[(base >> 2) + 8]);
+    const uint4 hl = *reinterpret_cast<const uint4 *>(&S.xql[(base >> 2) + 8]);
+    const float2 sc = *reinterpret_cast<const float2 *>(&S.xqs[base >> 5]);  // blocks 2j, 2j+1
+    const float sxl = S.xsum[base >> 4], sxh = S.xsum[(base >> 4) + 2];
 #pragma unroll
     for (int i = 0; i < N; i++) {
-        const float gt = wave_sum(q4k_chunk_dot_sx(w[4 * i][lane], w[4 * i + 1][lane], j, xl, xh, sxl, sxh));
-        const float up = wave_sum(q4k_chunk_dot_sx(w[4 * i + 2][lane], w[4 * i + 3][lane], j, xl, xh, sxl, sxh));
+        const float gt = wave_sum(
+            q4k_chunk_dot_q16(w[4 * i][lane], w[4 * i + 1][lane], j, lh, ll, hh, hl, sc.x, sc.y, sxl, sxh));
+        const float up = wave_sum(
+            q4k_chunk_dot_q16(w[4 * i + 2][lane], w[4 * i + 3][lane], j, lh, ll, hh, hl, sc.x, sc.y, sxl, sxh));
         out[i] = silu_mul(gt, up);
     }
 }
@@ -486,9 +524,12 @@ __device__ __forceinline__ void down_predecode(const Smem &S, int u, int sb, flo
         q6k_unpack(half ? ql0.y : ql0.x, half ? ql1.y : ql1.x, half ? qh.y : qh.x, q);
 #pragma unroll
         for (int s = 0; s < 4; s++) {
+            // fma(q, ds, -32 ds) rounds ds * (q - 32) once (-32 ds is exact):
+            // the same bits as the product, one instruction fewer
             const float ds = d * q6k_scale(scw, i2 + 2 * s);
+            const float nds = -32.0f * ds;
 #pragma unroll
-            for (int k = 0; k < 4; k++) w[8 * s + 4 * half + k] = ds * (float)((int)byte_of(q[s], k) - 32);
+            for (int k = 0; k < 4; k++) w[8 * s + 4 * half + k] = fmaf((float)byte_of(q[s], k), ds, nds);
         }
     }
 }
@@ -616,6 +657,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             if (lane <= K) cstore2(hnext + XREC * g + GR * lane, sent, sent);
             if (tid == 0) {
                 S.nready = 0;
+                S.xqcnt = 0;
                 S.lgcnt = 0;
                 S.dncnt = 0;
                 S.gucnt = 0;
@@ -750,6 +792,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                 __builtin_amdgcn_s_setprio(0);
             }
         }
+        if (wid >= W_XQ && wid < W_XQ + N_XQ) {
+            // x in fixed point for the gate/up dots, by waves that do not
+            // poll the logits: it runs during the logits exchange
+            quant_x(S, WAVE * (wid - W_XQ) + lane);
+            if (lane == 0) lds_add(&S.xqcnt, 1);
+        }
         if (wid >= W_GU && wid < W_GU + K) {
             // routed gate/up of slot k = wave, as soon as rank k is known
             const int slot = wid - W_GU + 1;
@@ -759,19 +807,23 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                              S.gu[slot - 1]);
                 __builtin_amdgcn_s_waitcnt(0);
                 if (lane == 0) lds_add(&S.gucnt, 1);
-                float hv[GR];
-                gu_compute<GR>(S, S.gu[slot - 1], hv);
-                if (lane == 0) {
-                    cstore2(hcur + XREC * g + GR * slot, hv[0], hv[1]);
-                    if (slot == K) trace_here(a, l, TP_HLAST);
+                if (lds_wait(S, &S.xqcnt, N_XQ)) {
+                    float hv[GR];
+                    gu_compute<GR>(S, S.gu[slot - 1], hv);
+                    if (lane == 0) {
+                        cstore2(hcur + XREC * g + GR * slot, hv[0], hv[1]);
+                        if (slot == K) trace_here(a, l, TP_HLAST);
+                    }
                 }
             }
         }
         if (wid == W_SH || wid == W_SH + 1) {
             // shared gate/up (weights prefetched), while routing runs
             float hsh[1];
-            gu_compute<1>(S, S.shw[wid - W_SH], hsh);
-            if (lane == 0) cstore(hcur + XREC * g + (wid - W_SH), hsh[0]);
+            if (lds_wait(S, &S.xqcnt, N_XQ)) {
+                gu_compute<1>(S, S.shw[wid - W_SH], hsh);
+                if (lane == 0) cstore(hcur + XREC * g + (wid - W_SH), hsh[0]);
+            }
         }
         if (wid >= W_DN) {
             // routed down bands; chunk ch (16 B) of slot ch / 210 + 1 lands
@@ -803,56 +855,64 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                 prefetch(S, load_layer(a, l + 1), g, E, wid, (l + 1) & 1);
         }
 
-        // ---- P4: pre-decode this wave's down unit once every band is in
-        // (units 16, 17 by waves 1, 2 into LDS)
+        // ---- P4 + P5: pre-decode this wave's down unit once every band is
+        // in (units 16, 17 by waves 1, 2 into LDS), and every slot's h into
+        // LDS, polled: chunk c = (workgroup w, q): float4 q of w's record
+        // holds slots 2q and 2q+1 (rows 2w, 2w+1).  A polling wave issues its
+        // first poll before the pre-decode, so the round trip overlaps it.
         float w0[32];
         const bool extra = wid >= W_GU && wid < W_GU + 2 && wid - W_GU + NWV < NU;
         float4 (*xw)[WAVE] = reinterpret_cast<float4 (*)[WAVE]>(&S.gu[wid >= W_GU && wid < W_GU + 2 ? wid - W_GU : 0][0][0]);
-        if (wid < NU && lds_wait(S, &S.dncnt, N_DN)) {
+        const bool pre = wid < NU && lds_wait(S, &S.dncnt, N_DN);
+        const bool hpoll = wid < N_HPOLL && !lds_get(&S.abort);
+        const int NQ = (K + 2) >> 1;  // float4 chunks in use per record
+        const auto hr = rsrc(hcur, G * XREC * 4);
+        // up to two chunks a thread, polled together
+        const int c0 = tid, c1 = tid + N_HPOLL * WAVE;
+        const bool two = c1 < G * NQ;
+        const int wa = c0 / NQ, q0 = c0 - wa * NQ, wb = c1 / NQ, q1 = c1 - wb * NQ;
+        const bool hi0 = 2 * q0 + 1 <= K, hi1 = 2 * q1 + 1 <= K;
+        float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+        bool r0 = !(c0 < G * NQ), r1 = !two;
+        if (hpoll) {
+            if (!r0)
+                v0 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    hr, (int)(4 * (XREC * wa + 4 * q0)), 0, AUX_COHERENT));
+            if (!r1)
+                v1 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    hr, (int)(4 * (XREC * wb + 4 * q1)), 0, AUX_COHERENT));
+        }
+        if (pre) {
             if (tid == 0) trace_here(a, l, TP_DNIN);
             down_predecode(S, wid, l & 1, w0);
             if (extra) predecode_to_lds(S, wid - W_GU + NWV, l & 1, xw);
         }
-
-        // ---- P5: every slot's h into LDS, polled: chunk c = (workgroup w,
-        // q): float4 q of w's record holds slots 2q and 2q+1 (rows 2w, 2w+1)
-        if (wid < N_HPOLL && !lds_get(&S.abort)) {
-            const int NQ = (K + 2) >> 1;  // float4 chunks in use per record
-            const auto hr = rsrc(hcur, G * XREC * 4);
+        if (hpoll) {
             bool ok = true;
-            // up to two chunks a thread, polled together
-            const int c0 = tid, c1 = tid + N_HPOLL * WAVE;
-            const bool two = c1 < G * NQ;
-            const int w0 = c0 / NQ, q0 = c0 - w0 * NQ, w1 = c1 / NQ, q1 = c1 - w1 * NQ;
-            const bool hi0 = 2 * q0 + 1 <= K, hi1 = 2 * q1 + 1 <= K;
-            float4 v0, v1;
-            bool r0 = !(c0 < G * NQ), r1 = !two;
-            for (uint32_t it = 0; it < SPIN_LIMIT && !(r0 && r1); it++) {
-                if (!r0) {
-                    v0 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                        hr, (int)(4 * (XREC * w0 + 4 * q0)), 0, AUX_COHERENT));
-                    r0 = !unwritten(v0.x) && !unwritten(v0.y) && !(hi0 && (unwritten(v0.z) || unwritten(v0.w)));
-                }
-                if (!r1) {
-                    v1 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                        hr, (int)(4 * (XREC * w1 + 4 * q1)), 0, AUX_COHERENT));
-                    r1 = !unwritten(v1.x) && !unwritten(v1.y) && !(hi1 && (unwritten(v1.z) || unwritten(v1.w)));
-                }
+            for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
+                if (!r0) r0 = !unwritten(v0.x) && !unwritten(v0.y) && !(hi0 && (unwritten(v0.z) || unwritten(v0.w)));
+                if (!r1) r1 = !unwritten(v1.x) && !unwritten(v1.y) && !(hi1 && (unwritten(v1.z) || unwritten(v1.w)));
                 if (r0 && r1) break;
                 if ((it & 63) == 63 && has_error(sy)) break;
                 __builtin_amdgcn_s_sleep(1);
+                if (!r0)
+                    v0 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        hr, (int)(4 * (XREC * wa + 4 * q0)), 0, AUX_COHERENT));
+                if (!r1)
+                    v1 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        hr, (int)(4 * (XREC * wb + 4 * q1)), 0, AUX_COHERENT));
             }
             if (!(r0 && r1)) {
                 if (!has_error(sy)) flag_error(sy, 1u);
                 ok = false;
             }
             if (c0 < G * NQ) {
-                *reinterpret_cast<float2 *>(&S.h[2 * q0 * DI + GR * w0]) = make_float2(v0.x, v0.y);
-                if (hi0) *reinterpret_cast<float2 *>(&S.h[(2 * q0 + 1) * DI + GR * w0]) = make_float2(v0.z, v0.w);
+                *reinterpret_cast<float2 *>(&S.h[2 * q0 * DI + GR * wa]) = make_float2(v0.x, v0.y);
+                if (hi0) *reinterpret_cast<float2 *>(&S.h[(2 * q0 + 1) * DI + GR * wa]) = make_float2(v0.z, v0.w);
             }
             if (two) {
-                *reinterpret_cast<float2 *>(&S.h[2 * q1 * DI + GR * w1]) = make_float2(v1.x, v1.y);
-                if (hi1) *reinterpret_cast<float2 *>(&S.h[(2 * q1 + 1) * DI + GR * w1]) = make_float2(v1.z, v1.w);
+                *reinterpret_cast<float2 *>(&S.h[2 * q1 * DI + GR * wb]) = make_float2(v1.x, v1.y);
+                if (hi1) *reinterpret_cast<float2 *>(&S.h[(2 * q1 + 1) * DI + GR * wb]) = make_float2(v1.z, v1.w);
             }
             if (!ok) S.abort = 1;
         }

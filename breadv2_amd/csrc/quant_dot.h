@@ -206,6 +206,41 @@ __device__ __forceinline__ float q80_row_partial(const uint8_t *row, int nb32, c
     return acc;
 }
 
+// q4k_chunk_dot against x in 16-bit block fixed point: over a 32-element
+// block, x_i ~= s * (256 * hi_i + lo_i) with hi, lo int8, packed four
+// elements to a word in element order (lh / ll: the high / low bytes of the
+// lane's low-nibble run, hh / hl: of its high-nibble run; s_lo, s_hi their
+// block scales).  sl, sh are the fp32 sums of the two runs, so the min term
+// is exact.  The nibble products accumulate in v_dot4_i32_i8 (q <= 15 fits a
+// signed byte; |sum| < 2^23, so the integer sums are exact and convert to
+// fp32 exactly): 7 instructions per 8 weights against 19 for the fp32 form.
+__device__ __forceinline__ float q4k_chunk_dot_q16(uint4 hd, uint4 q, uint32_t j, uint4 lh, uint4 ll, uint4 hh,
+                                                   uint4 hl, float s_lo, float s_hi, float sl, float sh)
+{
+    uint32_t sc0, m0, sc1, m1;
+    scale_min_k4(2 * j, hd.y, hd.z, hd.w, sc0, m0);
+    scale_min_k4(2 * j + 1, hd.y, hd.z, hd.w, sc1, m1);
+    const float d = h2f(hd.x);
+    const float dmin = h2f(hd.x >> 16);
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+    const uint32_t xlh[4] = {lh.x, lh.y, lh.z, lh.w}, xll[4] = {ll.x, ll.y, ll.z, ll.w};
+    const uint32_t xhh[4] = {hh.x, hh.y, hh.z, hh.w}, xhl[4] = {hl.x, hl.y, hl.z, hl.w};
+    int a_lh = 0, a_ll = 0, a_hh = 0, a_hl = 0;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int lo = (int)(qw[t] & 0x0F0F0F0Fu);
+        const int hi = (int)((qw[t] >> 4) & 0x0F0F0F0Fu);
+        a_lh = __builtin_amdgcn_sdot4(lo, (int)xlh[t], a_lh, false);
+        a_ll = __builtin_amdgcn_sdot4(lo, (int)xll[t], a_ll, false);
+        a_hh = __builtin_amdgcn_sdot4(hi, (int)xhh[t], a_hh, false);
+        a_hl = __builtin_amdgcn_sdot4(hi, (int)xhl[t], a_hl, false);
+    }
+    const float al = (float)(a_lh * 256 + a_ll) * s_lo;
+    const float ah = (float)(a_hh * 256 + a_hl) * s_hi;
+    return (d * (float)sc0) * al - (dmin * (float)m0) * sl + (d * (float)sc1) * ah -
+           (dmin * (float)m1) * sh;
+}
+
 // q4k_chunk_dot with the activation sums over the two 16-element runs
 // precomputed (they are the same for every row a lane visits).
 __device__ __forceinline__ float q4k_chunk_dot_sx(uint4 hd, uint4 q, uint32_t j, const float (&xl)[16],

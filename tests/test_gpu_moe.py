@@ -154,8 +154,9 @@ def test_decode_layer_matches_oracle(full_layer):
         assert np.array_equal(gi, ri)
         np.testing.assert_allclose(gw, rw, rtol=2e-5, atol=1e-7)
         rl2 = assert_moe_close(got, ref, base=hidden)
-        # far tighter than the contract: fp32 with a different summation order
-        assert rl2 < 1e-5
+        # far tighter than the contract: fp32 except the gate/up dots, whose
+        # activations are 16-bit block fixed point (~3e-5 of the layer output)
+        assert rl2 < 1e-4
     assert ctx.check_device() == 0
 
 
@@ -180,9 +181,9 @@ def test_decode_back_to_back_launches(full_layer):
 
 
 def test_decode_vs_multi_kernel_path(full_layer):
-    """The single-launch kernel and the per-token kernels (both fp32) agree
-    to fp32 reordering; the grouped path (fp16 operands) to the layer
-    tolerance."""
+    """The single-launch kernel (fp32 but for 16-bit fixed-point gate/up
+    activations) and the per-token kernels (fp32) agree to ~3e-5; the grouped
+    path (fp16 operands) to the layer tolerance."""
     s, t, _ = full_layer
     ctx = B.MoeContext(s, max_tokens=2)
     x = xs(1, s.hidden, 8)
@@ -197,7 +198,7 @@ def test_decode_vs_multi_kernel_path(full_layer):
     torch.cuda.synchronize()
     a, b, c = h1.cpu().numpy()[0], h2.cpu().numpy(), h3.cpu().numpy()
     assert np.array_equal(b[0], b[1])
-    assert rel_l2(a, b[0]) < 1e-5
+    assert rel_l2(a, b[0]) < 1e-4
     assert np.array_equal(c[0], c[1])
     assert_moe_close(c[0], a)
 
