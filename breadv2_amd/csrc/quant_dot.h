@@ -214,12 +214,26 @@ __device__ __forceinline__ float q80_row_partial(const uint8_t *row, int nb32, c
 // is exact.  The nibble products accumulate in v_dot4_i32_i8 (q <= 15 fits a
 // signed byte; |sum| < 2^23, so the integer sums are exact and convert to
 // fp32 exactly): 7 instructions per 8 weights against 19 for the fp32 form.
+// The (scale, min) pairs of sub-blocks 2j and 2j+1 of a Q4_K superblock as
+// bytes [sc0, sc1, m0, m1], without branches on j: get_scale_min_k4
+// (dequant_q4k_cpu.c:70-79) reads, for j < 2, the low six bits of bytes
+// 2j, 2j+1, 2j+4, 2j+5 and, for j >= 2 (r = 2j - 4), the nibbles of bytes
+// 8+r, 9+r with the top two bits of bytes r, r+1 (scales) and 4+r, 5+r
+// (mins).  Both cases gather with v_perm_b32.
+__device__ __forceinline__ uint32_t q4k_scale_pair(uint4 hd, uint32_t j)
+{
+    const uint32_t jj = (j & 1u) * 0x02020202u;
+    const uint32_t h = __builtin_amdgcn_perm(hd.z, hd.y, 0x05040100u + jj);
+    if (j < 2) return h & 0x3F3F3F3Fu;
+    const uint32_t l = __builtin_amdgcn_perm(hd.w, hd.w, 0x01000100u + jj);
+    return (l & 0x00000F0Fu) | ((l >> 4) & 0x0F0F0000u) | ((h >> 2) & 0x30303030u);
+}
+
 __device__ __forceinline__ float q4k_chunk_dot_q16(uint4 hd, uint4 q, uint32_t j, uint4 lh, uint4 ll, uint4 hh,
                                                    uint4 hl, float s_lo, float s_hi, float sl, float sh)
 {
-    uint32_t sc0, m0, sc1, m1;
-    scale_min_k4(2 * j, hd.y, hd.z, hd.w, sc0, m0);
-    scale_min_k4(2 * j + 1, hd.y, hd.z, hd.w, sc1, m1);
+    const uint32_t scm = q4k_scale_pair(hd, j);
+    const uint32_t sc0 = byte_of(scm, 0), sc1 = byte_of(scm, 1), m0 = byte_of(scm, 2), m1 = byte_of(scm, 3);
     const float d = h2f(hd.x);
     const float dmin = h2f(hd.x >> 16);
     const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
