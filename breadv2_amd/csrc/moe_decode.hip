@@ -186,6 +186,7 @@ struct Smem {
     int dncnt;                         // down waves whose bands are in LDS
     int gucnt;                         // routed gate/up waves whose weights are in LDS
     int xqcnt;                         // waves done converting their part of x (quant_x)
+    int gudone;                        // routed gate/up waves done computing
     int abort;                         // a wait failed: the workgroup leaves
 };
 // more than half of a CU's 160 KB, so the dispatcher puts one workgroup per CU
@@ -671,6 +672,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             if (tid == 0) {
                 S.nready = 0;
                 S.xqcnt = 0;
+                S.gudone = 0;
                 S.lgcnt = 0;
                 S.dncnt = 0;
                 S.gucnt = 0;
@@ -826,6 +828,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                     if (lane == 0) {
                         cstore2(hcur + XREC * g + GR * slot, hv[0], hv[1]);
                         if (slot == K) trace_here(a, l, TP_HLAST);
+                        lds_add(&S.gudone, 1);
                     }
                 }
             }
@@ -844,10 +847,9 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             const int nchunk = K * BAND16;
             const int c0 = WAVE * (wid - W_DN);
             const int ln = opaque(lane);
-            // gate/up first: the down bands are not needed before the h
-            // exchange, so their loads wait until every rank's gate/up weights
-            // are in
-            bool ok = lds_wait(S, &S.nready, K, true) && lds_wait(S, &S.gucnt, K, true);
+            // the down bands are not needed before the h exchange: their
+            // loads go out once every rank is known, behind the gate/up loads
+            bool ok = lds_wait(S, &S.nready, K);
 #pragma unroll
             for (int i = 0; i < DN_LOADS; i++) {
                 const int cw = c0 + N_DN * WAVE * i;  // first chunk of this wave's load
@@ -876,7 +878,9 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
         float w0[32];
         const bool extra = wid >= W_GU && wid < W_GU + 2 && wid - W_GU + NWV < NU;
         float4 (*xw)[WAVE] = reinterpret_cast<float4 (*)[WAVE]>(&S.gu[wid >= W_GU && wid < W_GU + 2 ? wid - W_GU : 0][0][0]);
-        const bool pre = wid < NU && lds_wait(S, &S.dncnt, N_DN);
+        // (after every routed gate/up is computed: the pre-decode would
+        // otherwise take VALU time from the gate/up dots)
+        const bool pre = wid < NU && lds_wait(S, &S.dncnt, N_DN) && lds_wait(S, &S.gudone, K);
         const bool hpoll = wid < N_HPOLL && !lds_get(&S.abort);
         const int NQ = (K + 2) >> 1;  // float4 chunks in use per record
         const auto hr = rsrc(hcur, G * XREC * 4);
