@@ -53,7 +53,7 @@ def measured_traffic():
         with open(path) as f:
             t = json.load(f)
     except (OSError, ValueError):
-        return None, "no PMC summary"
+        return None, "no PMC summary", None
     fs = t["calib_copy_kib"] / t["calib_fetch_kib"]
     ws = t["calib_copy_kib"] / t["calib_write_kib"]
     kib = t["fetch_kib_per_dispatch"] * fs + t["write_kib_per_dispatch"] * ws

@@ -14,6 +14,7 @@
 //                the combine);
 //   waves 1..8   router row and shared-gate dot, then the gate/up rows of
 //                routed slot k = wave;
+//   waves 4..11  x in 16-bit block fixed point, during the logits exchange;
 //   waves 9, 10  shared-expert gate/up rows (before routing is known);
 //   waves 9..15  the down-projection bands of the routed slots (8 rows x
 //                420 B each);
@@ -26,6 +27,10 @@
 // loads waits for them: the logit pollers never hold weight loads, and the
 // next layer's weights are requested early enough (after this layer's h is
 // in) to have landed before that layer's first poll returns.
+//
+// The gate/up dots multiply the Q4_K nibbles with x in 16-bit block fixed
+// point (x ~= s (256 hi + lo), hi and lo int8) by v_dot4_i32_i8, with exact
+// integer sums; the min term uses fp32 sums of x.  Everything else is fp32.
 //
 // Routing is published rank by rank: wave 0 writes expert k to LDS as soon as
 // selection pass k ends, and the gate/up and down waves start that slot's
