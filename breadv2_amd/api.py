@@ -424,7 +424,9 @@ class MoeContext:
 
     def stack_forward(self, layers, hidden: torch.Tensor, n_tokens: int, want_routing: bool = False, stream=None):
         """bread_moe_stack_forward: n_tokens tokens through len(layers) MoE
-        layers, h <- h + MoE_l(RMSNorm(h) * w_l), one grouped call per layer."""
+        layers, h <- h + MoE_l(RMSNorm(h) * w_l): one batched call per layer,
+        or one decode-stack launch per token for up to
+        bread_stack_loop_tokens() tokens (automatic choice)."""
         n = len(layers)
         arr = (MoeLayer * n)(*layers)
         K = self.shape.top_k

@@ -134,10 +134,13 @@ bool bread_small_supported(const bread_moe_shape_t &s, const bread_moe_layer_t *
 int bread_small_max_tokens();
 int bread_launch_moe_small(bread_moe_ctx_t *ctx, const bread_moe_layer_t *L, const float *x, float *hidden,
                            int n_tokens, hipStream_t st);
+// One token (token index tok of the call: its routing lands at record tok
+// of the context's routing buffers).
 int bread_launch_moe_decode(bread_moe_ctx_t *ctx, const bread_moe_layer_t *L, const float *x,
-                            float *hidden, hipStream_t st);
+                            float *hidden, hipStream_t st, int tok = 0);
+// Routing outputs of layer l at idx + l * rstride * K (w alike, gsh + l * rstride).
 int bread_launch_decode_layers(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layers, int n, float *hidden,
-                               int32_t *idx, float *w, float *gsh, hipStream_t st);
+                               int32_t *idx, float *w, float *gsh, hipStream_t st, int rstride = 1);
 int bread_decode_max_blocks(int *out);
 int bread_decode_grid(const bread_moe_shape_t &s);
 int bread_decode_trace_points();

@@ -155,9 +155,10 @@ struct DecArgs {
     uint64_t *tlogits;       // [256][LG_STRIDE] epoch-tagged logits
     float *xbuf;             // [2][G][XREC] layer outputs by parity: rows 8g..8g+7 of workgroup g
     float *hbuf;             // [3][G][XREC] SwiGLU outputs by layer mod 3: [slot][rows 2g, 2g+1]
-    int32_t *idx_out;        // [L][K] or NULL
-    float *w_out;            // [L][K] or NULL
-    float *gsh_out;          // [L] or NULL
+    int32_t *idx_out;        // [L][rstride][K] or NULL (this token's record of each layer)
+    float *w_out;            // [L][rstride][K] or NULL
+    float *gsh_out;          // [L][rstride] or NULL
+    int rstride;             // tokens per layer record of the routing outputs
     bread_decode_sync *sync;
     uint64_t *trace;         // [G][L][TP_N] or NULL
     int E, K;
@@ -801,9 +802,10 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                     if (lane < K) S.w[lane] = wk;
                     if (lane == 0) S.sgsh = sigmoidf_ref(gsh);
                     if (g == 0) {
-                        if (a.idx_out && lane < K) a.idx_out[l * K + lane] = my_idx;
-                        if (a.w_out && lane < K) a.w_out[l * K + lane] = wk;
-                        if (a.gsh_out && lane == 0) a.gsh_out[l] = gsh;
+                        const int rl = l * a.rstride;
+                        if (a.idx_out && lane < K) a.idx_out[rl * K + lane] = my_idx;
+                        if (a.w_out && lane < K) a.w_out[rl * K + lane] = wk;
+                        if (a.gsh_out && lane == 0) a.gsh_out[rl] = gsh;
                     }
                     trace_point(a, l, TP_ROUTED);
                 } else if (lane == 0) {
@@ -1052,7 +1054,7 @@ int bread_decode_max_blocks(int *out)
 }
 
 int bread_launch_moe_decode(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, float *hidden,
-                            hipStream_t st)
+                            hipStream_t st, int tok)
 {
     if (!decode_shape_ok(c->shape) || !layer_ok(*L)) return BREAD_ERR_SHAPE;
     DecArgs a;
@@ -1062,14 +1064,16 @@ int bread_launch_moe_decode(bread_moe_ctx_t *c, const bread_moe_layer_t *L, cons
     a.L = 1;
     a.x0 = x;
     a.hidden = hidden;
-    a.idx_out = c->idx;
-    a.w_out = c->w;
-    a.gsh_out = c->gsh;
+    const int K = c->shape.top_k;
+    a.idx_out = c->idx + (size_t)tok * K;
+    a.w_out = c->w + (size_t)tok * K;
+    a.gsh_out = c->gsh + tok;
+    a.rstride = 1;
     return launch(c, a, st);
 }
 
 int bread_launch_decode_layers(bread_moe_ctx_t *c, const bread_moe_layer_t *layers, int n, float *hidden,
-                               int32_t *idx, float *w, float *gsh, hipStream_t st)
+                               int32_t *idx, float *w, float *gsh, hipStream_t st, int rstride)
 {
     if (!decode_shape_ok(c->shape)) return BREAD_ERR_SHAPE;
     BREAD_REQUIRE(n <= c->max_layers, BREAD_ERR_CAPACITY, "more layers than the context holds");
@@ -1103,6 +1107,7 @@ int bread_launch_decode_layers(bread_moe_ctx_t *c, const bread_moe_layer_t *laye
     a.idx_out = idx;
     a.w_out = w;
     a.gsh_out = gsh;
+    a.rstride = rstride;
     return launch(c, a, st);
 }
 

@@ -112,16 +112,23 @@ extern "C" int bread_moe_stack_forward(bread_moe_ctx_t *c, const bread_moe_layer
                       "post_norm_w must be 16-byte aligned");
     }
     if (n == 0 || T == 0) return BREAD_OK;
-    // one token: the whole stack in one persistent launch when the path and
-    // shape allow it
-    if (T == 1 && (c->path == BREAD_PATH_AUTO || c->path == BREAD_PATH_DECODE) && n <= c->max_layers) {
-        hipStream_t st = to_hip(stream);
-        c->last_stream = st;
-        const int rc = bread_launch_decode_layers(c, layers, n, hidden, idx, w, gsh, st);
-        if (rc != BREAD_ERR_SHAPE || c->path == BREAD_PATH_DECODE) return rc;
-        bread_clear_stale_error();
-    }
     const int H = c->shape.hidden, K = c->shape.top_k;
+    // one token, or up to bread_stack_loop_tokens() under the automatic
+    // choice: the whole stack in one persistent launch per token, when the
+    // shape allows it (token t's routing goes to record t of each layer)
+    if ((T == 1 && (c->path == BREAD_PATH_AUTO || c->path == BREAD_PATH_DECODE)) ||
+        (T <= bread_stack_loop_tokens() && c->path == BREAD_PATH_AUTO)) {
+        if (n <= c->max_layers) {
+            hipStream_t st = to_hip(stream);
+            c->last_stream = st;
+            int rc = BREAD_OK;
+            for (int t = 0; t < T && rc == BREAD_OK; t++)
+                rc = bread_launch_decode_layers(c, layers, n, hidden + (size_t)t * H, idx ? idx + (size_t)t * K : nullptr,
+                                                w ? w + (size_t)t * K : nullptr, gsh ? gsh + t : nullptr, st, T);
+            if (rc != BREAD_ERR_SHAPE || c->path == BREAD_PATH_DECODE) return rc;
+            bread_clear_stale_error();
+        }
+    }
     hipStream_t st = to_hip(stream);
     for (int l = 0; l < n; l++) {
         bread_clear_stale_error();

@@ -166,6 +166,12 @@ typedef enum {
 int bread_moe_ctx_set_path(bread_moe_ctx_t *ctx, int path);
 /* Largest n_tokens the automatic choice sends to the small-batch path. */
 int bread_small_auto_tokens(void);
+/* Largest n_tokens for which the automatic choice runs one decode launch per
+ * token: in bread_moe_forward (one layer) and in bread_moe_stack_forward (one
+ * launch of the whole stack per token).  No reference counterpart; the
+ * crossovers measured on MI355X against the small-batch path. */
+int bread_decode_loop_tokens(void);
+int bread_stack_loop_tokens(void);
 
 /* Synchronises the context's last stream and returns BREAD_ERR_DEVICE (and
  * the kernel's error word in *device_error, if given) when a kernel flagged
@@ -201,8 +207,9 @@ int bread_route_layer(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer, cons
  * d_x_normed fp32 [n_tokens][H] (the post-attention RMSNorm output),
  * d_hidden fp32 [n_tokens][H] in/out.  Optional outputs d_idx/d_w/d_gsh as in
  * bread_route (may be NULL).  Path (bread_moe_ctx_set_path, default
- * BREAD_PATH_AUTO): n_tokens == 1 runs the persistent decode kernel when the
- * shape allows it (see bread_moe_decode_layers); small batches (up to
+ * BREAD_PATH_AUTO): up to bread_decode_loop_tokens() tokens run the persistent
+ * decode kernel, one launch per token, when the shape allows it (see
+ * bread_moe_decode_layers); small batches (up to
  * bread_small_auto_tokens()) run the small-batch path (each selected expert's
  * rows streamed once over the whole GPU and dotted with the tokens that chose
  * it, fp32; H <= 2048, intermediate sizes 256 or 512); larger batches run the
@@ -236,8 +243,9 @@ int bread_moe_forward_f16(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer, 
 /* n_tokens tokens through a stack of MoE layers:
  *   for l < n_layers:  x = RMSNorm(hidden) * layers[l].post_norm_w  (NULL: unit);
  *                      hidden += MoE_l(x)
- * one bread_moe_forward per layer for all tokens (the grouped path), or one
- * bread_moe_decode_layers launch for a single token.  Replaces the
+ * one bread_moe_forward per layer for all tokens (the grouped path), or, for
+ * a single token or up to bread_stack_loop_tokens() tokens under the automatic
+ * choice, one bread_moe_decode_layers launch per token.  Replaces the
  * token-by-token verification of main_speculative.cu:477-497 (one
  * bread_step per draft token) at the MoE boundary: the B = K + 1 tokens of a
  * round share each layer's expert reads.  d_hidden fp32 [n_tokens][H] in/out;

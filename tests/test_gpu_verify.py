@@ -136,6 +136,29 @@ def test_stack_forward_batched_equals_single_tokens(stack):
     assert ctx.check_device() == 0
 
 
+def test_stack_forward_few_tokens_run_decode_stacks(stack):
+    """Up to bread_stack_loop_tokens() tokens under the automatic choice: one
+    decode-stack launch per token, the routing of token t in record t of each
+    layer; equal to single-token stacks bit for bit."""
+    s, descs, _, _ = stack
+    T = B.lib.bread_stack_loop_tokens()
+    assert T >= 2
+    h0 = np.random.default_rng(24).standard_normal((T, s.hidden)).astype(np.float32)
+    ctx = B.MoeContext(s, max_tokens=T)
+    hb = dev(h0)
+    ib, wb, gb = ctx.stack_forward(descs, hb, T, want_routing=True)
+    ib, wb, gb = ib.cpu().numpy(), wb.cpu().numpy(), gb.cpu().numpy()
+    for t in range(T):
+        ht = dev(h0[t:t + 1])
+        it, wt, gt = ctx.stack_forward(descs, ht, 1, want_routing=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(hb[t].cpu().numpy().view(np.uint32), ht[0].cpu().numpy().view(np.uint32))
+        assert np.array_equal(ib[:, t], it.cpu().numpy()[:, 0])
+        assert np.array_equal(wb[:, t], wt.cpu().numpy()[:, 0])
+        assert np.array_equal(gb[:, t], gt.cpu().numpy()[:, 0])
+    assert ctx.check_device() == 0
+
+
 def head_weights(qtype, vocab, H, seed):
     return synth.synth_q4k(vocab * H // 256, seed) if qtype == Q4K else synth.synth_q6k(vocab * H // 256, seed)
 
