@@ -150,7 +150,6 @@ SIGNATURES = {
     "bread_moe_ctx_set_trace": (c_int, [c_void_p, c_void_p, ctypes.c_size_t, POINTER(c_int)]),
     "bread_moe_ctx_set_path": (c_int, [c_void_p, c_int]),
     "bread_small_auto_tokens": (c_int, []),
-    "bread_decode_loop_tokens": (c_int, []),
     "bread_stack_loop_tokens": (c_int, []),
     "bread_rmsnorm_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_void_p]),
     "bread_arena_create": (c_int, [POINTER(MoeShape), c_int, POINTER(c_void_p)]),

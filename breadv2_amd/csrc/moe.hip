@@ -506,17 +506,12 @@ extern "C" int bread_route_layer(bread_moe_ctx_t *c, const bread_moe_layer_t *L,
     return BREAD_OK;
 }
 
-// Below these batch sizes one decode launch per token (16.3 us per layer
-// launch on MI355X, 509 us per 40-layer stack) beats the small-batch path
-// (46 us per layer at 2 tokens, 65-69 at 4, 78-88 at 8), measured.
-extern "C" int bread_decode_loop_tokens(void)
-{
-    return 3;
-}
-
+// Up to this many tokens one decode-stack launch per token (509 us per
+// 40-layer stack on MI355X) beats 40 small-batch layers (28 us per layer at
+// 2 tokens, 35 at 4, 48 at 8), measured.
 extern "C" int bread_stack_loop_tokens(void)
 {
-    return 6;
+    return 2;
 }
 
 extern "C" int bread_moe_forward(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, float *hidden,
@@ -546,16 +541,7 @@ extern "C" int bread_moe_forward(bread_moe_ctx_t *c, const bread_moe_layer_t *L,
         if (rc == BREAD_ERR_SHAPE) return bread_fail(rc, "bread_moe_forward", "shape not supported by the small-batch path");
         break;
     default:
-        // up to bread_decode_loop_tokens() tokens: one decode launch per token
-        // (a shape the decode kernel rejects is rejected at the first token,
-        // before anything runs)
-        rc = BREAD_ERR_SHAPE;
-        if (T <= bread_decode_loop_tokens()) {
-            const int H = c->shape.hidden;
-            rc = BREAD_OK;
-            for (int t = 0; t < T && rc == BREAD_OK; t++)
-                rc = bread_launch_moe_decode(c, L, x + (size_t)t * H, hidden + (size_t)t * H, st, t);
-        }
+        rc = (T == 1) ? bread_launch_moe_decode(c, L, x, hidden, st) : BREAD_ERR_SHAPE;
         if (rc == BREAD_ERR_SHAPE && T <= bread_small_auto_tokens()) rc = bread_launch_moe_small(c, L, x, hidden, T, st);
         if (rc == BREAD_ERR_SHAPE) rc = bread_launch_moe_grouped(c, L, x, hidden, T, st);
         if (rc == BREAD_ERR_SHAPE) rc = bread_launch_moe_multi(c, L, x, hidden, T, st);

@@ -41,7 +41,7 @@
 namespace {
 
 constexpr int SB_MAX_T = 32;      // tokens per call (token bitmasks are 32 bits)
-constexpr int SB_AUTO_T = 8;      // the automatic choice takes this path up to here (measured crossover)
+constexpr int SB_AUTO_T = 16;     // the automatic choice takes this path up to here (measured crossover)
 constexpr int RT_WAVES = 16;      // selection waves
 constexpr int RT_THREADS = RT_WAVES * WAVE;
 constexpr int SB_CH = 4;          // pairs per slot: an expert's tokens in chunks of this many
@@ -563,6 +563,437 @@ __global__ __launch_bounds__(256) void k_sb_combine(float *__restrict__ hidden, 
     *reinterpret_cast<float4 *>(hidden + (size_t)t * H + c) = v;
 }
 
+// ---- wide kernels at the decode shape (H 2048, I = I_sh = 512, K <= 8) ---------------
+//
+// k_sw_gateup and k_sw_down replace k_sb_gateup, k_sb_down and k_sb_combine at
+// the decode kernel's shape.  Every workgroup owns a slice of every slot, as
+// the decode kernel's workgroups do: gate/up rows 2g and 2g+1, output rows
+// 8g..8g+7.  Each CU then has loads of all its slots in flight at once,
+// where the per-slot workgroups of the general kernels form chains of small
+// dependent steps.  The gate/up dots use the decode kernel's integer form
+// (x in 16-bit block fixed point, q4k_chunk_dot_q16); the down dots are fp32
+// on pre-decoded weights; the combine runs in the down kernel.
+
+constexpr int SW_G = 256;                                         // workgroups
+constexpr int SW_NT = 1024;                                       // threads per workgroup
+constexpr int SW_NW = SW_NT / WAVE;                               // 16 waves
+constexpr int SW_H = 2048;
+constexpr int SW_I = 512;
+constexpr int SW_K = 8;                                           // top-k at most
+constexpr int SW_MAX_T = 16;
+constexpr int SW_GU_BYTES = 4 * (SW_H / QK) * Q4K_BYTES;          // gate rows 2g, 2g+1, then up: 4608
+constexpr int SW_GU_CH = SW_GU_BYTES / 16;                        // 288 16-byte chunks
+constexpr int SW_GU_LOADS = (SW_GU_CH + WAVE - 1) / WAVE;         // 5
+constexpr int SW_ROW16 = (SW_H / QK) * Q4K_BYTES / 16;            // one gate/up row: 72 chunks
+constexpr int SW_DN_BYTES = 4 * (SW_I / QK) * Q6K_BYTES;          // four down rows: 1680
+constexpr int SW_DN_CH = SW_DN_BYTES / 16;                        // 105
+constexpr int SW_DN_LOADS = (SW_DN_CH + WAVE - 1) / WAVE;         // 2
+constexpr int SW_DN_ROW = (SW_I / QK) * Q6K_BYTES;                // 420
+constexpr int SW_MAX_P = SW_MAX_T * (SW_K + 1);                   // pairs
+// s_waitcnt lgkmcnt(0) with vmcnt and expcnt left at their maxima (gfx9
+// encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+constexpr int WAITCNT_LGKM0 = 0xF | (0x7 << 4) | (0x3 << 14);
+static_assert(SW_I / SW_G == 2 && SW_H / SW_G == 8, "row ownership assumes 256 workgroups");
+static_assert(SW_GU_BYTES % 16 == 0 && SW_DN_BYTES % 16 == 0, "16-byte loads");
+
+struct SwGuSmem {
+    uint4 w[SW_NW][SW_GU_LOADS][WAVE];       // each wave's slot: gate rows 2g, 2g+1, up rows 2g, 2g+1
+    uint32_t xqh[SW_MAX_T][SW_H / 4];        // x in 16-bit block fixed point: high bytes
+    uint32_t xql[SW_MAX_T][SW_H / 4];        // low bytes
+    float xqs[SW_MAX_T][SW_H / 32];          // block scales
+    float xsum[SW_MAX_T][SW_H / 16];         // fp32 sums of 16-column runs
+    float red[SW_NW][16];                    // each wave's reduced dots
+};
+static_assert(sizeof(SwGuSmem) <= 160 * 1024, "LDS");
+
+// x_t of columns 4c..4c+3 to fixed point (the decode kernel's conversion:
+// per 32-column block s = max|x| / 32511, x ~= s (256 hi + lo)); eight
+// consecutive lanes hold one block.
+__device__ __forceinline__ void sw_quant(SwGuSmem &M, int t, int c, float4 v)
+{
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    m = fmaxf(m, dpp_f<0xB1>(m));
+    m = fmaxf(m, dpp_f<0x4E>(m));
+    m = fmaxf(m, dpp_f<0x141>(m));
+    const float inv = m > 0.f ? 32511.0f / m : 0.f;
+    const float xv[4] = {v.x, v.y, v.z, v.w};
+    uint32_t hw = 0, lw = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int q = __float2int_rn(xv[k] * inv);
+        const int hi = (q + 128) >> 8;
+        const int lo = q - 256 * hi;
+        hw |= ((uint32_t)hi & 0xFFu) << (8 * k);
+        lw |= ((uint32_t)lo & 0xFFu) << (8 * k);
+    }
+    M.xqh[t][c] = hw;
+    M.xql[t][c] = lw;
+    if ((c & 7) == 0) M.xqs[t][c >> 3] = m / 32511.0f;
+    float r = (v.x + v.y) + (v.z + v.w);
+    r += dpp_f<0xB1>(r);
+    r += dpp_f<0x4E>(r);
+    if ((c & 3) == 0) M.xsum[t][c >> 2] = r;
+}
+
+// The slot's gate/up rows of this workgroup into the wave's LDS staging.
+__device__ __forceinline__ void sw_gu_issue(SwGuSmem &M, const SbLayer &L, int e, int g, int wid, int lane)
+{
+    const uint8_t *gs = (e < 0 ? L.gate_sh : L.gate_exps + (uint64_t)e * L.gate_eb) + (size_t)(2 * g) * SW_ROW16 * 16;
+    const uint8_t *us = (e < 0 ? L.up_sh : L.up_exps + (uint64_t)e * L.up_eb) + (size_t)(2 * g) * SW_ROW16 * 16;
+#pragma unroll
+    for (int k = 0; k < SW_GU_LOADS; k++) {
+        const int c = WAVE * k + lane;
+        if (c < SW_GU_CH) {
+            const uint8_t *src = c < 2 * SW_ROW16 ? gs + 16 * c : us + 16 * (c - 2 * SW_ROW16);
+            __builtin_amdgcn_global_load_lds(src, &M.w[wid][k][0], 16, 0, 0);
+        }
+    }
+}
+
+// Transposed wave reduction steps: two values a, b a lane become one, each
+// summed over a pair of lane groups, a kept by the lower group and b by the
+// upper.  tr32 pairs lane L with L^32 (permlane32 swap), tr16 L with L^16
+// inside each half (permlane16 swap), tr8 and tr4 L with the mirrored lane
+// of the 16- or 8-lane group (DPP).  The swaps' two results pass through an
+// empty asm: hipcc (ROCm 7.2) otherwise adds result 0 to itself when both
+// results of a swap with two different operands meet in one sum.
+__device__ __forceinline__ float tr32(float a, float b)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                                    false, false);
+    uint32_t r0 = r[0], r1 = r[1];
+    asm volatile("" : "+v"(r0), "+v"(r1));
+    return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+}
+
+__device__ __forceinline__ float tr16(float a, float b)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                                    false, false);
+    uint32_t r0 = r[0], r1 = r[1];
+    asm volatile("" : "+v"(r0), "+v"(r1));
+    return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+}
+
+__device__ __forceinline__ float tr8(float a, float b, int lane)
+{
+    const bool hi = (lane & 8) != 0;
+    return (hi ? b : a) + dpp_f<0x140>(hi ? a : b);  // row_mirror: lane i reads 15 - i
+}
+
+__device__ __forceinline__ float tr4(float a, float b, int lane)
+{
+    const bool hi = (lane & 4) != 0;
+    return (hi ? b : a) + dpp_f<0x141>(hi ? a : b);  // row_half_mirror: lane i reads 7 - i of its 8
+}
+
+// v[i] summed over the wave lands in lanes 4i .. 4i+3.
+__device__ __forceinline__ float reduce16(const float (&v)[16], int lane)
+{
+    float u[8], w4[4], x2[2];
+#pragma unroll
+    for (int i = 0; i < 8; i++) u[i] = tr32(v[i], v[i + 8]);
+#pragma unroll
+    for (int i = 0; i < 4; i++) w4[i] = tr16(u[i], u[i + 4]);
+#pragma unroll
+    for (int i = 0; i < 2; i++) x2[i] = tr8(w4[i], w4[i + 2], lane);
+    float y = tr4(x2[0], x2[1], lane);
+    y += dpp_f<0xB1>(y);  // quad_perm [1,0,3,2]
+    y += dpp_f<0x4E>(y);  // quad_perm [2,3,0,1]
+    return y;
+}
+
+__global__ __launch_bounds__(SW_NT, 1) void k_sw_gateup(SbLayer L, const float *__restrict__ x, SbSlots S,
+                                                        float *__restrict__ h, int E, int K, int T, int max_slots)
+{
+    __shared__ SwGuSmem M;
+    const int g = (int)blockIdx.x, tid = (int)threadIdx.x, wid = tid / WAVE, lane = lane_id();
+    const int P = T * (K + 1);
+    int ns = *S.n;
+    ns = ns < max_slots ? (ns > 0 ? ns : 0) : max_slots;
+    // activations requested first (a wait for them must not include the
+    // weights), then the first slot's weights, then the conversion
+    constexpr int XI = SW_MAX_T * (SW_H / 4) / SW_NT;  // conversion items a thread (8)
+    float4 xv[XI];
+#pragma unroll
+    for (int i = 0; i < XI; i++) {
+        const int it = SW_NT * i + tid, t = it / (SW_H / 4), c = it % (SW_H / 4);
+        xv[i] = t < T ? *reinterpret_cast<const float4 *>(x + (size_t)t * SW_H + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    int e0 = -2;
+    if (wid < ns) {
+        e0 = __builtin_amdgcn_readfirstlane(S.expert[wid]);
+        if (e0 >= -1 && e0 < E) sw_gu_issue(M, L, e0, g, wid, lane);
+    }
+#pragma unroll
+    for (int i = 0; i < XI; i++) {
+        const int it = SW_NT * i + tid, t = it / (SW_H / 4), c = it % (SW_H / 4);
+        if (t < T) sw_quant(M, t, c, xv[i]);
+    }
+    __syncthreads();
+    const int base = (lane >> 3) * QK + 64 * ((lane & 7) >> 1) + 16 * (lane & 1);  // the lane's columns (gu_base)
+    const uint32_t j = (uint32_t)(lane & 7) >> 1;
+    const int sbl = lane >> 3, cq = lane & 7;
+    const uint4 *wf = &M.w[wid][0][0];
+    // the staging holds slot s; the next slot's loads go out as soon as slot
+    // s is unpacked into registers, so they overlap its dot products
+    int e = e0;
+    for (int s = wid; s < ns; s += SW_NW) {
+        const int sn = s + SW_NW;
+        const int en = sn < ns ? __builtin_amdgcn_readfirstlane(S.expert[sn]) : -2;
+        const int cnt_s = __builtin_amdgcn_readfirstlane(S.cnt[s]);
+        const bool ok = e >= -1 && e < E;
+        const int cnt = ok ? (cnt_s < SB_CH ? (cnt_s > 0 ? cnt_s : 0) : SB_CH) : 0;
+        int pr[SB_CH];
+#pragma unroll
+        for (int k = 0; k < SB_CH; k++) {
+            const int p = k < cnt ? __builtin_amdgcn_readfirstlane(S.pair[(size_t)s * SB_CH + k]) : -1;
+            pr[k] = p >= 0 && p < P ? p : -1;
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's staging has landed
+        // the four row chunks of the lane (m = 2 mat + row: gate rows 0, 1,
+        // up rows 0, 1), unpacked once for every token of the slot
+        uint32_t qlo[4][4], qhi[4][4];
+        float dsc0[4], dsc1[4], dm0[4], dm1[4];
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const int hx = SW_ROW16 * (m & 1) + 2 * SW_ROW16 * (m >> 1) + 9 * sbl;
+            const uint4 hd = wf[hx], q = wf[hx + 1 + cq];
+            const uint32_t scm = q4k_scale_pair(hd, j);
+            const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+            dsc0[m] = d * (float)byte_of(scm, 0);
+            dsc1[m] = d * (float)byte_of(scm, 1);
+            dm0[m] = dmin * (float)byte_of(scm, 2);
+            dm1[m] = dmin * (float)byte_of(scm, 3);
+            const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                qlo[m][t] = qw[t] & 0x0F0F0F0Fu;
+                qhi[m][t] = (qw[t] >> 4) & 0x0F0F0F0Fu;
+            }
+        }
+        // the staging is read (the LDS reads above completed): next slot's loads
+        __builtin_amdgcn_s_waitcnt(WAITCNT_LGKM0);
+        if (en >= -1 && en < E) sw_gu_issue(M, L, en, g, wid, lane);
+        e = en;
+        if (!ok) continue;
+        // v[4 m + k]: the lane's part of row chunk m times token k
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < SB_CH; k++) {
+            const int t = pr[k] >= 0 ? pr[k] / (K + 1) : 0;
+            const uint4 lh = *reinterpret_cast<const uint4 *>(&M.xqh[t][base >> 2]);
+            const uint4 ll = *reinterpret_cast<const uint4 *>(&M.xql[t][base >> 2]);
+            const uint4 hh = *reinterpret_cast<const uint4 *>(&M.xqh[t][(base >> 2) + 8]);
+            const uint4 hl = *reinterpret_cast<const uint4 *>(&M.xql[t][(base >> 2) + 8]);
+            const float2 sc = *reinterpret_cast<const float2 *>(&M.xqs[t][base >> 5]);
+            const float sxl = M.xsum[t][base >> 4], sxh = M.xsum[t][(base >> 4) + 2];
+            const uint32_t xlh[4] = {lh.x, lh.y, lh.z, lh.w}, xll[4] = {ll.x, ll.y, ll.z, ll.w};
+            const uint32_t xhh[4] = {hh.x, hh.y, hh.z, hh.w}, xhl[4] = {hl.x, hl.y, hl.z, hl.w};
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                int a_lh = 0, a_ll = 0, a_hh = 0, a_hl = 0;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    a_lh = __builtin_amdgcn_sdot4((int)qlo[m][q], (int)xlh[q], a_lh, false);
+                    a_ll = __builtin_amdgcn_sdot4((int)qlo[m][q], (int)xll[q], a_ll, false);
+                    a_hh = __builtin_amdgcn_sdot4((int)qhi[m][q], (int)xhh[q], a_hh, false);
+                    a_hl = __builtin_amdgcn_sdot4((int)qhi[m][q], (int)xhl[q], a_hl, false);
+                }
+                const float al = (float)(a_lh * 256 + a_ll) * sc.x;
+                const float ah = (float)(a_hh * 256 + a_hl) * sc.y;
+                v[4 * m + k] = k < cnt ? dsc0[m] * al - dm0[m] * sxl + dsc1[m] * ah - dm1[m] * sxh : 0.f;
+            }
+        }
+        const float tot = reduce16(v, lane);
+        if ((lane & 3) == 0) M.red[wid][lane >> 2] = tot;
+        __builtin_amdgcn_wave_barrier();
+        // lane k < cnt: token k's SwiGLU of rows 2g, 2g+1 (gate m = row, up m = 2 + row)
+        if (lane < cnt) {
+            int p = pr[0];
+#pragma unroll
+            for (int k = 1; k < SB_CH; k++)
+                if (lane == k) p = pr[k];
+            if (p >= 0) {
+                const float h0 = silu_mul(M.red[wid][lane], M.red[wid][8 + lane]);
+                const float h1 = silu_mul(M.red[wid][4 + lane], M.red[wid][12 + lane]);
+                *reinterpret_cast<float2 *>(h + (size_t)p * SW_I + 2 * g) = make_float2(h0, h1);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+struct SwDnSmem {
+    uint4 band[SW_NW][SW_DN_LOADS][WAVE];  // each wave's four down rows of its slot
+    float hst[SW_NW / 2][SB_CH][SW_I];     // the slot's SwiGLU rows, shared by its two waves
+    float dot[SW_MAX_P][8];                // per pair: the workgroup's eight output rows
+    int hin[SW_NW];                        // per wave: rounds whose loads have landed
+    int hout[SW_NW];                       // per wave: rounds whose SwiGLU rows it has used
+};
+static_assert(sizeof(SwDnSmem) <= 160 * 1024, "LDS");
+
+// Bounded wait on a partner wave's LDS round counter.
+__device__ __forceinline__ void sw_wait(const int *p, int target)
+{
+    for (uint32_t it = 0; it < (1u << 20); it++) {
+        if (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+__device__ __forceinline__ void sw_put(int *p, int v)
+{
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Waves 2m and 2m+1 take slots m, m + 8, ...: each its four of the
+// workgroup's eight down rows, and half of the slot's SwiGLU rows staged in
+// LDS for both.  Lane l = lane % 16 of row rr = lane / 16 owns columns
+// 64 jj + 4 l + k (jj < 8, k < 4), so a 16-byte read of one SwiGLU row covers
+// 256 consecutive bytes: superblock b = jj / 4, half n = (jj / 2) % 2, group
+// s = 2 (jj % 2) + l / 8, element 4 (l % 8) + k: the low / high nibbles of ql
+// bytes 64n + 32 (l / 8) + 4 (l % 8) + k and bit pairs s of the qh bytes
+// 32n + 4 (l % 8) + k, with scales 8n + (l % 8) / 4 + 2s
+// (dequant_q4k_cpu.c:155-170).
+__global__ __launch_bounds__(SW_NT, 1) void k_sw_down(SbLayer L, const float *__restrict__ h, SbSlots S,
+                                                      float *__restrict__ hidden, const float *__restrict__ w,
+                                                      const float *__restrict__ gsh, int E, int K, int T,
+                                                      int max_slots)
+{
+    __shared__ SwDnSmem M;
+    const int g = (int)blockIdx.x, tid = (int)threadIdx.x, wid = tid / WAVE, lane = lane_id();
+    const int P = T * (K + 1);
+    for (int i = tid; i < SW_MAX_P * 8; i += SW_NT) (&M.dot[0][0])[i] = 0.f;
+    if (tid < SW_NW) {
+        M.hin[tid] = 0;
+        M.hout[tid] = 0;
+    }
+    int ns = *S.n;
+    ns = ns < max_slots ? (ns > 0 ? ns : 0) : max_slots;
+    const int m2 = wid >> 1, u = wid & 1, pw = wid ^ 1;
+    const int l = lane & 15, rr = lane >> 4, sl = l >> 3, l7 = l & 7;
+    const uint32_t *band = reinterpret_cast<const uint32_t *>(&M.band[wid][0][0]);
+    __syncthreads();
+    // slot metadata of a round; an invalid slot has no pairs (both waves of
+    // a pair see the same slots and keep the round counters in step)
+    auto meta = [&](int s, int &e, int &cnt, int (&pr)[SB_CH]) {
+        e = s < ns ? __builtin_amdgcn_readfirstlane(S.expert[s]) : -2;
+        const bool ok = e >= -1 && e < E;
+        const int cnt_s = ok ? __builtin_amdgcn_readfirstlane(S.cnt[s]) : 0;
+        cnt = ok ? (cnt_s < SB_CH ? (cnt_s > 0 ? cnt_s : 0) : SB_CH) : 0;
+#pragma unroll
+        for (int k = 0; k < SB_CH; k++) {
+            const int p = k < cnt ? __builtin_amdgcn_readfirstlane(S.pair[(size_t)s * SB_CH + k]) : -1;
+            pr[k] = p >= 0 && p < P ? p : -1;
+        }
+    };
+    auto issue_band = [&](int e) {
+        const uint8_t *src = (e < 0 ? L.down_sh : L.down_exps + (uint64_t)e * L.down_eb) +
+                             (size_t)(8 * g + 4 * u) * SW_DN_ROW;
+#pragma unroll
+        for (int k = 0; k < SW_DN_LOADS; k++) {
+            const int c = WAVE * k + lane;
+            if (c < SW_DN_CH) __builtin_amdgcn_global_load_lds(src + 16 * c, &M.band[wid][k][0], 16, 0, 0);
+        }
+    };
+    // this wave's pairs (k % 2 == u) of the slot's SwiGLU rows: 2 KB, two loads each
+    auto issue_h = [&](const int (&pr)[SB_CH]) {
+#pragma unroll
+        for (int k = 0; k < SB_CH; k++) {
+            if ((k & 1) != u || pr[k] < 0) continue;
+            const float *hs = h + (size_t)pr[k] * SW_I;
+#pragma unroll
+            for (int q = 0; q < SW_I / (4 * WAVE); q++)
+                __builtin_amdgcn_global_load_lds(hs + 4 * (WAVE * q + lane), &M.hst[m2][k][4 * WAVE * q], 16, 0, 0);
+        }
+    };
+    int e, cnt, pr[SB_CH];
+    meta(m2, e, cnt, pr);
+    if (cnt > 0) {
+        issue_band(e);
+        issue_h(pr);
+    }
+    int rnd = 0;
+    for (int s = m2; s < ns; s += SW_NW / 2, rnd++) {
+        int en, cntn, prn[SB_CH];
+        meta(s + SW_NW / 2, en, cntn, prn);
+        __builtin_amdgcn_s_waitcnt(0);  // this round's band and this wave's SwiGLU rows
+        if (lane == 0) sw_put(&M.hin[wid], rnd + 1);
+        sw_wait(&M.hin[pw], rnd + 1);
+        if (cnt > 0) {
+            // pre-decode the lane's 32 weights of row rr: w[4 jj + k] = (d sc)
+            // (q - 32) as fma(q, ds, -32 ds), one rounding
+            float wq[32];
+#pragma unroll
+            for (int bn = 0; bn < 4; bn++) {
+                const int b = bn >> 1, n = bn & 1;
+                const uint32_t ob = (uint32_t)(rr * SW_DN_ROW + b * Q6K_BYTES);
+                const uint32_t o1 = ob + 64 * n + 32 * sl + 4 * l7, o2 = ob + 128 + 32 * n + 4 * l7;
+                const uint32_t ql = __builtin_amdgcn_alignbyte(band[(o1 + 3) >> 2], band[o1 >> 2], o1 & 3u);
+                const uint32_t qh = __builtin_amdgcn_alignbyte(band[(o2 + 3) >> 2], band[o2 >> 2], o2 & 3u);
+                const uint2 scw = lds8_a2(band, ob + 192 + 8 * n);
+                const float d = h2f(lds16_a2(band, ob + 208));
+                const uint32_t q[2] = {(ql & 0x0F0F0F0Fu) | (((qh >> (2 * sl)) & 0x03030303u) << 4),
+                                       ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * sl + 4)) & 0x03030303u) << 4)};
+#pragma unroll
+                for (int ee = 0; ee < 2; ee++) {
+                    const float ds = d * q6k_scale(scw, (uint32_t)((l7 >> 2) + 2 * (2 * ee + sl)));
+                    const float nds = -32.0f * ds;
+                    const int jj = 4 * b + 2 * n + ee;
+#pragma unroll
+                    for (int k = 0; k < 4; k++) wq[4 * jj + k] = fmaf((float)byte_of(q[ee], k), ds, nds);
+                }
+            }
+            // the band is read: the next round's band goes out during the dots
+            __builtin_amdgcn_s_waitcnt(WAITCNT_LGKM0);
+            if (cntn > 0) issue_band(en);
+#pragma unroll
+            for (int k = 0; k < SB_CH; k++) {
+                if (pr[k] < 0) continue;
+                const float *hr = &M.hst[m2][k][4 * l];
+                float acc = 0.f;
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++) {
+                    const float4 hv = *reinterpret_cast<const float4 *>(hr + 64 * jj);
+                    acc = fmaf(wq[4 * jj + 0], hv.x, acc);
+                    acc = fmaf(wq[4 * jj + 1], hv.y, acc);
+                    acc = fmaf(wq[4 * jj + 2], hv.z, acc);
+                    acc = fmaf(wq[4 * jj + 3], hv.w, acc);
+                }
+                acc = sum16(acc);
+                if (l == 0) M.dot[pr[k]][4 * u + rr] = acc;
+            }
+        } else if (cntn > 0) {
+            issue_band(en);
+        }
+        // both waves are done with this round's SwiGLU rows: the next round's
+        __builtin_amdgcn_s_waitcnt(WAITCNT_LGKM0);
+        if (lane == 0) sw_put(&M.hout[wid], rnd + 1);
+        sw_wait(&M.hout[pw], rnd + 1);
+        if (cntn > 0) issue_h(prn);
+        e = en;
+        cnt = cntn;
+#pragma unroll
+        for (int k = 0; k < SB_CH; k++) pr[k] = prn[k];
+    }
+    __syncthreads();
+    // combine in the reference order (one_layer.cu:1443-1471): shared expert
+    // first, then the routed experts by rank
+    if (tid < T * 8) {
+#pragma clang fp contract(off)
+        const int t = tid >> 3, r = tid & 7;
+        const int pb = t * (K + 1);
+        float v = hidden[(size_t)t * SW_H + 8 * g + r];
+        const float sw = 1.0f / (1.0f + expf(-gsh[t]));
+        v += sw * M.dot[pb][r];
+        for (int k = 0; k < K; k++) v += w[(size_t)t * K + k] * M.dot[pb + 1 + k][r];
+        hidden[(size_t)t * SW_H + 8 * g + r] = v;
+    }
+}
+
 }  // namespace
 
 bool bread_small_supported(const bread_moe_shape_t &s, const bread_moe_layer_t *L)
@@ -647,6 +1078,14 @@ int bread_launch_moe_small(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const
     else
         hipLaunchKernelGGL(k_sb_select<16>, dim3(1), dim3(RT_THREADS), 0, st, c->logits, E, K, T, c->idx, c->w,
                            g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots);
+    if (H == SW_H && I == SW_I && Ish == SW_I && K <= SW_K && T <= SW_MAX_T) {
+        // the decode shape: every workgroup owns a slice of every slot
+        hipLaunchKernelGGL(k_sw_gateup, dim3(SW_G), dim3(SW_NT), 0, st, sl, x, ss, c->h, E, K, T, S);
+        hipLaunchKernelGGL(k_sw_down, dim3(SW_G), dim3(SW_NT), 0, st, sl, c->h, ss, hidden, c->w, c->gsh, E, K, T,
+                           S);
+        BREAD_HIP(hipGetLastError());
+        return BREAD_OK;
+    }
     hipLaunchKernelGGL(k_sb_gateup, dim3(S, (Imax + GU_RG - 1) / GU_RG), dim3(256), 0, st, sl, x, ss, c->h, H, I,
                        Ish, E, K, T, Imax);
     hipLaunchKernelGGL(k_sb_down, dim3(S, (H + DN_RG - 1) / DN_RG), dim3(256), 0, st, sl, c->h, ss, g.eo, H, I, Ish,

@@ -166,11 +166,9 @@ typedef enum {
 int bread_moe_ctx_set_path(bread_moe_ctx_t *ctx, int path);
 /* Largest n_tokens the automatic choice sends to the small-batch path. */
 int bread_small_auto_tokens(void);
-/* Largest n_tokens for which the automatic choice runs one decode launch per
- * token: in bread_moe_forward (one layer) and in bread_moe_stack_forward (one
- * launch of the whole stack per token).  No reference counterpart; the
- * crossovers measured on MI355X against the small-batch path. */
-int bread_decode_loop_tokens(void);
+/* Largest n_tokens for which bread_moe_stack_forward's automatic choice runs
+ * one launch of the whole decode stack per token.  No reference counterpart;
+ * the crossover measured on MI355X against the small-batch path. */
 int bread_stack_loop_tokens(void);
 
 /* Synchronises the context's last stream and returns BREAD_ERR_DEVICE (and
@@ -207,9 +205,8 @@ int bread_route_layer(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer, cons
  * d_x_normed fp32 [n_tokens][H] (the post-attention RMSNorm output),
  * d_hidden fp32 [n_tokens][H] in/out.  Optional outputs d_idx/d_w/d_gsh as in
  * bread_route (may be NULL).  Path (bread_moe_ctx_set_path, default
- * BREAD_PATH_AUTO): up to bread_decode_loop_tokens() tokens run the persistent
- * decode kernel, one launch per token, when the shape allows it (see
- * bread_moe_decode_layers); small batches (up to
+ * BREAD_PATH_AUTO): n_tokens == 1 runs the persistent decode kernel when the
+ * shape allows it (see bread_moe_decode_layers); small batches (up to
  * bread_small_auto_tokens()) run the small-batch path (each selected expert's
  * rows streamed once over the whole GPU and dotted with the tokens that chose
  * it, fp32; H <= 2048, intermediate sizes 256 or 512); larger batches run the

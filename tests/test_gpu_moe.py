@@ -180,27 +180,6 @@ def test_decode_back_to_back_launches(full_layer):
     assert ctx.check_device() == 0
 
 
-@pytest.mark.parametrize("T", [2, 3])
-def test_auto_small_batches_run_decode_per_token(full_layer, T):
-    """Under the automatic choice, up to bread_decode_loop_tokens() tokens run
-    one decode launch per token: outputs and routing equal single-token calls
-    bit for bit, and match the oracle."""
-    s, t, hl = full_layer
-    assert T <= B.lib.bread_decode_loop_tokens()
-    x = xs(T, s.hidden, 300 + T)
-    hidden = xs(T, s.hidden, 400 + T)
-    ctx = B.MoeContext(s, max_tokens=T)
-    got, gi, gw, gg = run_forward(ctx, t, x, hidden)
-    for k in range(T):
-        one = run_forward(ctx, t, x[k:k + 1], hidden[k:k + 1])
-        assert np.array_equal(got[k].view(np.uint32), one[0][0].view(np.uint32))
-        assert np.array_equal(gi[k], one[1][0]) and np.array_equal(gw[k], one[2][0]) and gg[k] == one[3][0]
-    ref, ri, rw, rg = oracle_forward(hl, x, hidden)
-    assert np.array_equal(gi, np.asarray(ri).reshape(gi.shape))
-    assert_moe_close(got, ref, base=hidden)
-    assert ctx.check_device() == 0
-
-
 def test_decode_vs_multi_kernel_path(full_layer):
     """The single-launch kernel (fp32 but for 16-bit fixed-point gate/up
     activations) and the per-token kernels (fp32) agree to ~3e-5; the grouped

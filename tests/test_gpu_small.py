@@ -159,14 +159,16 @@ def test_small_repeat_is_bitwise_stable(zipf_layer):
 
 
 def test_small_matches_per_token_path(full_layer):
-    """Both paths compute in fp32: same routing, outputs within ~1e-6."""
+    """Same routing; outputs within ~4e-5 (the small-batch path's gate/up dots
+    take 16-bit fixed-point activations at the decode shape; the per-token
+    path is fp32)."""
     s, t, _ = full_layer
     x = tokens(24, s.hidden, 51, zipf=False)
     hidden = np.zeros_like(x)
     a = run(s, t, x, hidden, path=api.PATH_SMALL)
     b = run(s, t, x, hidden, path=api.PATH_PER_TOKEN)
     assert np.array_equal(a[1], b[1])
-    assert rel_l2(a[0], b[0]) < 1e-5
+    assert rel_l2(a[0], b[0]) < 1e-4
 
 
 def test_small_auto_choice(full_layer):
