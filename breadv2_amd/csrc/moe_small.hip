@@ -1,6 +1,8 @@
 // moe_small.hip — the small-batch MoE path (2 <= n_tokens <= 32; the
-// automatic choice uses it up to 8: batched decode, speculative-verify
-// rounds).
+// automatic choice uses it up to 16: batched decode, speculative-verify
+// rounds).  At the decode shape (H 2048, I = I_sh = 512, K <= 8) and up to
+// 16 tokens, k_sw_gateup and k_sw_down (end of the file) replace the
+// per-slot gate/up, down and combine kernels.
 //
 // Per token the result is the MoE block of one_layer_forward
 // (one_layer.cu:1800-1986; CPU form 1413-1471), computed in fp32 like the
