@@ -1,5 +1,6 @@
 """GPU parity of the small-batch path (2..32 tokens: selected experts' rows
-streamed over the whole GPU, fp32 dots) against the CPU oracle.
+streamed over the whole GPU; at the decode shape and up to 16 tokens the
+workgroup-per-CU kernels with integer gate/up dots) against the CPU oracle.
 
 The oracle is the per-token MoE block (one_layer.cu:1413-1471) applied to
 every token: routing bit-exact (indices in rank order), renormalised weights
@@ -119,6 +120,30 @@ def test_small_other_shapes(dims):
     hl = host_layer(t)
     x = tokens(T, H, 31 + T, zipf=False)
     hidden = np.random.default_rng(5).standard_normal(x.shape).astype(np.float32)
+    check(hl, x, hidden, run(s, t, x, hidden))
+
+
+def test_small_wide_hot_experts(full_layer):
+    """Decode-shape kernels: 16 copies of one token (every expert of the
+    token chosen 16 times: four slots of four pairs each per expert, the
+    shared expert too), and a single token."""
+    s, t, hl = full_layer
+    x = np.repeat(tokens(1, s.hidden, 71, zipf=False), 16, axis=0)
+    hidden = np.random.default_rng(72).standard_normal(x.shape).astype(np.float32)
+    check(hl, x, hidden, run(s, t, x, hidden))
+    x1 = tokens(1, s.hidden, 73, zipf=False)
+    check(hl, x1, np.zeros_like(x1), run(s, t, x1, np.zeros_like(x1)))
+
+
+@pytest.mark.parametrize("E,K,T", [(256, 4, 16), (128, 8, 11), (64, 6, 5), (256, 1, 3)])
+def test_small_wide_other_k_e(E, K, T):
+    """Decode shape (H 2048, I 512) with other expert counts and top-k."""
+    s = api.shape(n_experts=E, top_k=K)
+    t = api.synth_layer_tensors(s, seed=500 + E + K, layer=0)
+    torch.cuda.synchronize()
+    hl = host_layer(t)
+    x = tokens(T, s.hidden, 600 + T, zipf=False)
+    hidden = np.random.default_rng(601).standard_normal(x.shape).astype(np.float32)
     check(hl, x, hidden, run(s, t, x, hidden))
 
 
