@@ -18,9 +18,10 @@
 //   waves 9, 10  shared-expert gate/up rows (before routing is known);
 //   waves 9..15  the down-projection bands of the routed slots (8 rows x
 //                420 B each);
-//   waves 4..15  the next layer's routing-independent weights (router row,
+//   waves 12..15 the next layer's routing-independent weights (router row,
 //                norm weights, shared-gate vector, shared gate/up rows and
-//                shared down band), once this layer's h is in.
+//                shared down band), once this layer's h is in; waves 0..3
+//                load the first layer's at kernel entry.
 // Weights travel HBM -> LDS by gfx950 direct-to-LDS loads, so no wave holds
 // weight registers while loads are in flight.  On gfx9, s_waitcnt vmcnt counts
 // loads and stores together and in order, so a poll issued behind weight
@@ -611,16 +612,18 @@ __device__ __forceinline__ void down_dot_lds(Smem &S, int u, const float4 (*src)
 
 // ---------------------------------------------------------------- fixed weights
 
-// Routing-independent weights of a layer into LDS, by waves 12..15 (256
+// Routing-independent weights of a layer into LDS, by waves wb..wb+3 (256
 // lanes, 8 direct-to-LDS loads each): router row g, norm weights, shared-gate
 // vector, shared gate/up rows and the shared down band (into sdown[sb]).
-// These waves never poll, so the loads delay no exchange (gfx9 completes a
-// wave's loads in order).
-__device__ __forceinline__ void prefetch(Smem &S, const DecLayer &Ly, int g, int E, int wid, int sb)
+// Between layers waves 12..15 issue them: they never poll, so the loads delay
+// no exchange (gfx9 completes a wave's loads in order).  At kernel entry
+// waves 0..3 do: a workgroup's waves start over about a microsecond, wave 0
+// first.
+__device__ __forceinline__ void prefetch(Smem &S, const DecLayer &Ly, int g, int E, int wid, int sb, int wb)
 {
     const int lane = opaque(lane_id());
-    if (wid < W_PF) return;
-    const int w4 = wid - W_PF;           // 0..3
+    if (wid < wb || wid >= wb + 4) return;
+    const int w4 = wid - wb;             // 0..3
     const int c = WAVE * w4 + lane;      // 0..255
 #pragma unroll
     for (int i = 0; i < 2; i++) {        // 16-byte chunk c + 256 i of a 2048-float row
@@ -650,9 +653,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
     const int NU = 2 * (K + 1);   // down units
     bread_decode_sync *sy = a.sync;
     const float sent = __builtin_bit_cast(float, SENTINEL);
+    // No barrier here: one would wait for the prefetch (a barrier waits for
+    // the wave's direct-to-LDS loads), serialising it with layer 0's input
+    // load.  P1's barrier publishes S.abort = 0; layer 0 never polls, so no
+    // wave sets S.abort before it.
     if (tid == 0) S.abort = 0;
-    prefetch(S, load_layer(a, 0), g, E, wid, 0);
-    __syncthreads();
+    prefetch(S, load_layer(a, 0), g, E, wid, 0, 0);
 
     for (int l = 0; l < a.L; l++) {
         // per-lane values recomputed each layer rather than kept live
@@ -702,6 +708,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             const float ss = wave_sum(fmaf(hv.x, hv.x, fmaf(hv.y, hv.y, fmaf(hv.z, hv.z, hv.w * hv.w))));
             if (lane == 0) S.red[wid] = ss;
             if (!ok) S.abort = 1;
+            if (l == 0 && wid < 4) __builtin_amdgcn_s_waitcnt(0);  // the kernel-entry prefetch has landed
         } else if (wid >= W_PF) {
             __builtin_amdgcn_s_waitcnt(0);  // the layer's prefetched weights have landed
         }
@@ -874,7 +881,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             // layer's are consumed (the shared gate/up was used before waves
             // 9 and 10 loaded their bands)
             if (wid >= W_PF && l + 1 < a.L && lds_wait(S, &S.dncnt, N_DN, true))
-                prefetch(S, load_layer(a, l + 1), g, E, wid, (l + 1) & 1);
+                prefetch(S, load_layer(a, l + 1), g, E, wid, (l + 1) & 1, W_PF);
         }
 
         // ---- P4 + P5: pre-decode this wave's down unit once every band is
@@ -957,7 +964,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
         trace_point(a, l, TP_COMB);
 
         // ---- P7: next layer's fixed weights (every buffer they land in has
-        // been consumed) by waves 4..15; combine in the reference order
+        // been consumed) by waves 12..15; combine in the reference order
         // (one_layer.cu:1443-1471) and publish the rows to the next layer and
         // the caller by wave 0
 
