@@ -9,11 +9,12 @@
 // Workgroup g owns router row g, gate/up rows 2g and 2g+1 of every expert
 // slot (slot 0 = shared expert, slot k = routed rank k-1) and output rows
 // 8g..8g+7.  Its 16 waves have fixed jobs:
-//   all waves    poll the previous layer's output (two columns a thread);
+//   waves 0..7   poll the previous layer's output (four columns a thread),
+//                normalise it and take the router-row and shared-gate dots
+//                of their columns;
 //   waves 0..3   poll the router logits (wave 0 then runs softmax/top-k and
 //                the combine);
-//   waves 1..8   router row and shared-gate dot, then the gate/up rows of
-//                routed slot k = wave;
+//   waves 1..8   the gate/up rows of routed slot k = wave;
 //   waves 4..11  x in 16-bit block fixed point, during the logits exchange;
 //   waves 9, 10  shared-expert gate/up rows (before routing is known);
 //   waves 9..15  the down-projection bands of the routed slots (8 rows x
@@ -181,7 +182,7 @@ struct Smem {
     uint4 gu[MAXK][4 * GR][WAVE];      // routed gate/up rows: [slot-1][4 row + (hg, qg, hu, qu)][lane]
     float lg[256];                     // router logits of the layer
     float red[NWV];                    // sum-of-squares partials
-    float rl[MAXK], gl[MAXK];          // router / shared-gate partials
+    float rl[N_XPOLL], gl[N_XPOLL];    // router / shared-gate partials of the polling waves
     float dot[NSLOT][OR];              // down dots
     float hown[OR];                    // this workgroup's rows of h before the layer
     int idx[MAXK];                     // routed experts, rank order
@@ -203,7 +204,10 @@ static_assert(sizeof(Smem) > 80 * 1024 && sizeof(Smem) <= 160 * 1024, "LDS footp
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_t bytes)
 {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, (int)BUF_WORD3);
+    // the base is made wave-uniform explicitly: a descriptor the compiler
+    // keeps in vector registers costs a waterfall loop around every load
+    return __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(const_cast<void *>(base)), (short)0,
+                                             uniform((int)bytes), (int)BUF_WORD3);
 }
 
 // An empty asm hides v's value from the optimiser, so per-lane address math
@@ -328,18 +332,6 @@ __device__ __forceinline__ bool poll4(bread_decode_sync *s, __amdgpu_buffer_rsrc
     for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
         v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX_COHERENT));
         if (!unwritten(v.x) && !unwritten(v.y) && !(hi && (unwritten(v.z) || unwritten(v.w)))) return true;
-        if ((it & 63) == 63 && has_error(s)) return false;
-        __builtin_amdgcn_s_sleep(1);
-    }
-    flag_error(s, 1u);
-    return false;
-}
-
-__device__ __forceinline__ bool poll2(bread_decode_sync *s, __amdgpu_buffer_rsrc_t r, uint32_t off, float2 &v)
-{
-    for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
-        v = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, AUX_COHERENT));
-        if (!unwritten(v.x) && !unwritten(v.y)) return true;
         if ((it & 63) == 63 && has_error(s)) return false;
         __builtin_amdgcn_s_sleep(1);
     }
@@ -728,37 +720,32 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                 }
             }
             *reinterpret_cast<float4 *>(&S.x[4 * tid]) = hv;
-        }
-        __syncthreads();
-        trace_point(a, l, TP_XREADY);
-
-        // ---- P2: router / shared-gate partials (waves 1..8, 4 columns a lane)
-        if (wid >= W_GU && wid < W_GU + MAXK) {
-            const int tr = tid - W_GU * WAVE;
-            const float4 xv = *reinterpret_cast<const float4 *>(&S.x[4 * tr]);
+            // P2: router / shared-gate partials of the wave's 256 columns,
+            // from the registers that already hold them
             float r = 0.f, q = 0.f;
             if (g < E) {
-                const float4 wr = *reinterpret_cast<const float4 *>(&S.wrow[4 * tr]);
-                r = fmaf(wr.x, xv.x, fmaf(wr.y, xv.y, fmaf(wr.z, xv.z, wr.w * xv.w)));
+                const float4 wr = *reinterpret_cast<const float4 *>(&S.wrow[4 * tid]);
+                r = fmaf(wr.x, hv.x, fmaf(wr.y, hv.y, fmaf(wr.z, hv.z, wr.w * hv.w)));
             }
             if (Ly.shg) {
-                const uint2 hh = *reinterpret_cast<const uint2 *>(&S.shg[4 * tr]);
-                q = fmaf(h2f(hh.x), xv.x, fmaf(h2f(hh.x >> 16), xv.y, fmaf(h2f(hh.y), xv.z, h2f(hh.y >> 16) * xv.w)));
+                const uint2 hh = *reinterpret_cast<const uint2 *>(&S.shg[4 * tid]);
+                q = fmaf(h2f(hh.x), hv.x, fmaf(h2f(hh.x >> 16), hv.y, fmaf(h2f(hh.y), hv.z, h2f(hh.y >> 16) * hv.w)));
             }
             r = wave_sum(r);
             q = wave_sum(q);
             if (lane == 0) {
-                S.rl[wid - W_GU] = r;
-                S.gl[wid - W_GU] = q;
+                S.rl[wid] = r;
+                S.gl[wid] = q;
             }
         }
         __syncthreads();
+        trace_point(a, l, TP_XREADY);
 
         // ---- P3: logits, routing, expert streams
         if (wid < NPOLL) {
             float logit = 0.f;
 #pragma unroll
-            for (int w = 0; w < MAXK; w++) logit += S.rl[w];
+            for (int w = 0; w < N_XPOLL; w++) logit += S.rl[w];
             if (wid == 0) {
                 if (lane == 0 && g < E)
                     __hip_atomic_store(a.tlogits + LG_STRIDE * g,
@@ -805,7 +792,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                     const float wk = renorm_weight(lane < K ? S.key[lane] : 0u, K);
                     float gsh = 0.f;
 #pragma unroll
-                    for (int w = 0; w < MAXK; w++) gsh += S.gl[w];
+                    for (int w = 0; w < N_XPOLL; w++) gsh += S.gl[w];
                     if (lane < K) S.w[lane] = wk;
                     if (lane == 0) S.sgsh = sigmoidf_ref(gsh);
                     if (g == 0) {
