@@ -14,9 +14,9 @@
 //
 // Kernels per layer, stream-ordered:
 //   k_sb_router   one router row a wave held in registers, dotted with every
-//                 token (the next token's activations requested while the
-//                 current one is summed); the extra row E is the fp16
-//                 shared-gate vector.
+//                 token (batches of 4 tokens, one batch's activations
+//                 requested while the other's are summed); the extra row E is
+//                 the fp16 shared-gate vector.
 //   k_sb_select   one workgroup: softmax / top-k per token, then slots: an
 //                 expert's tokens in chunks of at most SB_CH (the shared
 //                 expert's chunks first, with every token, then the chosen
@@ -161,15 +161,67 @@ __device__ void sb_select(const float *__restrict__ logits, int E, int K, int T,
     for (int t = tid; t < T; t += RT_THREADS) slot_pair[t] = t * (K + 1);  // slot t / SB_CH, place t % SB_CH
 }
 
-// Router rows: one a wave held in registers, dotted with every token (the
-// next token's activations requested while the current one is summed); the
-// extra row E is the fp16 shared-gate vector.
-__global__ __launch_bounds__(256) void k_sb_router(const float *__restrict__ router, const uint16_t *__restrict__ shg,
-                                                   const float *__restrict__ x, float *__restrict__ logits,
-                                                   float *__restrict__ gsh, int H, int E, int T)
+// Router rows: one a wave held in registers, dotted with every token; the
+// extra row E is the fp16 shared-gate vector.  Tokens go in batches of RB
+// through two register buffers in turn: one batch's activations are in flight
+// while the other's are summed, so a call costs about T / (2 RB) L2 round
+// trips rather than T.
+constexpr int RB = 4;
+
+__device__ __forceinline__ void load_batch(const float *x, int t0, int T, int H, int lane, int nm,
+                                           float4 (&v)[RB][MAX_H / 256])
 {
-    const int wv = (int)threadIdx.x / WAVE, lane = lane_id();
-    const int e = (int)blockIdx.x * 4 + wv;
+#pragma unroll
+    for (int j = 0; j < RB; j++) {
+        if (t0 + j < T) {
+            load_row4(x + (size_t)(t0 + j) * H, lane, nm, v[j]);
+        } else {
+#pragma unroll
+            for (int m = 0; m < MAX_H / 256; m++) v[j][m] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+}
+
+// The batch's RB dot products advance together (independent chains, each in
+// router_row_dot's order); tokens past T have zero activations and are not
+// stored.
+__device__ __forceinline__ void dot_batch(const float4 (&r)[MAX_H / 256], const float4 (&v)[RB][MAX_H / 256], int t0,
+                                          int T, int e, int E, int lane, const uint16_t *shg, float *logits,
+                                          float *gsh)
+{
+    float acc[RB];
+#pragma unroll
+    for (int j = 0; j < RB; j++) acc[j] = 0.f;
+#pragma unroll
+    for (int m = 0; m < MAX_H / 256; m++) {
+#pragma unroll
+        for (int j = 0; j < RB; j++) {
+            acc[j] = fmaf(r[m].x, v[j][m].x, acc[j]);
+            acc[j] = fmaf(r[m].y, v[j][m].y, acc[j]);
+            acc[j] = fmaf(r[m].z, v[j][m].z, acc[j]);
+            acc[j] = fmaf(r[m].w, v[j][m].w, acc[j]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < RB; j++) acc[j] = wave_sum(acc[j]);
+    if (lane == 0) {
+#pragma unroll
+        for (int j = 0; j < RB; j++) {
+            if (t0 + j >= T) break;
+            if (e < E) logits[(size_t)(t0 + j) * E + e] = acc[j];
+            else gsh[t0 + j] = shg ? acc[j] : 0.f;
+        }
+    }
+}
+
+// One wave a workgroup: each wave reads every token's activations, so the
+// E + 1 waves are spread over every CU's L1 rather than four to a CU.
+__global__ __launch_bounds__(WAVE) void k_sb_router(const float *__restrict__ router, const uint16_t *__restrict__ shg,
+                                                    const float *__restrict__ x, float *__restrict__ logits,
+                                                    float *__restrict__ gsh, int H, int E, int T)
+{
+    const int lane = lane_id();
+    const int e = (int)blockIdx.x;
     if (e > E) return;
     const int nm = H / 256;
     // this wave's row: lane holds columns 4 lane + 256 m (router_row_dot's order)
@@ -186,25 +238,18 @@ __global__ __launch_bounds__(256) void k_sb_router(const float *__restrict__ rou
             }
         }
     }
-    float4 xc[MAX_H / 256], xn[MAX_H / 256];
-    load_row4(x, lane, nm, xc);
-    for (int t = 0; t < T; t++) {
-        if (t + 1 < T) load_row4(x + (size_t)(t + 1) * H, lane, nm, xn);
-        float acc = 0.f;
-#pragma unroll
-        for (int m = 0; m < MAX_H / 256; m++) {
-            acc = fmaf(r[m].x, xc[m].x, acc);
-            acc = fmaf(r[m].y, xc[m].y, acc);
-            acc = fmaf(r[m].z, xc[m].z, acc);
-            acc = fmaf(r[m].w, xc[m].w, acc);
-        }
-        acc = wave_sum(acc);
-        if (lane == 0) {
-            if (e < E) logits[(size_t)t * E + e] = acc;
-            else gsh[t] = shg ? acc : 0.f;
-        }
-#pragma unroll
-        for (int m = 0; m < MAX_H / 256; m++) xc[m] = xn[m];
+    // every wave reads every token's activations: wave e starts at batch
+    // e mod nb, so the waves spread over the activations (and the L2
+    // channels holding them) instead of all reading one row at a time
+    const int nb = (T + RB - 1) / RB, b0 = e % nb;
+    auto tb = [&](int i) { return (b0 + i < nb ? b0 + i : b0 + i - nb) * RB; };
+    float4 xa[RB][MAX_H / 256], xb[RB][MAX_H / 256];
+    load_batch(x, tb(0), T, H, lane, nm, xa);
+    for (int i = 0; i < nb; i += 2) {
+        if (i + 1 < nb) load_batch(x, tb(i + 1), T, H, lane, nm, xb);
+        dot_batch(r, xa, tb(i), T, e, E, lane, shg, logits, gsh);
+        if (i + 2 < nb) load_batch(x, tb(i + 2), T, H, lane, nm, xa);
+        if (i + 1 < nb) dot_batch(r, xb, tb(i + 1), T, e, E, lane, shg, logits, gsh);
     }
 }
 
@@ -1072,7 +1117,7 @@ int bread_launch_moe_small(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const
                      L->gate_expert_bytes, L->up_expert_bytes, L->down_expert_bytes};
     const SbSlots ss{g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots};
     bread_clear_stale_error();
-    hipLaunchKernelGGL(k_sb_router, dim3((E + 1 + 3) / 4), dim3(256), 0, st, L->router, L->shexp_gate, x, c->logits,
+    hipLaunchKernelGGL(k_sb_router, dim3(E + 1), dim3(WAVE), 0, st, L->router, L->shexp_gate, x, c->logits,
                        c->gsh, H, E, T);
     if (E <= 4 * WAVE)
         hipLaunchKernelGGL(k_sb_select<4>, dim3(1), dim3(RT_THREADS), 0, st, c->logits, E, K, T, c->idx, c->w,
