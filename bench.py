@@ -432,8 +432,9 @@ def main() -> int:
         }
     if args.mt_steps > 0 and L >= 40:
         result["multi_token"] = {
-            "path": "automatic: small-batch (2..8 tokens: selected experts' rows over the whole GPU, fp32 dots) or "
-                    "grouped (tokens bucketed by expert, fp16 MFMA expert GEMMs, fp32 accumulate)",
+            "path": "automatic: small-batch (2..16 tokens: selected experts' rows over the whole GPU, fp32 dots; "
+                    "gate/up on 16-bit fixed-point activations at the decode shape) or grouped (more tokens: "
+                    "bucketed by expert, fp16 MFMA expert GEMMs, fp32 accumulate)",
             "mfma_peak_tflops": MFMA_F16_PEAK_TFS,
             "flops_note": "algorithmic: 9 x 6,291,456 per token (8 routed + shared) + router 1,048,576; "
                           "executed MFMA work is higher (32-pair tiles padded, activations as hi+lo fp16)",
