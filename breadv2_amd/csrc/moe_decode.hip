@@ -89,7 +89,7 @@ constexpr int BAND16 = BAND / 16;        // 210 16-byte chunks
 constexpr int MAXK = 8;
 constexpr int NSLOT = MAXK + 1;
 constexpr int NPOLL = 4;                 // waves 0..3 poll the logits, one a lane
-constexpr int W_GU = 1;                  // waves 1..8: router partials, routed gate/up
+constexpr int W_GU = 1;                  // waves 1..8: routed gate/up, slot k = wave
 constexpr int W_SH = 9;                  // waves 9, 10: shared gate/up
 constexpr int W_DN = 9;                  // waves 9..15: routed down bands
 constexpr int N_DN = NWV - W_DN;         // 7
@@ -97,7 +97,7 @@ constexpr int DN_LOADS = (MAXK * BAND16 + N_DN * WAVE - 1) / (N_DN * WAVE);  // 
 constexpr int W_XQ = 4;                  // waves 4..11 convert x to fixed point (quant_x)
 constexpr int N_XQ = 8;
 constexpr int W_PF = 12;                 // waves 12..15 prefetch routing-independent weights, never poll
-constexpr int N_XPOLL = 8;               // waves 0..7 poll the previous layer's output, 4 columns a thread
+constexpr int N_XPOLL = 8;               // waves 0..7 poll the previous layer's output (4 columns a thread) and take the router partials
 constexpr int N_HPOLL = W_PF;            // waves 0..11 poll the SwiGLU outputs
 constexpr uint32_t SPIN_LIMIT = 1u << 18;
 constexpr uint32_t BUF_WORD3 = 0x00020000u;  // raw buffer descriptor word 3 (gfx9)
@@ -122,7 +122,7 @@ static_assert(G * ((MAXK + 2) / 2) <= 2 * N_HPOLL * WAVE, "h poll: at most two c
 // Trace points recorded per (workgroup, layer) when a trace buffer is given.
 enum {
     TP_START = 0,   // layer entered
-    TP_XREADY = 1,  // previous layer's output seen, x in LDS
+    TP_XREADY = 1,  // previous layer's output seen, x in LDS, router partials taken
     TP_LOGIT = 2,   // own logit published
     TP_POLLED = 3,  // every logit seen
     TP_RANK1 = 4,   // rank-1 expert known
