@@ -21,8 +21,8 @@
 //                420 B each);
 //   waves 12..15 the next layer's routing-independent weights (router row,
 //                norm weights, shared-gate vector, shared gate/up rows and
-//                shared down band), once this layer's h is in; waves 0..3
-//                load the first layer's at kernel entry.
+//                shared down band), once this layer's h is in, and the first
+//                layer's at kernel entry.
 // Weights travel HBM -> LDS by gfx950 direct-to-LDS loads, so no wave holds
 // weight registers while loads are in flight.  On gfx9, s_waitcnt vmcnt counts
 // loads and stores together and in order, so a poll issued behind weight
@@ -100,6 +100,7 @@ constexpr int W_PF = 12;                 // waves 12..15 prefetch routing-indepe
 constexpr int N_XPOLL = 8;               // waves 0..7 poll the previous layer's output (4 columns a thread) and take the router partials
 constexpr int N_HPOLL = W_PF;            // waves 0..11 poll the SwiGLU outputs
 constexpr uint32_t SPIN_LIMIT = 1u << 18;
+constexpr int WAITCNT_VM3 = 3 | (7 << 4) | (15 << 8);  // s_waitcnt vmcnt(3), other counters free (gfx9 encoding)
 constexpr uint32_t BUF_WORD3 = 0x00020000u;  // raw buffer descriptor word 3 (gfx9)
 constexpr int AUX_COHERENT = 16;             // sc1: device-coherent access
 constexpr uint32_t SENTINEL = 0x7FA5A5A5u;   // signalling NaN: "not written yet"
@@ -289,7 +290,19 @@ __device__ __forceinline__ void trace_point(const DecArgs &a, int l, int tp)
 // The layer record is the same for the whole grid: keep it in scalar registers.
 __device__ __forceinline__ DecLayer load_layer(const DecArgs &a, int l)
 {
-    DecLayer d = a.layers ? a.layers[l] : a.one;
+    // the table is read through the constant address space: scalar loads,
+    // counted apart from the wave's vector loads, so reading a record does
+    // not wait for the weight loads in flight
+    typedef const __attribute__((address_space(4))) uint64_t *ConstWords;
+    static_assert(sizeof(DecLayer) % 8 == 0, "layer record in 64-bit words");
+    DecLayer d = a.one;
+    if (a.layers) {
+        const ConstWords p = (ConstWords)uniform_ptr(a.layers + l);
+        uint64_t w[sizeof(DecLayer) / 8];
+#pragma unroll
+        for (int i = 0; i < (int)(sizeof(DecLayer) / 8); i++) w[i] = p[i];
+        __builtin_memcpy(&d, w, sizeof(d));
+    }
     d.gate_exps = uniform_ptr(d.gate_exps);
     d.up_exps = uniform_ptr(d.up_exps);
     d.down_exps = uniform_ptr(d.down_exps);
@@ -604,18 +617,18 @@ __device__ __forceinline__ void down_dot_lds(Smem &S, int u, const float4 (*src)
 
 // ---------------------------------------------------------------- fixed weights
 
-// Routing-independent weights of a layer into LDS, by waves wb..wb+3 (256
+// Routing-independent weights of a layer into LDS, by waves 12..15 (256
 // lanes, 8 direct-to-LDS loads each): router row g, norm weights, shared-gate
 // vector, shared gate/up rows and the shared down band (into sdown[sb]).
-// Between layers waves 12..15 issue them: they never poll, so the loads delay
-// no exchange (gfx9 completes a wave's loads in order).  At kernel entry
-// waves 0..3 do: a workgroup's waves start over about a microsecond, wave 0
-// first.
-__device__ __forceinline__ void prefetch(Smem &S, const DecLayer &Ly, int g, int E, int wid, int sb, int wb)
+// These waves never poll and never load a layer's input, so the loads delay
+// no exchange: gfx9 completes a wave's loads in order, and the layer-record
+// load at the top of each layer is followed by a wait for all of the wave's
+// loads.
+__device__ __forceinline__ void prefetch(Smem &S, const DecLayer &Ly, int g, int E, int wid, int sb)
 {
     const int lane = opaque(lane_id());
-    if (wid < wb || wid >= wb + 4) return;
-    const int w4 = wid - wb;             // 0..3
+    if (wid < W_PF) return;
+    const int w4 = wid - W_PF;           // 0..3
     const int c = WAVE * w4 + lane;      // 0..255
 #pragma unroll
     for (int i = 0; i < 2; i++) {        // 16-byte chunk c + 256 i of a 2048-float row
@@ -628,6 +641,8 @@ __device__ __forceinline__ void prefetch(Smem &S, const DecLayer &Ly, int g, int
     const uint8_t *base = ((w4 & 1) ? Ly.up_sh : Ly.gate_sh) + (size_t)r * GU_ROW;
     const uint32_t oh = (uint32_t)((lane >> 3) * Q4K_BYTES);
     const uint32_t oq = oh + 16u + 16u * (uint32_t)(lane & 7);
+    // the shared gate/up rows and the down band go last: P1 waits only for
+    // the five loads above (vmcnt <= 3), the next barrier for these three
     lds_load16(base + oh, &S.shw[w4 >> 1][2 * (w4 & 1)][0]);
     lds_load16(base + oq, &S.shw[w4 >> 1][2 * (w4 & 1) + 1][0]);
     if (c < BAND16) lds_load16(Ly.down_sh + (size_t)g * BAND + 16 * c, &S.sdown[sb][4 * WAVE * w4]);
@@ -650,7 +665,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
     // load.  P1's barrier publishes S.abort = 0; layer 0 never polls, so no
     // wave sets S.abort before it.
     if (tid == 0) S.abort = 0;
-    prefetch(S, load_layer(a, 0), g, E, wid, 0, 0);
+    prefetch(S, load_layer(a, 0), g, E, wid, 0);
 
     for (int l = 0; l < a.L; l++) {
         // per-lane values recomputed each layer rather than kept live
@@ -700,9 +715,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             const float ss = wave_sum(fmaf(hv.x, hv.x, fmaf(hv.y, hv.y, fmaf(hv.z, hv.z, hv.w * hv.w))));
             if (lane == 0) S.red[wid] = ss;
             if (!ok) S.abort = 1;
-            if (l == 0 && wid < 4) __builtin_amdgcn_s_waitcnt(0);  // the kernel-entry prefetch has landed
         } else if (wid >= W_PF) {
-            __builtin_amdgcn_s_waitcnt(0);  // the layer's prefetched weights have landed
+            // the layer's router row, norm weights and shared-gate vector
+            // have landed (the prefetch's first five loads; the shared
+            // gate/up rows and down band, issued last, are waited for before
+            // the next barrier)
+            __builtin_amdgcn_s_waitcnt(WAITCNT_VM3);
         }
         __syncthreads();
         if (S.abort) break;
@@ -737,6 +755,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                 S.rl[wid] = r;
                 S.gl[wid] = q;
             }
+        } else if (wid >= W_PF) {
+            __builtin_amdgcn_s_waitcnt(0);  // the rest of the prefetch (shared gate/up rows, shared down band)
         }
         __syncthreads();
         trace_point(a, l, TP_XREADY);
@@ -868,7 +888,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             // layer's are consumed (the shared gate/up was used before waves
             // 9 and 10 loaded their bands)
             if (wid >= W_PF && l + 1 < a.L && lds_wait(S, &S.dncnt, N_DN, true))
-                prefetch(S, load_layer(a, l + 1), g, E, wid, (l + 1) & 1, W_PF);
+                prefetch(S, load_layer(a, l + 1), g, E, wid, (l + 1) & 1);
         }
 
         // ---- P4 + P5: pre-decode this wave's down unit once every band is
