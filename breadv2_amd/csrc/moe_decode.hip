@@ -192,6 +192,7 @@ struct Smem {
     float sgsh;                        // sigmoid of the shared-gate logit
     int nready;                        // ranks published in idx
     int lgcnt;                         // polling waves done with the logits
+    int rlcnt;                         // x-polling waves whose router partials are in S.rl
     int dncnt;                         // down waves whose bands are in LDS
     int gucnt;                         // routed gate/up waves whose weights are in LDS
     int xqcnt;                         // waves done converting their part of x (quant_x)
@@ -693,6 +694,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                 S.xqcnt = 0;
                 S.gudone = 0;
                 S.lgcnt = 0;
+                S.rlcnt = 0;
                 S.dncnt = 0;
                 S.gucnt = 0;
             }
@@ -754,6 +756,19 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             if (lane == 0) {
                 S.rl[wid] = r;
                 S.gl[wid] = q;
+                lds_add(&S.rlcnt, 1);
+            }
+            // wave 0 publishes the logit as soon as the partials are in,
+            // without waiting for the other waves at the barrier below
+            if (wid == 0 && lds_wait(S, &S.rlcnt, N_XPOLL)) {
+                float logit = 0.f;
+#pragma unroll
+                for (int w = 0; w < N_XPOLL; w++) logit += S.rl[w];
+                if (lane == 0 && g < E)
+                    __hip_atomic_store(a.tlogits + LG_STRIDE * g,
+                                       ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, logit),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                trace_point(a, l, TP_LOGIT);
             }
         } else if (wid >= W_PF) {
             __builtin_amdgcn_s_waitcnt(0);  // the rest of the prefetch (shared gate/up rows, shared down band)
@@ -765,14 +780,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
         if (wid < NPOLL) {
             float logit = 0.f;
 #pragma unroll
-            for (int w = 0; w < N_XPOLL; w++) logit += S.rl[w];
-            if (wid == 0) {
-                if (lane == 0 && g < E)
-                    __hip_atomic_store(a.tlogits + LG_STRIDE * g,
-                                       ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, logit),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                trace_point(a, l, TP_LOGIT);
-            }
+            for (int w = 0; w < N_XPOLL; w++) logit += S.rl[w];  // as published (own entry)
             // poll one logit a lane
             float v = -__builtin_inff();
             bool ok = true;
