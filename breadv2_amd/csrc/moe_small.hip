@@ -13,10 +13,11 @@
 // vector ALUs.
 //
 // Kernels per layer, stream-ordered:
-//   k_sb_router   one router row a wave held in registers, dotted with every
-//                 token (batches of 4 tokens, one batch's activations
-//                 requested while the other's are summed); the extra row E is
-//                 the fp16 shared-gate vector.
+//   k_sb_router   one router row a workgroup of 4 waves, a quarter of the row
+//                 a wave held in registers, dotted with every token (batches
+//                 of 4 tokens, one batch's activations requested while the
+//                 other's are summed); the extra row E is the fp16
+//                 shared-gate vector.
 //   k_sb_select   one workgroup: softmax / top-k per token, then slots: an
 //                 expert's tokens in chunks of at most SB_CH (the shared
 //                 expert's chunks first, with every token, then the chosen
@@ -161,39 +162,43 @@ __device__ void sb_select(const float *__restrict__ logits, int E, int K, int T,
     for (int t = tid; t < T; t += RT_THREADS) slot_pair[t] = t * (K + 1);  // slot t / SB_CH, place t % SB_CH
 }
 
-// Router rows: one a wave held in registers, dotted with every token; the
-// extra row E is the fp16 shared-gate vector.  Tokens go in batches of RB
-// through two register buffers in turn: one batch's activations are in flight
-// while the other's are summed, so a call costs about T / (2 RB) L2 round
-// trips rather than T.
+// Router rows: one a workgroup of RW waves; wave v holds the 4-column chunks
+// 64 (v + RW m) + lane of the row, so each wave does a quarter of every
+// token's dot (at one wave a row the kernel was bound by the issue of ~120
+// instructions per token at one wave per SIMD).  Row E is the fp16
+// shared-gate vector.  Tokens go in batches of RB through two register
+// buffers in turn, one batch's activations in flight while the other's are
+// summed; the wave partials are added in wave order through LDS.
 constexpr int RB = 4;
+constexpr int RW = 4;                    // waves per router row
+constexpr int RM = MAX_H / (4 * WAVE * RW);  // chunks a lane holds (2)
 
-__device__ __forceinline__ void load_batch(const float *x, int t0, int T, int H, int lane, int nm,
-                                           float4 (&v)[RB][MAX_H / 256])
+__device__ __forceinline__ void load_chunks(const float *p, int lane, int wv, int nq, float4 (&v)[RM])
 {
 #pragma unroll
-    for (int j = 0; j < RB; j++) {
-        if (t0 + j < T) {
-            load_row4(x + (size_t)(t0 + j) * H, lane, nm, v[j]);
-        } else {
-#pragma unroll
-            for (int m = 0; m < MAX_H / 256; m++) v[j][m] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+    for (int m = 0; m < RM; m++) {
+        const int q = lane + WAVE * (wv + RW * m);
+        v[m] = q < nq ? *reinterpret_cast<const float4 *>(p + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 }
 
-// The batch's RB dot products advance together (independent chains, each in
-// router_row_dot's order); tokens past T have zero activations and are not
-// stored.
-__device__ __forceinline__ void dot_batch(const float4 (&r)[MAX_H / 256], const float4 (&v)[RB][MAX_H / 256], int t0,
-                                          int T, int e, int E, int lane, const uint16_t *shg, float *logits,
-                                          float *gsh)
+__device__ __forceinline__ void load_batch(const float *x, int t0, int T, int H, int lane, int wv,
+                                           float4 (&v)[RB][RM])
+{
+#pragma unroll
+    for (int j = 0; j < RB; j++) load_chunks(x + (size_t)min(t0 + j, T - 1) * H, lane, wv, H / 4, v[j]);
+}
+
+// The batch's RB partial dots advance together (independent chains); tokens
+// past T are computed on a repeated row and not stored.
+__device__ __forceinline__ void dot_batch(const float4 (&r)[RM], const float4 (&v)[RB][RM], int t0, int T, int lane,
+                                          float *part)
 {
     float acc[RB];
 #pragma unroll
     for (int j = 0; j < RB; j++) acc[j] = 0.f;
 #pragma unroll
-    for (int m = 0; m < MAX_H / 256; m++) {
+    for (int m = 0; m < RM; m++) {
 #pragma unroll
         for (int j = 0; j < RB; j++) {
             acc[j] = fmaf(r[m].x, v[j][m].x, acc[j]);
@@ -206,50 +211,51 @@ __device__ __forceinline__ void dot_batch(const float4 (&r)[MAX_H / 256], const 
     for (int j = 0; j < RB; j++) acc[j] = wave_sum(acc[j]);
     if (lane == 0) {
 #pragma unroll
-        for (int j = 0; j < RB; j++) {
-            if (t0 + j >= T) break;
-            if (e < E) logits[(size_t)(t0 + j) * E + e] = acc[j];
-            else gsh[t0 + j] = shg ? acc[j] : 0.f;
-        }
+        for (int j = 0; j < RB; j++)
+            if (t0 + j < T) part[t0 + j] = acc[j];
     }
 }
 
-// One wave a workgroup: each wave reads every token's activations, so the
-// E + 1 waves are spread over every CU's L1 rather than four to a CU.
-__global__ __launch_bounds__(WAVE) void k_sb_router(const float *__restrict__ router, const uint16_t *__restrict__ shg,
-                                                    const float *__restrict__ x, float *__restrict__ logits,
-                                                    float *__restrict__ gsh, int H, int E, int T)
+__global__ __launch_bounds__(RW * WAVE) void k_sb_router(const float *__restrict__ router,
+                                                         const uint16_t *__restrict__ shg,
+                                                         const float *__restrict__ x, float *__restrict__ logits,
+                                                         float *__restrict__ gsh, int H, int E, int T)
 {
-    const int lane = lane_id();
+    __shared__ float part[RW][SB_MAX_T];
+    const int wv = wave_id(), lane = lane_id();
     const int e = (int)blockIdx.x;
-    if (e > E) return;
-    const int nm = H / 256;
-    // this wave's row: lane holds columns 4 lane + 256 m (router_row_dot's order)
-    float4 r[MAX_H / 256];
+    const int nq = H / 4;
+    float4 r[RM];
     if (e < E) {
-        load_row4(router + (size_t)e * H, lane, nm, r);
+        load_chunks(router + (size_t)e * H, lane, wv, nq, r);
     } else {
 #pragma unroll
-        for (int m = 0; m < MAX_H / 256; m++) {
+        for (int m = 0; m < RM; m++) {
+            const int q = lane + WAVE * (wv + RW * m);
             r[m] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (m < nm && shg) {
-                const uint2 g = *reinterpret_cast<const uint2 *>(shg + 4 * lane + 256 * m);
+            if (q < nq && shg) {
+                const uint2 g = *reinterpret_cast<const uint2 *>(shg + 4 * q);
                 r[m] = make_float4(h2f(g.x), h2f(g.x >> 16), h2f(g.y), h2f(g.y >> 16));
             }
         }
     }
-    // every wave reads every token's activations: wave e starts at batch
-    // e mod nb, so the waves spread over the activations (and the L2
-    // channels holding them) instead of all reading one row at a time
-    const int nb = (T + RB - 1) / RB, b0 = e % nb;
-    auto tb = [&](int i) { return (b0 + i < nb ? b0 + i : b0 + i - nb) * RB; };
-    float4 xa[RB][MAX_H / 256], xb[RB][MAX_H / 256];
-    load_batch(x, tb(0), T, H, lane, nm, xa);
-    for (int i = 0; i < nb; i += 2) {
-        if (i + 1 < nb) load_batch(x, tb(i + 1), T, H, lane, nm, xb);
-        dot_batch(r, xa, tb(i), T, e, E, lane, shg, logits, gsh);
-        if (i + 2 < nb) load_batch(x, tb(i + 2), T, H, lane, nm, xa);
-        if (i + 1 < nb) dot_batch(r, xb, tb(i + 1), T, e, E, lane, shg, logits, gsh);
+    float4 xa[RB][RM], xb[RB][RM];
+    load_batch(x, 0, T, H, lane, wv, xa);
+    for (int t0 = 0; t0 < T; t0 += 2 * RB) {
+        load_batch(x, t0 + RB, T, H, lane, wv, xb);
+        dot_batch(r, xa, t0, T, lane, part[wv]);
+        if (t0 + RB >= T) break;
+        load_batch(x, t0 + 2 * RB, T, H, lane, wv, xa);
+        dot_batch(r, xb, t0 + RB, T, lane, part[wv]);
+    }
+    __syncthreads();
+    const int t = (int)threadIdx.x;
+    if (t < T) {
+        float v = part[0][t];
+#pragma unroll
+        for (int w = 1; w < RW; w++) v += part[w][t];
+        if (e < E) logits[(size_t)t * E + e] = v;
+        else gsh[t] = shg ? v : 0.f;
     }
 }
 
@@ -1117,7 +1123,7 @@ int bread_launch_moe_small(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const
                      L->gate_expert_bytes, L->up_expert_bytes, L->down_expert_bytes};
     const SbSlots ss{g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots};
     bread_clear_stale_error();
-    hipLaunchKernelGGL(k_sb_router, dim3(E + 1), dim3(WAVE), 0, st, L->router, L->shexp_gate, x, c->logits,
+    hipLaunchKernelGGL(k_sb_router, dim3(E + 1), dim3(RW * WAVE), 0, st, L->router, L->shexp_gate, x, c->logits,
                        c->gsh, H, E, T);
     if (E <= 4 * WAVE)
         hipLaunchKernelGGL(k_sb_select<4>, dim3(1), dim3(RT_THREADS), 0, st, c->logits, E, K, T, c->idx, c->w,
