@@ -33,8 +33,10 @@
 //   k_mt_xprep    one workgroup per token: row scale, hi/lo fp16 activations
 //                 in the gate/up operand order, shared-gate logit
 //   k_mt_router   router logits on fp32 MFMA (16 tokens x 16 experts per
-//                 workgroup, K split over 16 waves)
-//   k_topk        softmax / top-k / renormalisation (moe.hip, route_dev.h)
+//                 workgroup, K over 16 waves; up to 128 tokens over 4
+//                 workgroups of 4 waves)
+//   k_topk        softmax / top-k / renormalisation (moe.hip, route_dev.h);
+//                 up to 128 tokens k_topk_sum, which first adds the 4 K ranges
 //   k_mt_bucket   one workgroup: expert histogram, token lists by expert,
 //                 M-tiles of 32 pairs
 //   k_mt_gateup   per (M-tile, 128 rows): gate and up GEMMs, SwiGLU
@@ -311,22 +313,27 @@ __global__ __launch_bounds__(256) void k_mt_xprep(const float *__restrict__ x, c
     }
 }
 
-// logits[t][e] = router row e . x[t] (one_layer.cu:964-971), fp32 products
-// and sums.  Wave w covers K range [w*H/16, (w+1)*H/16); lane (r, g) feeds
-// token t0 + r and expert e0 + r, 4 consecutive K each 16-element chunk;
-// all of a wave's loads are issued before its MFMAs.  The 16 partial tiles
-// are summed in wave order.
+// Partial router logits part[z][t][e] = router row e . x[t] over K range z of
+// gridDim.z (one_layer.cu:964-971), fp32 products and sums.  A workgroup of
+// nw = RT_WAVES / gridDim.z waves takes one 16-token x 16-expert tile and one
+// K range; wave w covers K [(z nw + w) H/16, +H/16); lane (r, g) feeds token
+// t0 + r and expert e0 + r, 4 consecutive K each 16-element chunk; all of a
+// wave's loads are issued before its MFMAs.  The wave tiles are summed in
+// wave order; k_topk_sum adds the K ranges in order.  Splitting K over
+// workgroups puts a 64-token call on 256 workgroups instead of 64.
 __global__ __launch_bounds__(RT_WAVES * WAVE) void k_mt_router(const float *__restrict__ router,
                                                                const float *__restrict__ x,
-                                                               float *__restrict__ logits, int H, int E, int T)
+                                                               float *__restrict__ part, int H, int E, int T)
 {
-    __shared__ f32x4 part[RT_WAVES][WAVE];
+    __shared__ f32x4 wpart[RT_WAVES][WAVE];
     const int w = wave_id(), lane = lane_id();
+    const int nw = (int)(blockDim.x / WAVE), z = (int)blockIdx.z;
     const int r = lane & 15, g = lane >> 4;
     const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
     const int kq = H / RT_WAVES, nch = kq / 16;
-    const float *xr = x + (size_t)min(t0 + r, T - 1) * H + w * kq + 4 * g;
-    const float *wr = router + (size_t)min(e0 + r, E - 1) * H + w * kq + 4 * g;
+    const int k0 = (z * nw + w) * kq;
+    const float *xr = x + (size_t)min(t0 + r, T - 1) * H + k0 + 4 * g;
+    const float *wr = router + (size_t)min(e0 + r, E - 1) * H + k0 + 4 * g;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int c0 = 0; c0 < nch; c0 += 8) {
         float4 a[8], b[8];
@@ -345,17 +352,54 @@ __global__ __launch_bounds__(RT_WAVES * WAVE) void k_mt_router(const float *__re
                 acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].w, b[u].w, acc, 0, 0, 0);
             }
     }
-    part[w][lane] = acc;
+    wpart[w][lane] = acc;
     __syncthreads();
     if (w != 0) return;
-    f32x4 s = part[0][lane];
-#pragma unroll
-    for (int i = 1; i < RT_WAVES; i++) s += part[i][lane];
+    f32x4 sum = wpart[0][lane];
+    for (int i = 1; i < nw; i++) sum += wpart[i][lane];
     const int e = e0 + r;
+    float *out = part + (size_t)z * T * E;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int t = t0 + 4 * g + i;
-        if (t < T && e < E) logits[(size_t)t * E + e] = s[i];
+        if (t < T && e < E) out[(size_t)t * E + e] = sum[i];
+    }
+}
+
+// Per token: the logits as the sum of the RT_SPLIT partial K ranges in order
+// (also stored to logits), then softmax / top-k / renormalisation
+// (route_dev.h).  Every partial load is issued before the first sum (clamped
+// index, no branch), so a lane waits for one round trip.
+constexpr int RT_SPLIT = 4;  // K ranges of the router for small calls
+
+template <int MAXV>
+__global__ __launch_bounds__(WAVE) void k_topk_sum(const float *__restrict__ part, int T, int E, int K,
+                                                   float *__restrict__ logits, int32_t *__restrict__ idx,
+                                                   float *__restrict__ w)
+{
+    const int t = (int)blockIdx.x, lane = lane_id();
+    float q[RT_SPLIT][MAXV];
+#pragma unroll
+    for (int z = 0; z < RT_SPLIT; z++)
+#pragma unroll
+        for (int v = 0; v < MAXV; v++)
+            q[z][v] = part[((size_t)z * T + t) * E + min(lane + WAVE * v, E - 1)];
+    float p[MAXV];  // lane's entries lane + 64 v, topk_wave's layout
+#pragma unroll
+    for (int v = 0; v < MAXV; v++) {
+        const int e = lane + WAVE * v;
+        float sum = q[0][v];
+#pragma unroll
+        for (int z = 1; z < RT_SPLIT; z++) sum += q[z][v];
+        p[v] = e < E ? sum : -__builtin_inff();
+        if (e < E) logits[(size_t)t * E + e] = sum;
+    }
+    int ik;
+    float wk;
+    topk_wave_vals<MAXV>(p, E, K, ik, wk);
+    if (lane < K) {
+        idx[(size_t)t * K + lane] = ik;
+        w[(size_t)t * K + lane] = wk;
     }
 }
 
@@ -854,11 +898,25 @@ int bread_launch_moe_grouped(bread_moe_ctx_t *c, const bread_moe_layer_t *L, con
     hipLaunchKernelGGL(k_mt_xprep, dim3(T), dim3(256), 0, st, x, (const uint16_t *)L->shexp_gate, H,
                        (uint4 *)g.xhi, (uint4 *)g.xlo, g.xexp, c->gsh);
     BREAD_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_mt_router, dim3((T + 15) / 16, (E + 15) / 16), dim3(RT_WAVES * WAVE), 0, st,
-                       (const float *)L->router, x, c->logits, H, E, T);
+    // Up to 128 tokens the router tiles are too few for the device: K goes
+    // over RT_SPLIT workgroups per tile, partials in the expert-output buffer
+    // (written only by the down kernel, after the top-k has read them).
+    const bool split = T <= 128 && (size_t)(K + 1) * H >= (size_t)RT_SPLIT * E;
+    const int RS = split ? RT_SPLIT : 1;
+    float *part = split ? g.eo : c->logits;
+    hipLaunchKernelGGL(k_mt_router, dim3((T + 15) / 16, (E + 15) / 16, RS), dim3(RT_WAVES / RS * WAVE), 0, st,
+                       (const float *)L->router, x, part, H, E, T);
     BREAD_HIP(hipGetLastError());
-    int rc = bread_launch_topk(c->logits, E, K, T, c->idx, c->w, st);
-    if (rc) return rc;
+    if (split) {
+        if ((E + WAVE - 1) / WAVE <= 4)
+            hipLaunchKernelGGL(k_topk_sum<4>, dim3(T), dim3(WAVE), 0, st, part, T, E, K, c->logits, c->idx, c->w);
+        else
+            hipLaunchKernelGGL(k_topk_sum<16>, dim3(T), dim3(WAVE), 0, st, part, T, E, K, c->logits, c->idx, c->w);
+        BREAD_HIP(hipGetLastError());
+    } else {
+        const int rc = bread_launch_topk(c->logits, E, K, T, c->idx, c->w, st);
+        if (rc) return rc;
+    }
     hipLaunchKernelGGL(k_mt_bucket, dim3(1), dim3(1024), 0, st, c->idx, T, K, E, g.pair_tok, g.pos_of,
                        (MtTile *)g.tiles, g.n_tiles);
     BREAD_HIP(hipGetLastError());
