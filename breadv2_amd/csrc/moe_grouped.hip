@@ -62,6 +62,7 @@ constexpr int GU_ROWS = GU_WAVES / 2 * 32;       // SwiGLU rows per gate/up work
 constexpr int DN_WAVES = 8, DN_BLOCKS = 2;       // 32-row down blocks per wave
 constexpr int DN_ROWS = DN_WAVES * DN_BLOCKS * 32;  // output rows per down workgroup
 constexpr int RT_WAVES = 16;                     // router K split
+constexpr int RT_SPLIT = 4;                      // K ranges over workgroups for calls up to 128 tokens
 constexpr int MAX_INTER = 512;                   // largest intermediate size the LDS plan holds
 constexpr uint32_t MAGIC = 0x64646464u;          // fp16 0x64xx = 1024 + xx
 
@@ -268,12 +269,11 @@ __device__ __forceinline__ void q6k_load(const uint8_t *sb, int g, Q6Raw &R)
 // Activation preparation and router
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(256) void k_mt_xprep(const float *__restrict__ x, const uint16_t *__restrict__ shg,
-                                                  int H, uint4 *__restrict__ xhi, uint4 *__restrict__ xlo,
-                                                  int *__restrict__ xexp, float *__restrict__ gsh)
+__device__ __forceinline__ void mt_xprep(int t, const float *__restrict__ x, const uint16_t *__restrict__ shg, int H,
+                                         uint4 *__restrict__ xhi, uint4 *__restrict__ xlo, int *__restrict__ xexp,
+                                         float *__restrict__ gsh)
 {
     __shared__ float smax[4], sdot[4];
-    const int t = blockIdx.x;
     const float *xt = x + (size_t)t * H;
     float mx = 0.f, dot = 0.f;
     for (int i = 4 * (int)threadIdx.x; i < H; i += 1024) {
@@ -313,6 +313,13 @@ __global__ __launch_bounds__(256) void k_mt_xprep(const float *__restrict__ x, c
     }
 }
 
+__global__ __launch_bounds__(256) void k_mt_xprep(const float *__restrict__ x, const uint16_t *__restrict__ shg,
+                                                  int H, uint4 *__restrict__ xhi, uint4 *__restrict__ xlo,
+                                                  int *__restrict__ xexp, float *__restrict__ gsh)
+{
+    mt_xprep((int)blockIdx.x, x, shg, H, xhi, xlo, xexp, gsh);
+}
+
 // Partial router logits part[z][t][e] = router row e . x[t] over K range z of
 // gridDim.z (one_layer.cu:964-971), fp32 products and sums.  A workgroup of
 // nw = RT_WAVES / gridDim.z waves takes one 16-token x 16-expert tile and one
@@ -321,15 +328,14 @@ __global__ __launch_bounds__(256) void k_mt_xprep(const float *__restrict__ x, c
 // wave's loads are issued before its MFMAs.  The wave tiles are summed in
 // wave order; k_topk_sum adds the K ranges in order.  Splitting K over
 // workgroups puts a 64-token call on 256 workgroups instead of 64.
-__global__ __launch_bounds__(RT_WAVES * WAVE) void k_mt_router(const float *__restrict__ router,
-                                                               const float *__restrict__ x,
-                                                               float *__restrict__ part, int H, int E, int T)
+__device__ __forceinline__ void mt_router(int bx, int by, int z, const float *__restrict__ router,
+                                          const float *__restrict__ x, float *__restrict__ part, int H, int E, int T)
 {
     __shared__ f32x4 wpart[RT_WAVES][WAVE];
     const int w = wave_id(), lane = lane_id();
-    const int nw = (int)(blockDim.x / WAVE), z = (int)blockIdx.z;
+    const int nw = (int)(blockDim.x / WAVE);
     const int r = lane & 15, g = lane >> 4;
-    const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
+    const int t0 = bx * 16, e0 = by * 16;
     const int kq = H / RT_WAVES, nch = kq / 16;
     const int k0 = (z * nw + w) * kq;
     const float *xr = x + (size_t)min(t0 + r, T - 1) * H + k0 + 4 * g;
@@ -366,12 +372,32 @@ __global__ __launch_bounds__(RT_WAVES * WAVE) void k_mt_router(const float *__re
     }
 }
 
+__global__ __launch_bounds__(RT_WAVES * WAVE) void k_mt_router(const float *__restrict__ router,
+                                                               const float *__restrict__ x,
+                                                               float *__restrict__ part, int H, int E, int T)
+{
+    mt_router((int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, router, x, part, H, E, T);
+}
+
+// Small calls: the split router's tiles (RT_SPLIT workgroups of 4 waves each)
+// and the activation preparation in one launch: workgroups [0, nr) are
+// router (tile, K range) pairs, the next T prepare one token each.  Both only
+// read x.
+__global__ __launch_bounds__(RT_WAVES / RT_SPLIT * WAVE) void k_mt_route_prep(
+    const float *__restrict__ router, const float *__restrict__ x, float *__restrict__ part, int H, int E, int T,
+    const uint16_t *__restrict__ shg, uint4 *__restrict__ xhi, uint4 *__restrict__ xlo, int *__restrict__ xexp,
+    float *__restrict__ gsh)
+{
+    const int nbx = (T + 15) / 16, nby = (E + 15) / 16, nr = nbx * nby * RT_SPLIT;
+    const int b = (int)blockIdx.x;
+    if (b < nr) mt_router(b % nbx, (b / nbx) % nby, b / (nbx * nby), router, x, part, H, E, T);
+    else mt_xprep(b - nr, x, shg, H, xhi, xlo, xexp, gsh);
+}
+
 // Per token: the logits as the sum of the RT_SPLIT partial K ranges in order
 // (also stored to logits), then softmax / top-k / renormalisation
 // (route_dev.h).  Every partial load is issued before the first sum (clamped
 // index, no branch), so a lane waits for one round trip.
-constexpr int RT_SPLIT = 4;  // K ranges of the router for small calls
-
 template <int MAXV>
 __global__ __launch_bounds__(WAVE) void k_topk_sum(const float *__restrict__ part, int T, int E, int K,
                                                    float *__restrict__ logits, int32_t *__restrict__ idx,
@@ -895,17 +921,24 @@ int bread_launch_moe_grouped(bread_moe_ctx_t *c, const bread_moe_layer_t *L, con
     const int Imax = s.expert_inter > s.shared_inter ? s.expert_inter : s.shared_inter;
     bread_grouped_ws &g = c->gws;
     bread_clear_stale_error();
-    hipLaunchKernelGGL(k_mt_xprep, dim3(T), dim3(256), 0, st, x, (const uint16_t *)L->shexp_gate, H,
-                       (uint4 *)g.xhi, (uint4 *)g.xlo, g.xexp, c->gsh);
-    BREAD_HIP(hipGetLastError());
     // Up to 128 tokens the router tiles are too few for the device: K goes
     // over RT_SPLIT workgroups per tile, partials in the expert-output buffer
-    // (written only by the down kernel, after the top-k has read them).
+    // (written only by the down kernel, after the top-k has read them), and
+    // the activation preparation shares the launch.
     const bool split = T <= 128 && (size_t)(K + 1) * H >= (size_t)RT_SPLIT * E;
-    const int RS = split ? RT_SPLIT : 1;
     float *part = split ? g.eo : c->logits;
-    hipLaunchKernelGGL(k_mt_router, dim3((T + 15) / 16, (E + 15) / 16, RS), dim3(RT_WAVES / RS * WAVE), 0, st,
-                       (const float *)L->router, x, part, H, E, T);
+    if (split) {
+        const int nr = ((T + 15) / 16) * ((E + 15) / 16) * RT_SPLIT;
+        hipLaunchKernelGGL(k_mt_route_prep, dim3(nr + T), dim3(RT_WAVES / RT_SPLIT * WAVE), 0, st,
+                           (const float *)L->router, x, part, H, E, T, (const uint16_t *)L->shexp_gate,
+                           (uint4 *)g.xhi, (uint4 *)g.xlo, g.xexp, c->gsh);
+    } else {
+        hipLaunchKernelGGL(k_mt_xprep, dim3(T), dim3(256), 0, st, x, (const uint16_t *)L->shexp_gate, H,
+                           (uint4 *)g.xhi, (uint4 *)g.xlo, g.xexp, c->gsh);
+        BREAD_HIP(hipGetLastError());
+        hipLaunchKernelGGL(k_mt_router, dim3((T + 15) / 16, (E + 15) / 16, 1), dim3(RT_WAVES * WAVE), 0, st,
+                           (const float *)L->router, x, part, H, E, T);
+    }
     BREAD_HIP(hipGetLastError());
     if (split) {
         if ((E + WAVE - 1) / WAVE <= 4)
