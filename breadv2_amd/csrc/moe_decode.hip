@@ -100,7 +100,6 @@ constexpr int W_PF = 12;                 // waves 12..15 prefetch routing-indepe
 constexpr int N_XPOLL = 8;               // waves 0..7 poll the previous layer's output (4 columns a thread) and take the router partials
 constexpr int N_HPOLL = W_PF;            // waves 0..11 poll the SwiGLU outputs
 constexpr uint32_t SPIN_LIMIT = 1u << 18;
-constexpr int WAITCNT_VM3 = 3 | (7 << 4) | (15 << 8);  // s_waitcnt vmcnt(3), other counters free (gfx9 encoding)
 constexpr uint32_t BUF_WORD3 = 0x00020000u;  // raw buffer descriptor word 3 (gfx9)
 constexpr int AUX_COHERENT = 16;             // sc1: device-coherent access
 constexpr uint32_t SENTINEL = 0x7FA5A5A5u;   // signalling NaN: "not written yet"
@@ -642,8 +641,6 @@ __device__ __forceinline__ void prefetch(Smem &S, const DecLayer &Ly, int g, int
     const uint8_t *base = ((w4 & 1) ? Ly.up_sh : Ly.gate_sh) + (size_t)r * GU_ROW;
     const uint32_t oh = (uint32_t)((lane >> 3) * Q4K_BYTES);
     const uint32_t oq = oh + 16u + 16u * (uint32_t)(lane & 7);
-    // the shared gate/up rows and the down band go last: P1 waits only for
-    // the five loads above (vmcnt <= 3), the next barrier for these three
     lds_load16(base + oh, &S.shw[w4 >> 1][2 * (w4 & 1)][0]);
     lds_load16(base + oq, &S.shw[w4 >> 1][2 * (w4 & 1) + 1][0]);
     if (c < BAND16) lds_load16(Ly.down_sh + (size_t)g * BAND + 16 * c, &S.sdown[sb][4 * WAVE * w4]);
@@ -718,11 +715,9 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             if (lane == 0) S.red[wid] = ss;
             if (!ok) S.abort = 1;
         } else if (wid >= W_PF) {
-            // the layer's router row, norm weights and shared-gate vector
-            // have landed (the prefetch's first five loads; the shared
-            // gate/up rows and down band, issued last, are waited for before
-            // the next barrier)
-            __builtin_amdgcn_s_waitcnt(WAITCNT_VM3);
+            // the layer's prefetched weights have landed (the barrier below
+            // is a workgroup fence: it waits for them anyway)
+            __builtin_amdgcn_s_waitcnt(0);
         }
         __syncthreads();
         if (S.abort) break;
@@ -770,8 +765,6 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 trace_point(a, l, TP_LOGIT);
             }
-        } else if (wid >= W_PF) {
-            __builtin_amdgcn_s_waitcnt(0);  // the rest of the prefetch (shared gate/up rows, shared down band)
         }
         __syncthreads();
         trace_point(a, l, TP_XREADY);
