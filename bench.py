@@ -38,6 +38,9 @@ EXPERT_BYTES = 2_039_808                # gate 589,824 + up 589,824 + down 860,1
 LAYER_EXPERT_BYTES = 9 * EXPERT_BYTES   # 8 routed + 1 shared = 18,358,272
 LAYER_TOTAL_BYTES = LAYER_EXPERT_BYTES + 2_097_152 + 4_096 + 16_384  # + router, shared gate, x/y
 HBM_PEAK_GBS = 8000.0
+PREROLL = 64                            # untimed launches queued before the start event
+CFG1_ROWS, CFG1_COLS = 512, 2048        # config 1: one expert gate projection
+CFG1_BYTES = 589_824 + 8_192 + 2_048    # W + fp32 x + fp32 y = 600,064 B
 
 
 def log(msg: str) -> None:
@@ -91,6 +94,93 @@ def cpu_baseline(arena, s, seconds: float):
         out[nt] = (n / el, n, el)
         log(f"cpu baseline {nt} threads: {n} tokens in {el:.2f}s -> {n / el:.1f} layer-tok/s")
     return out, threads, cores
+
+
+def config1(steps: int, stream, copies: int = 1024, cpu_seconds: float = 6.0, run_cpu: bool = True):
+    """Config 1: one Q4_K dequant-matvec, an expert gate projection (512 x
+    2048, 8 superblocks a row; fp32 x ~ N(0,1) and y) through
+    bread_matvec_f32.  Cold: launch i reads weight copy i % copies, each copy
+    its own seeded bytes (1024 x 590 KB = 604 MB, beyond the 256 MB Infinity
+    Cache), back to back on one stream (expert_bench.cu:157-180 times its
+    block the same way, with events around a loop).  The CPU baseline is the
+    oracle's matvec (the dequant_q4k_cpu.c block dequant and a sequential
+    fp32 row sum, layer_ops.cu:133-149) on copy 0, one thread and all host
+    threads over rows."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from breadv2_amd import api
+    from breadv2_amd._lib import lib
+
+    R, C = CFG1_ROWS, CFG1_COLS
+    rb = C // 256 * 144
+    w = torch.empty(copies * R * rb, dtype=torch.uint8, device="cuda:0")
+    api.synth_q4k(w, copies * R * C // 256, 4242)
+    x = torch.randn(C, device="cuda:0", generator=torch.Generator("cuda:0").manual_seed(11))
+    y = torch.empty(R, device="cuda:0")
+    base, xp, yp = w.data_ptr(), ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr())
+    ptrs = [ctypes.c_void_p(base + i * R * rb) for i in range(copies)]
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    fn = lib.bread_matvec_f32
+
+    def launch(i):
+        rc = fn(ptrs[i % copies], xp, yp, R, C, api.QTYPE_Q4_K, sp)
+        if rc:
+            raise RuntimeError(f"bread_matvec_f32 failed: {rc}")
+
+    with torch.cuda.stream(stream):
+        for i in range(copies):
+            launch(i)
+        torch.cuda.synchronize()
+        for i in range(PREROLL):
+            launch(i)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
+            launch(PREROLL + i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    gbs = CFG1_BYTES / us / 1e3
+    out = {
+        "workload": "config1: one Q4_K dequant-matvec 512 x 2048 (expert gate projection), fp32 x/y, cold "
+                    f"(cycled over {copies} distinct weight copies, {copies * R * rb / 1e6:.0f} MB)",
+        "entry": "bread_matvec_f32", "kernel": "k_matvec<Q4_K, float, float>",
+        "launches": steps, "us_per_matvec": round(us, 3), "matvec_per_s": round(1e6 / us, 1),
+        "algorithmic_bytes": CFG1_BYTES, "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+        "bound_note": "one launch moves 590 KB: a single HBM round trip of latency plus the dispatch gap, "
+                      "so it is latency-bound, far from the bandwidth roofline",
+        "cpu": None,
+    }
+    log(f"config1: {us:.2f} us per matvec, {gbs:.0f} GB/s")
+    if run_cpu:
+        from oracle import oracle as O
+        wh = w[: R * rb].cpu().numpy()
+        xh = x.cpu().numpy()
+        cores = O.affinity_cores()
+        omp = os.environ.get("OMP_NUM_THREADS")
+        threads = min(cores, int(omp)) if omp and omp.isdigit() else cores
+        cpu = {}
+        for nt in sorted({1, threads}):
+            O.matvec(wh, O.QTYPE_Q4_K, xh, R, C, nthreads=nt)
+            n, t0 = 0, time.perf_counter()
+            while True:
+                O.matvec(wh, O.QTYPE_Q4_K, xh, R, C, nthreads=nt)
+                n += 1
+                el = time.perf_counter() - t0
+                if el >= cpu_seconds / 2 and n >= 10:
+                    break
+            cpu[str(nt)] = {"us_per_matvec": round(el / n * 1e6, 2), "gbs": round(CFG1_BYTES * n / el / 1e9, 3),
+                            "matvecs": n, "seconds": round(el, 2)}
+            log(f"config1 cpu {nt} threads: {el / n * 1e6:.1f} us per matvec")
+        out["cpu"] = {"kind": "port", "threads": cpu, "host_cores": cores,
+                      "sample": "oracle_matvec on copy 0 (block dequant + sequential fp32 row sums), "
+                                "1 thread and all threads over rows"}
+    del w
+    return out
 
 
 MT_CASES = [("config4: batched decode / verify, B=8, Zipf(1.1) routing", 8, True),
@@ -267,6 +357,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mt-steps", type=int, default=40,
                     help="configs 4/5: timed grouped-path layers per case (0 skips them)")
+    ap.add_argument("--cfg1-steps", type=int, default=4000,
+                    help="config 1: timed cold 512 x 2048 Q4_K matvec launches (0 skips it)")
     ap.add_argument("--only-mt", action="store_true",
                     help="profiling aid: run only the configs 4/5 cases and print their JSON")
     ap.add_argument("--only-verify", action="store_true",
@@ -309,9 +401,10 @@ def main() -> int:
         return 0
     h = torch.randn(1, s.hidden, device="cuda:0", generator=torch.Generator("cuda:0").manual_seed(1))
 
-    def step(i):
-        # one MoE layer of one decode token: x = RMSNorm(h); h += MoE_l(x), one launch
-        ctx.decode_layers([descs[i % L]], h, stream=stream)
+    # one MoE layer of one decode token: x = RMSNorm(h); h += MoE_l(x), one
+    # launch; the ctypes arguments are built once, so the host enqueues a step
+    # in a few microseconds, well inside the kernel's own time
+    step = ctx.decode_launcher(descs, h, stream=stream)
 
     with torch.cuda.stream(stream):
         for i in range(args.warmup):
@@ -323,6 +416,11 @@ def main() -> int:
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
+        # untimed launches queued ahead of the start event keep the GPU busy
+        # while the timed ones are enqueued, so the region holds kernel time
+        # and the dispatch gaps only, for any --steps
+        for i in range(PREROLL):
+            step(args.warmup + i)
         e0.record(stream)
         for i in range(args.steps):
             step(i)
@@ -387,7 +485,8 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f32 (fp32 router, softmax, SwiGLU, down and combine; gate/up dots on 16-bit block "
+                 "fixed-point activations with exact integer sums)",
         "data": "synthetic (seeded Q4_K/Q6_K experts, fp32 router ~N(0,0.02), x = RMSNorm(h))",
         "config": {
             "workload": "config2: one MoE layer, decode batch 1, Qwen3.5-35B-A3B shape "
@@ -440,6 +539,8 @@ def main() -> int:
                           "executed MFMA work is higher (32-pair tiles padded, activations as hi+lo fp16)",
             "cases": multi_token(arena, s, args.mt_steps, stream),
         }
+    if args.cfg1_steps > 0:
+        result["config1"] = config1(args.cfg1_steps, stream, run_cpu=not args.no_cpu)
     if args.mt_steps > 0:
         result["lm_head"] = {"entry": "bread_matvec (fp16 x/y)", "cases": lm_head(20)}
     if args.mt_steps > 0 and L >= 40:

@@ -124,6 +124,10 @@ SIGNATURES = {
         c_int,
         [c_void_p, POINTER(MoeLayer), c_void_p, POINTER(c_int32), POINTER(c_float), POINTER(c_float), c_void_p],
     ),
+    "bread_route_layer_f16": (
+        c_int,
+        [c_void_p, POINTER(MoeLayer), c_void_p, POINTER(c_int32), POINTER(c_float), POINTER(c_float), c_void_p],
+    ),
     "bread_moe_forward": (
         c_int,
         [c_void_p, POINTER(MoeLayer), c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p],

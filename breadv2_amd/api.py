@@ -377,6 +377,19 @@ class MoeContext:
               "bread_route_layer")
         return list(idx), list(w), g.value
 
+    def route_layer_f16(self, layer: MoeLayer, normed16: torch.Tensor, stream=None):
+        """route_layer on the reference's own input (one_layer.cu:937-939):
+        fp16 d_normed2 [H], widened on the device; host lists and the raw
+        shared-gate logit."""
+        assert normed16.dtype == torch.float16 and normed16.is_contiguous()
+        K = self.shape.top_k
+        idx = (ctypes.c_int32 * K)()
+        w = (ctypes.c_float * K)()
+        g = ctypes.c_float()
+        check(lib.bread_route_layer_f16(self._h, ctypes.byref(layer), _p(normed16), idx, w, ctypes.byref(g),
+                                        _s(stream)), "bread_route_layer_f16")
+        return list(idx), list(w), g.value
+
     def forward(self, layer: MoeLayer, x: torch.Tensor, hidden: torch.Tensor, n_tokens: int,
                 want_routing: bool = False, stream=None):
         K = self.shape.top_k
@@ -421,6 +434,22 @@ class MoeContext:
         check(lib.bread_moe_decode_layers(self._h, arr, n, _p(hidden), _p(idx), _p(w), _p(gsh), _s(stream)),
               "bread_moe_decode_layers")
         return idx, w, gsh
+
+    def decode_launcher(self, layers, hidden: torch.Tensor, stream=None):
+        """A callable f(i) that runs bread_moe_decode_layers on the single
+        layer layers[i % len(layers)] with every ctypes argument built once:
+        a launch costs one foreign call (for loops that time the kernel)."""
+        arrs = [(MoeLayer * 1)(l) for l in layers]
+        n = len(arrs)
+        fn = lib.bread_moe_decode_layers
+        h, hp, sp = self._h, _p(hidden), _s(stream)
+
+        def launch(i: int) -> None:
+            rc = fn(h, arrs[i % n], 1, hp, None, None, None, sp)
+            if rc:
+                check(rc, "bread_moe_decode_layers")
+
+        return launch
 
     def stack_forward(self, layers, hidden: torch.Tensor, n_tokens: int, want_routing: bool = False, stream=None):
         """bread_moe_stack_forward: n_tokens tokens through len(layers) MoE

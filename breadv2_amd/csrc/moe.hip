@@ -405,6 +405,18 @@ __global__ __launch_bounds__(256) void k_f16_in(const uint16_t *__restrict__ hid
     }
 }
 
+// fp16 bits -> fp32, 8 values a thread (exact): route_layer's widening of
+// d_normed2 (vram_half_to_cpu_float, one_layer.cu:961) on the device.
+__global__ __launch_bounds__(256) void k_widen_f16(const uint16_t *__restrict__ in, float *__restrict__ out,
+                                                   size_t n8)
+{
+    const size_t v = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (v >= n8) return;
+    const uint4 q = reinterpret_cast<const uint4 *>(in)[v];
+    reinterpret_cast<float4 *>(out)[2 * v] = make_float4(h2f(q.x), h2f(q.x >> 16), h2f(q.y), h2f(q.y >> 16));
+    reinterpret_cast<float4 *>(out)[2 * v + 1] = make_float4(h2f(q.z), h2f(q.z >> 16), h2f(q.w), h2f(q.w >> 16));
+}
+
 // ... and out: hidden = fp16(h32), round to nearest even, 8 values a thread.
 __global__ __launch_bounds__(256) void k_f16_out(const float *__restrict__ h32, uint16_t *__restrict__ hidden,
                                                  size_t n8)
@@ -504,6 +516,24 @@ extern "C" int bread_route_layer(bread_moe_ctx_t *c, const bread_moe_layer_t *L,
     BREAD_HIP(hipMemcpyAsync(gsh_logit, c->gsh, sizeof(float), hipMemcpyDeviceToHost, st));
     BREAD_HIP(hipStreamSynchronize(st));
     return BREAD_OK;
+}
+
+extern "C" int bread_route_layer_f16(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const uint16_t *normed,
+                                     int *expert_indices, float *expert_weights, float *gsh_logit,
+                                     bread_stream_t stream)
+{
+    BREAD_REQUIRE(c && normed, BREAD_ERR_ARG, "NULL context or d_normed2");
+    BREAD_REQUIRE(expert_indices && expert_weights && gsh_logit, BREAD_ERR_ARG, "NULL host output");
+    BREAD_REQUIRE(((uintptr_t)normed & 15) == 0, BREAD_ERR_ALIGN, "d_normed2 must be 16-byte aligned");
+    int rc = bread_validate_layer(&c->shape, L);
+    if (rc) return rc;
+    // x32 holds max_tokens >= 1 rows of H floats; H is a multiple of 256
+    const size_t n8 = (size_t)c->shape.hidden / 8;
+    bread_clear_stale_error();
+    hipLaunchKernelGGL(k_widen_f16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, to_hip(stream), normed,
+                       c->x32, n8);
+    BREAD_HIP(hipGetLastError());
+    return bread_route_layer(c, L, c->x32, expert_indices, expert_weights, gsh_logit, stream);
 }
 
 // Up to this many tokens one decode-stack launch per token (509 us per

@@ -198,6 +198,19 @@ int bread_route_layer(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer, cons
                       int *expert_indices, float *expert_weights, float *gsh_logit,
                       bread_stream_t stream);
 
+/* route_layer with the reference's own input: d_normed2, the fp16
+ * post-attention RMSNorm output of one token (fp16 bits [H], device,
+ * 16-byte aligned), widened to fp32 on the device exactly as route_layer
+ * widens it on the host (vram_half_to_cpu_float, one_layer.cu:961), then
+ * routed as bread_route_layer.  Replaces `float route_layer(loader_t *L,
+ * gguf_ctx_t *g, int layer_idx, const half *d_normed2, int *expert_indices,
+ * float *expert_weights)` (one_layer.cu:937-939), whose callers are
+ * one_layer.cu:1853 and :1998; the raw shared-gate logit that route_layer
+ * returns lands in *gsh_logit. */
+int bread_route_layer_f16(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer, const uint16_t *d_normed2,
+                          int *expert_indices, float *expert_weights, float *gsh_logit,
+                          bread_stream_t stream);
+
 /* The MoE FFN for n_tokens tokens, accumulated into the residual:
  *   hidden[t] += sigmoid(gsh_t) * shared(x_t) + sum_k w_tk * expert_{idx_tk}(x_t)
  * with expert(x) = down(silu(gate x) * (up x)), summed per element in the

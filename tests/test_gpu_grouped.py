@@ -119,10 +119,22 @@ def test_grouped_all_tokens_same_experts(full_layer):
     check(hl, x, hidden, got)
 
 
-def test_grouped_two_tokens_auto_path(full_layer):
-    """n_tokens = 2 takes the grouped path under PATH_AUTO."""
+def test_grouped_two_tokens_forced(full_layer):
+    """n_tokens = 2 on the grouped path, forced (AUTO takes the small-batch
+    path up to bread_small_auto_tokens() tokens)."""
     s, t, hl = full_layer
     x = tokens(2, s.hidden, 12, zipf=False)
+    hidden = np.zeros_like(x)
+    check(hl, x, hidden, run(s, t, x, hidden, path=api.PATH_GROUPED))
+
+
+@pytest.mark.parametrize("T", [17, 18])
+def test_auto_hands_off_to_grouped(full_layer, T):
+    """Just above bread_small_auto_tokens() tokens PATH_AUTO takes the grouped
+    path; the result still meets the oracle."""
+    s, t, hl = full_layer
+    assert T > B.lib.bread_small_auto_tokens()
+    x = tokens(T, s.hidden, 40 + T, zipf=False)
     hidden = np.zeros_like(x)
     check(hl, x, hidden, run(s, t, x, hidden, path=api.PATH_AUTO))
 

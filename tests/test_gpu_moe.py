@@ -139,6 +139,31 @@ def test_route_layer_shim(full_layer):
     np.testing.assert_allclose(hg, rg, rtol=1e-4, atol=1e-5)
 
 
+@pytest.mark.parametrize("seed", [5, 6, 7])
+def test_route_layer_f16_shim(full_layer, seed):
+    """The reference's route_layer input is fp16 d_normed2 (one_layer.cu:937-961):
+    the shim widens it on the device; routing must equal the oracle's on the
+    widened (exact) fp32 values, and the raw shared-gate logit is returned."""
+    s, t, hl = full_layer
+    x16 = xs(1, s.hidden, seed)[0].astype(np.float16)
+    ctx = B.MoeContext(s, max_tokens=1)
+    hi, hw, hg = ctx.route_layer_f16(t.desc(), torch.from_numpy(x16).to(DEV))
+    ri, rw, rg = O.route(hl, x16.astype(np.float32))
+    assert hi == list(ri)
+    np.testing.assert_allclose(hw, rw, rtol=2e-5)
+    np.testing.assert_allclose(hg, rg, rtol=1e-4, atol=1e-5)
+    assert ctx.check_device() == 0
+
+
+def test_route_layer_f16_rejects_misaligned(full_layer):
+    s, t, _ = full_layer
+    ctx = B.MoeContext(s, max_tokens=1)
+    buf = torch.zeros(s.hidden + 8, dtype=torch.float16, device=DEV)
+    with pytest.raises(B.BreadError) as e:
+        ctx.route_layer_f16(t.desc(), buf[1:s.hidden + 1])
+    assert e.value.status == api._lib.ERR_ALIGN
+
+
 # ------------------------------------------------------------------ MoE layer
 
 
@@ -206,7 +231,8 @@ def test_decode_vs_multi_kernel_path(full_layer):
 @pytest.mark.parametrize("path", [api.PATH_AUTO, api.PATH_PER_TOKEN])
 @pytest.mark.parametrize("T", [2, 8, 16])
 def test_multi_token_matches_oracle(full_layer, T, path):
-    """AUTO runs the grouped path at these sizes; PER_TOKEN the GEMV kernels."""
+    """AUTO runs the small-batch path at these sizes (up to
+    bread_small_auto_tokens() = 16 tokens); PER_TOKEN the GEMV kernels."""
     s, t, hl = full_layer
     ctx = B.MoeContext(s, max_tokens=T)
     ctx.set_path(path)
