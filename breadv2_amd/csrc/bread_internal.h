@@ -123,6 +123,11 @@ int bread_launch_route(bread_moe_ctx_t *ctx, const bread_moe_layer_t *L, const f
 int bread_launch_moe_multi(bread_moe_ctx_t *ctx, const bread_moe_layer_t *L, const float *x,
                            float *hidden, int n_tokens, hipStream_t st);
 int bread_launch_topk(const float *logits, int E, int K, int T, int32_t *idx, float *w, hipStream_t st);
+// Router logits in the reference's sequential order (route.hip): logits
+// [T][E]; with shg_row also the shared-gate score of every token into gsh.
+int bread_route_rows_per_wave(int T, int E);
+int bread_launch_route_logits(const float *router, const uint16_t *shg, const float *x, float *logits, float *gsh,
+                              int H, int E, int T, bool shg_row, hipStream_t st);
 int bread_grouped_alloc(bread_moe_ctx_t *ctx);
 void bread_grouped_free(bread_moe_ctx_t *ctx);
 bool bread_grouped_supported(const bread_moe_shape_t &s, const bread_moe_layer_t *L);

@@ -3,7 +3,7 @@
 //
 // Multi-token path (any n_tokens, and the fallback for shapes the
 // single-launch decode kernel is not built for): four stream-ordered kernels
-//   router logits  -> softmax/top-k (one wave per token)
+//   router logits  -> softmax/top-k (one wave per token; route.hip, exact)
 //   -> gate/up + SwiGLU (one wave per (token, slot, row))
 //   -> down + combine (one wave per (token, row), slots in reference order).
 // Slot 0 is the shared expert, slots 1..K the routed experts by rank.
@@ -220,41 +220,8 @@ extern "C" int bread_moe_ctx_set_trace(bread_moe_ctx_t *c, uint64_t *d_buf, size
 }
 
 // ---------------------------------------------------------------------------
-// Routing kernels
+// Per-token expert kernels (routing: route.hip)
 // ---------------------------------------------------------------------------
-
-// One wave per router row (rows E.. hold the shared-gate dot); every token.
-__global__ __launch_bounds__(256) void k_router(const float *__restrict__ router, const uint16_t *__restrict__ shg,
-                                                const float *__restrict__ x, float *__restrict__ logits,
-                                                float *__restrict__ gsh, int H, int E, int T)
-{
-    const int v = (int)((blockIdx.x * blockDim.x + threadIdx.x) / WAVE);
-    if (v > E) return;
-    for (int t = 0; t < T; t++) {
-        const float *xt = x + (size_t)t * H;
-        if (v < E) {
-            const float s = router_row_dot(router + (size_t)v * H, xt, H);
-            if (lane_id() == 0) logits[(size_t)t * E + v] = s;
-        } else {
-            const float s = shg ? shgate_dot(shg, xt, H) : 0.f;
-            if (lane_id() == 0) gsh[t] = s;
-        }
-    }
-}
-
-template <int MAXV>
-__global__ __launch_bounds__(64) void k_topk(const float *__restrict__ logits, int E, int K,
-                                             int32_t *__restrict__ idx, float *__restrict__ w)
-{
-    const int t = blockIdx.x;
-    int ik;
-    float wk;
-    topk_wave<MAXV>(logits + (size_t)t * E, E, K, ik, wk);
-    if (lane_id() < K) {
-        idx[(size_t)t * K + lane_id()] = ik;
-        w[(size_t)t * K + lane_id()] = wk;
-    }
-}
 
 // One wave per (token, slot, row): gate and up rows, then SwiGLU.
 __global__ __launch_bounds__(256) void k_gateup(bread_moe_layer_t L, const float *__restrict__ x,
@@ -436,29 +403,6 @@ __global__ __launch_bounds__(256) void k_f16_out(const float *__restrict__ h32, 
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
-
-int bread_launch_topk(const float *logits, int E, int K, int T, int32_t *idx, float *w, hipStream_t st)
-{
-    const int mv = (E + WAVE - 1) / WAVE;
-    if (mv <= 4)
-        hipLaunchKernelGGL(k_topk<4>, dim3(T), dim3(64), 0, st, logits, E, K, idx, w);
-    else
-        hipLaunchKernelGGL(k_topk<16>, dim3(T), dim3(64), 0, st, logits, E, K, idx, w);
-    BREAD_HIP(hipGetLastError());
-    return BREAD_OK;
-}
-
-int bread_launch_route(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, int T, int32_t *idx,
-                       float *w, float *gsh, hipStream_t st)
-{
-    const bread_moe_shape_t &s = c->shape;
-    const int waves = s.n_experts + 1;
-    bread_clear_stale_error();
-    hipLaunchKernelGGL(k_router, dim3((waves + 3) / 4), dim3(256), 0, st, L->router, L->shexp_gate, x, c->logits,
-                       gsh, s.hidden, s.n_experts, T);
-    BREAD_HIP(hipGetLastError());
-    return bread_launch_topk(c->logits, s.n_experts, s.top_k, T, idx, w, st);
-}
 
 int bread_launch_moe_multi(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, float *hidden, int T,
                            hipStream_t st)

@@ -99,6 +99,8 @@ constexpr int N_XQ = 8;
 constexpr int W_PF = 12;                 // waves 12..15 prefetch routing-independent weights, never poll
 constexpr int N_XPOLL = 8;               // waves 0..7 poll the previous layer's output (4 columns a thread) and take the router partials
 constexpr int N_HPOLL = W_PF;            // waves 0..11 poll the SwiGLU outputs
+constexpr int W_RAD = 4;                 // wave 4 publishes the logit's radius
+constexpr int W_CERT = NWV - 1;          // wave 15 certifies the routing (a down wave, idle until the ranks are in)
 constexpr uint32_t SPIN_LIMIT = 1u << 18;
 constexpr uint32_t BUF_WORD3 = 0x00020000u;  // raw buffer descriptor word 3 (gfx9)
 constexpr int AUX_COHERENT = 16;             // sc1: device-coherent access
@@ -133,7 +135,13 @@ enum {
     TP_OUT = 9,     // output rows stored
     TP_HLAST = 10,  // the last routed slot's gate/up wave stored its h
     TP_DNIN = 11,   // every routed down band in LDS (seen by wave 0)
-    TP_N = 12
+    TP_PASSES = 12, // last selection pass done
+    TP_CERT = 13,   // ranks final (certified, or recomputed)
+    TP_XDOT = 14,   // uncertified: own logit in the reference's order done
+    TP_XPOLL = 15,  // uncertified: every such logit seen
+    TP_PREP = 16,   // certificate wave: radii and maxima settled
+    TP_READY = 17,  // certificate wave: every pass seen
+    TP_N = 18
 };
 
 struct DecLayer {
@@ -154,7 +162,9 @@ struct DecArgs {
     const float *x0;         // non-NULL: layer 0 input given (already normalised)
     float *hidden;           // [H] caller's hidden: input of layer 0, output of every layer
     float eps;
-    uint64_t *tlogits;       // [256][LG_STRIDE] epoch-tagged logits
+    uint64_t *tlogits;       // [256][LG_STRIDE] tagged logits
+    uint64_t *texact;        // [256][LG_STRIDE] tagged exact logits (uncertified layers)
+    uint64_t *tradius;       // [256][LG_STRIDE] tagged radii of the logits
     float *xbuf;             // [2][G][XREC] layer outputs by parity: rows 8g..8g+7 of workgroup g
     float *hbuf;             // [3][G][XREC] SwiGLU outputs by layer mod 3: [slot][rows 2g, 2g+1]
     int32_t *idx_out;        // [L][rstride][K] or NULL (this token's record of each layer)
@@ -180,22 +190,29 @@ struct Smem {
     uint16_t shg[DH];                  // shared-expert gate vector (prefetched)
     uint4 shw[2][4][WAVE];             // shared gate/up rows: [row][hg, qg, hu, qu][lane] (prefetched)
     uint4 gu[MAXK][4 * GR][WAVE];      // routed gate/up rows: [slot-1][4 row + (hg, qg, hu, qu)][lane]
-    float lg[256];                     // router logits of the layer
+    __attribute__((aligned(16))) float lg[256];  // router logits of the layer (scratch of the exact softmax)
     float red[NWV];                    // sum-of-squares partials
     float rl[N_XPOLL], gl[N_XPOLL];    // router / shared-gate partials of the polling waves
+    float rbw[N_XPOLL];                // their radius terms
+    float lr[256];                     // radii of the logits: |logit - reference sum| <= lr
+    float2 smax;                       // the max and sum of the selection softmax
+    float own_lg;                      // this workgroup's logit, as published
     float dot[NSLOT][OR];              // down dots
     float hown[OR];                    // this workgroup's rows of h before the layer
     int idx[MAXK];                     // routed experts, rank order
     uint32_t key[MAXK];                // their probability keys
     float w[MAXK];                     // their weights
     float sgsh;                        // sigmoid of the shared-gate logit
+    float gsh;                         // the shared-gate logit
     int nready;                        // ranks published in idx
     int lgcnt;                         // polling waves done with the logits
     int rlcnt;                         // x-polling waves whose router partials are in S.rl
+    int rbcnt;                         // x-polling waves whose radius terms are in S.rbw
     int dncnt;                         // down waves whose bands are in LDS
     int gucnt;                         // routed gate/up waves whose weights are in LDS
     int xqcnt;                         // waves done converting their part of x (quant_x)
     int gudone;                        // routed gate/up waves done computing
+    int cert;                          // 0: ranks may still change; 1: certified; 2: recomputed exactly
     int abort;                         // a wait failed: the workgroup leaves
 };
 // more than half of a CU's 160 KB, so the dispatcher puts one workgroup per CU
@@ -287,6 +304,12 @@ __device__ __forceinline__ void trace_point(const DecArgs &a, int l, int tp)
     if (threadIdx.x == 0) trace_here(a, l, tp);
 }
 
+// The same, from the calling wave's lane 0.
+__device__ __forceinline__ void trace_point_lane0(const DecArgs &a, int l, int tp)
+{
+    if (lane_id() == 0) trace_here(a, l, tp);
+}
+
 // The layer record is the same for the whole grid: keep it in scalar registers.
 __device__ __forceinline__ DecLayer load_layer(const DecArgs &a, int l)
 {
@@ -352,20 +375,50 @@ __device__ __forceinline__ bool poll4(bread_decode_sync *s, __amdgpu_buffer_rsrc
     return false;
 }
 
-// Per-thread bounded poll of router logit i of this epoch (tagged word).
-__device__ __forceinline__ bool poll_logit(bread_decode_sync *s, const uint64_t *p, uint32_t tag, float &v)
+// Exchange words of the routing: the 32-bit layer tag (bits 63-32, from the
+// context's layer epoch) and an fp32 value (31-0), one word per workgroup in
+// its own 64-byte line.  Three kinds: the fast logit, its radius (stored a
+// little later, in a separate line, so that the logit's line is written
+// once) and the logit in the reference's order (only in layers whose
+// routing is not certified).  The logit and radius words are rewritten every
+// layer; an exact-logit word can be many layers old, which 32-bit tags tell
+// apart (the host clears the words before the count wraps).
+__device__ __forceinline__ uint64_t tag_word(uint32_t tag, float v)
+{
+    return ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ void publish(uint64_t *p, uint32_t tag, float v)
+{
+    __hip_atomic_store(p, tag_word(tag, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Per-thread bounded poll of one tagged word of this layer.
+__device__ __forceinline__ uint64_t load_word(const uint64_t *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Per-thread bounded poll of one tagged word of this layer, w its first read.
+__device__ __forceinline__ bool poll_word_from(bread_decode_sync *s, const uint64_t *p, uint32_t tag, float &v,
+                                               uint64_t w)
 {
     for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
-        const uint64_t w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if ((uint32_t)(w >> 32) == tag) {
             v = __builtin_bit_cast(float, (uint32_t)w);
             return true;
         }
         if ((it & 63) == 63 && has_error(s)) return false;
         __builtin_amdgcn_s_sleep(1);
+        w = load_word(p);
     }
     flag_error(s, 2u);
     return false;
+}
+
+__device__ __forceinline__ bool poll_word(bread_decode_sync *s, const uint64_t *p, uint32_t tag, float &v)
+{
+    return poll_word_from(s, p, tag, v, load_word(p));
 }
 
 // ---------------------------------------------------------------- routing
@@ -646,6 +699,386 @@ __device__ __forceinline__ void prefetch(Smem &S, const DecLayer &Ly, int g, int
     if (c < BAND16) lds_load16(Ly.down_sh + (size_t)g * BAND + 16 * c, &S.sdown[sb][4 * WAVE * w4]);
 }
 
+// ---------------------------------------------------------------- exact routing
+
+// w[k] = w[k] * x[k] (rounded) for the DH columns, by one wave; its later LDS
+// loads see the stores.
+__device__ __forceinline__ void products_in_place(float *w, const float *x, int lane)
+{
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int i = 0; i < DH / (4 * WAVE); i++) {
+        const int o = 4 * (WAVE * i + lane);
+        const float4 xv = *reinterpret_cast<const float4 *>(&x[o]);
+        const float4 wv = *reinterpret_cast<const float4 *>(&w[o]);
+        *reinterpret_cast<float4 *>(&w[o]) = make_float4(wv.x * xv.x, wv.y * xv.y, wv.z * xv.z, wv.w * xv.w);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_wave_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// The uncertified case, run by wave W_CERT of every workgroup (all make the
+// same decision from the same published data): the workgroup's own logit in the
+// reference's order, ((0 + w_0 x_0) + w_1 x_1) + ... (one_layer.cu:969-971;
+// every lane runs the same chain over the router row and x in LDS), exchanged
+// through the exact-logit words; then the host's softmax arithmetic
+// (softmax_keys_exact) and cpu_topk's passes on the exact logits: indices and
+// weights as the reference computes them.  Returns false if a wait failed.
+__device__ bool exact_routing(const DecArgs &a, const DecLayer &Ly, Smem &S, int g, int E, int K, uint32_t tag32,
+                              int lane, int l, bool reload)
+{
+    float acc = 0.f;
+    if (g < E) {
+        if (reload) {
+            // S.wrow held other rows (certify): this workgroup's again
+#pragma unroll
+            for (int i = 0; i < DH / (4 * WAVE); i++)
+                lds_load16(Ly.router + (size_t)g * DH + 4 * (WAVE * i + lane), &S.wrow[4 * WAVE * i]);
+            __builtin_amdgcn_s_waitcnt(0);
+        }
+        // the products w_k x_k in place, then their sequential sum
+        products_in_place(S.wrow, S.x, lane);
+        acc = seq_sum_lds(S.wrow, DH);
+        if (lane == 0) publish(a.texact + LG_STRIDE * g, tag32, acc);
+    }
+    trace_point_lane0(a, l, TP_XDOT);
+    float p[4];
+    bool ok = true;
+#pragma unroll
+    for (int vv = 0; vv < 4; vv++) {
+        const int e = lane + WAVE * vv;
+        p[vv] = -__builtin_inff();
+        if (e < E) {
+            if (e == g) {
+                p[vv] = acc;
+            } else {
+                float v = 0.f;
+                ok = poll_word(a.sync, a.texact + LG_STRIDE * e, tag32, v) && ok;
+                p[vv] = v;
+            }
+        }
+    }
+    if (__builtin_amdgcn_ballot_w64(!ok)) return false;
+    trace_point_lane0(a, l, TP_XPOLL);
+    uint32_t key[4];
+    softmax_keys_exact<4>(p, E, key, S.lg);
+    for (int k = 0; k < K; k++) {
+        uint32_t M;
+        const int win = select_round<4>(key, M);
+        if (lane == 0) {
+            S.idx[k] = win < E ? win : 0;
+            S.key[k] = M;
+        }
+    }
+    return true;
+}
+
+// ---------------------------------------------------------------- certificate
+
+// DPP move with `old` in the lanes that have no source.
+template <int CTRL>
+__device__ __forceinline__ float dpp_or(float old, float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v),
+                                                                 CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float lane_f(float v, int i)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), i));
+}
+
+// Wave W_CERT, once every logit is polled: every logit's radius read (four
+// words a lane, in flight together) into S.lr, and the maxima over all
+// experts: x = max radius, y = max |logit|, z = 1 if every logit and radius
+// is finite and |logit| <= 64, w = 1 unless a wait failed.
+__device__ float4 cert_prepare(const DecArgs &a, Smem &S, int E, uint32_t tag32, float (&lv)[4])
+{
+    const int lane = opaque(lane_id());
+#pragma unroll
+    for (int vv = 0; vv < 4; vv++) lv[vv] = -__builtin_inff();
+    if (!lds_wait(S, &S.lgcnt, NPOLL)) return make_float4(0.f, 0.f, 0.f, 0.f);
+    uint64_t w[4];
+#pragma unroll
+    for (int vv = 0; vv < 4; vv++) {
+        const int e = lane + WAVE * vv;
+        w[vv] = e < E ? load_word(a.tradius + LG_STRIDE * e) : tag_word(tag32, 0.f);
+    }
+    bool ok = false;
+    for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
+        bool mine = true;
+#pragma unroll
+        for (int vv = 0; vv < 4; vv++) mine = mine && (uint32_t)(w[vv] >> 32) == tag32;
+        if (__builtin_amdgcn_ballot_w64(!mine) == 0) {
+            ok = true;
+            break;
+        }
+        if ((it & 63) == 63 && has_error(a.sync)) break;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int vv = 0; vv < 4; vv++) {
+            const int e = lane + WAVE * vv;
+            if ((uint32_t)(w[vv] >> 32) != tag32) w[vv] = load_word(a.tradius + LG_STRIDE * e);
+        }
+    }
+    if (!ok) {
+        if (!has_error(a.sync)) flag_error(a.sync, 2u);
+        return make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float rm = 0.f, am = 0.f;
+    bool fin = true;
+#pragma unroll
+    for (int vv = 0; vv < 4; vv++) {
+        const int e = lane + WAVE * vv;
+        if (e < E) {
+            const float re = __builtin_bit_cast(float, (uint32_t)w[vv]);
+            S.lr[e] = re;
+            const float le = S.lg[e];
+            lv[vv] = le;
+            fin = fin && __builtin_isfinite(le) && __builtin_isfinite(re);
+            rm = fmaxf(rm, re);
+            am = fmaxf(am, fabsf(le));
+        }
+    }
+    rm = wave_max(rm);
+    am = wave_max(am);
+    const bool sane = __builtin_amdgcn_ballot_w64(!fin) == 0 && am <= 64.f;
+    return make_float4(rm, am, sane ? 1.f : 0.f, 1.f);
+}
+
+// Wave W_CERT's one-radius certificate on wave 0's ranks as they arrive:
+// each new rank's logit against the previous rank's (gap > T = 2 R_max +
+// tau), and once rank K-1 is in, no expert outside the top K within T of it
+// (counted, from the logits cert_prepare left in registers: exactly K
+// logits >= l_{K-1} - T).  Strict gaps beyond every
+// rounding mean the reference's order is the same.  Returns 1 (certified),
+// 0 (not: the full certificate decides) or -1 (the workgroup aborts).
+__device__ int cert_fast(Smem &S, int E, int K, float4 cm, const float (&lv)[4])
+{
+    const int lane = opaque(lane_id());
+    const float T = 2.f * cm.x + 12.f * CERT_U * (1.f + cm.y + cm.x);
+    bool good = cm.z != 0.f;
+    int have = 0;
+    float prev = 0.f;
+    for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
+        const int n = lds_get(&S.nready);
+        if (n > have) {
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            for (int k = have; k < n; k++) {
+                const float lk = S.lg[S.idx[k < MAXK ? k : 0]];
+                if (k > 0 && !(prev - lk > T)) good = false;
+                prev = lk;
+            }
+            have = n;
+        }
+        if (have >= K) break;
+        if (lds_get(&S.abort)) return -1;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (have < K) return -1;
+    if (!good) return 0;
+    if (K >= E) return 1;
+    const float lo = prev - T;
+    int cnt = 0;
+#pragma unroll
+    for (int vv = 0; vv < 4; vv++) {
+        const int e = lane + WAVE * vv;
+        cnt += __builtin_popcountll(__builtin_amdgcn_ballot_w64(e < E && lv[vv] >= lo));
+    }
+    return cnt == K ? 1 : 0;
+}
+
+// Run by wave W_CERT once the K + 1 selection passes are published: the
+// fast logits order the top K + 1 as the reference's sums would (route_dev.h
+// gives each logit a radius around the reference's sequential sum).
+//   1. One radius for all: every consecutive gap of the top K + 1 exceeds
+//      2 R_max + tau (tau: the softmax rounding, so that strictly separated
+//      sums give strictly ordered probabilities).
+//   2. Each expert's own radius: with lo_k / hi_k = logit -/+ radius of rank
+//      k and M_k the largest hi of every expert ranked below k, ranks 0..k
+//      are certainly above the rest when min(lo_0..lo_k) > M_k + tau' (tau
+//      plus the rounding of lo and hi); certified when that holds for
+//      k = 0..K-1.
+//   3. If the only doubt is the order of two adjacent ranks j, j+1 (j + 1 <=
+//      K, separated from everything else), both logits are computed in the
+//      reference's order here (their router rows staged in S.wrow and S.nw,
+//      the products formed in place, then one lane's sequential sum each):
+//      equal logits tie (the lower index first, as cpu_topk's strict '>'
+//      takes it), logits more than tau apart order strictly.
+//   4. Otherwise exact_routing (every logit in the reference's order).
+// Returns 1 (certified), 2 (ranks settled anew) or 0 (a wait failed).
+// Wave W_CERT's wait for the K ranks, gathering each rank's expert and
+// logit into lane k as the ranks arrive (the LDS reads overlap the passes),
+// then rank K: the largest logit not selected, the lowest such index (its
+// probability key is the one the passes would give it: wk_key).  False if
+// the workgroup aborts.
+__device__ bool cert_gather(Smem &S, int E, int K, int &wk, float &lk, uint32_t &kK)
+{
+    const int lane = opaque(lane_id());
+    int have = 0;
+    wk = 0;
+    lk = 0.f;
+    bool ok = false;
+    for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
+        const int n = lds_get(&S.nready);
+        if (n > have) {
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            if (lane >= have && lane < n) {
+                wk = S.idx[lane < MAXK ? lane : 0];
+                lk = S.lg[wk];
+            }
+            have = n;
+        }
+        if (have >= K) {
+            ok = true;
+            break;
+        }
+        if (lds_get(&S.abort)) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (!ok) return false;
+    kK = 0u;
+    if (K >= E) return true;
+    int ws[MAXK];
+#pragma unroll
+    for (int i = 0; i < MAXK; i++) ws[i] = i < K ? __builtin_amdgcn_readlane(wk, i) : -1;
+    float bm = -__builtin_inff();
+    int bi = E;
+#pragma unroll
+    for (int vv = 0; vv < 4; vv++) {
+        const int e = lane + WAVE * vv;
+        bool sel = e >= E;
+#pragma unroll
+        for (int i = 0; i < MAXK; i++) sel = sel || ws[i] == e;
+        const float le = S.lg[e < E ? e : 0];
+        if (!sel && (le > bm || bi == E)) {
+            bm = le;
+            bi = e;
+        }
+    }
+    // NaN logits are left to the certificate's finiteness check
+    const float m = wave_max(bm);
+    const uint64_t at = __builtin_amdgcn_ballot_w64(bi < E && bm == m);
+    const int wl = at ? (int)__builtin_ctzll(at) : 0;
+    const int eK = __builtin_amdgcn_readlane(bi, wl);
+    const float2 ms = S.smax;
+    if (lane == K) {
+        wk = eK < E ? eK : 0;
+        lk = m;
+    }
+    kK = prob_key(expf(m - ms.x) / ms.y);
+    return true;
+}
+
+__device__ int certify(const DecArgs &a, const DecLayer &Ly, Smem &S, int g, int E, int K, uint32_t tag32, int l,
+                       float4 cm, int wk, float lk, uint32_t kK)
+{
+#pragma clang fp contract(off)
+    const int lane = opaque(lane_id());  // not hoisted out of the layer loop
+    const int np = K < E ? K + 1 : K;
+    const float rm = cm.x, am = cm.y;
+    const bool sane = cm.z != 0.f;
+    const float tau = 12.f * CERT_U * (1.f + am + rm);
+    // lane k < np holds rank k's expert and logit (cert_gather; rank K is
+    // the first expert not selected)
+    const bool rk = lane < np;
+    // 1: consecutive gaps against one radius (lane k: ranks k-1, k)
+    const float prev = dpp_or<0x111>(__builtin_inff(), lk);
+    const bool gk = lane == 0 || !rk || prev - lk > 2.f * rm + tau;
+    if (sane && __builtin_amdgcn_ballot_w64(!gk) == 0) return 1;
+    const float rr = rk ? S.lr[wk] : 0.f;
+    bool clobbered = false;
+    if (sane && np > K) {
+        // 2: per-expert radii.  um: the largest hi of the experts not selected
+        int ws[MAXK + 1];
+#pragma unroll
+        for (int i = 0; i < MAXK + 1; i++) ws[i] = i < np ? __builtin_amdgcn_readlane(wk, i) : -1;
+        float um = -__builtin_inff();
+#pragma unroll
+        for (int vv = 0; vv < 4; vv++) {
+            const int e = lane + WAVE * vv;
+            bool sel = e >= E;
+#pragma unroll
+            for (int i = 0; i < MAXK + 1; i++) sel = sel || ws[i] == e;
+            if (!sel) um = fmaxf(um, S.lg[e] + S.lr[e]);
+        }
+        um = wave_max(um);
+        const float tau2 = tau + 4.f * CERT_U * (rm + am);
+        const float inf = __builtin_inff();
+        // lane k: prefix min of lo over ranks 0..k, and the largest hi below
+        // rank k (ranks k+1.. of the selected, then um); ranks sit in lanes
+        // 0..np-1 of row 0, so row shifts suffice
+        float pm = rk ? lk - rr : inf;
+        pm = fminf(pm, dpp_or<0x111>(inf, pm));
+        pm = fminf(pm, dpp_or<0x112>(inf, pm));
+        pm = fminf(pm, dpp_or<0x114>(inf, pm));
+        pm = fminf(pm, dpp_or<0x118>(inf, pm));
+        float hx = dpp_or<0x101>(-inf, rk ? lk + rr : -inf);
+        hx = fmaxf(hx, dpp_or<0x101>(-inf, hx));
+        hx = fmaxf(hx, dpp_or<0x102>(-inf, hx));
+        hx = fmaxf(hx, dpp_or<0x104>(-inf, hx));
+        hx = fmaxf(hx, dpp_or<0x108>(-inf, hx));
+        const bool sepk = rk && pm > fmaxf(hx, um) + tau2;
+        const uint64_t sep = __builtin_amdgcn_ballot_w64(sepk);
+        const uint64_t doubt = ~sep & ((1ull << K) - 1ull);
+        if (doubt == 0) return 1;
+        const int j = (int)__builtin_ctzll(doubt);
+        if ((doubt & (doubt - 1)) == 0 && ((sep >> (j + 1)) & 1ull)) {
+            // 3: the two logits of ranks j, j+1 in the reference's order
+            const int ea = __builtin_amdgcn_readlane(wk, j);
+            const int eb = __builtin_amdgcn_readlane(wk, j + 1);
+            clobbered = true;
+#pragma unroll
+            for (int i = 0; i < DH / (4 * WAVE); i++) {
+                lds_load16(Ly.router + (size_t)ea * DH + 4 * (WAVE * i + lane), &S.wrow[4 * WAVE * i]);
+                lds_load16(Ly.router + (size_t)eb * DH + 4 * (WAVE * i + lane), &S.nw[4 * WAVE * i]);
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            products_in_place(S.wrow, S.x, lane);
+            products_in_place(S.nw, S.x, lane);
+            const float acc = seq_sum_lds(lane == 1 ? S.nw : S.wrow, DH);
+            const float la = lane_f(acc, 0), lb = lane_f(acc, 1);
+            trace_point_lane0(a, l, TP_XDOT);
+            if (__builtin_isfinite(la) && __builtin_isfinite(lb) && (la == lb || fabsf(la - lb) > tau)) {
+                const bool swap = la == lb ? eb < ea : lb > la;
+                if (swap && lane == 0) {
+                    const uint32_t kb = j + 1 < K ? S.key[j + 1] : kK;
+                    if (j + 1 < K) {
+                        S.idx[j + 1] = ea;
+                        S.key[j + 1] = S.key[j];
+                    }
+                    S.idx[j] = eb;
+                    S.key[j] = kb;
+                }
+                return 2;
+            }
+        }
+    }
+    // 4: every logit in the reference's order
+    return exact_routing(a, Ly, S, g, E, K, tag32, lane, l, clobbered) ? 2 : 0;
+}
+
+// ---------------------------------------------------------------- logit radius
+
+// The radius of a workgroup's fp32 logit around the reference's sequential
+// sum s_n (route_dev.h: |s_n - s*_n| <= u (S + c_H A) + 2n 2^-150, S the
+// sum of the |exact prefixes|).  Thread t of x-polling wave w holds columns
+// 256 w + 4 t .. +3, which start at the prefix W_w + o_t (wave offset +
+// in-wave exclusive prefix), so S <= sum_w 256 |W_w| + sum_t (4 |o_t| + 4 A_t)
+// with A_t = sum |w_k x_k| of the thread.  The logit itself carries at most
+// 17 u A of rounding (4 in a thread's fma chain, 6 in the wave tree, 7 across
+// the waves), which the radius absorbs: per unit of A, 4 + c_H + 17 with 2 to
+// spare for the fp32 rounding of the prefixes used here.  wave_terms gives
+// wave w's sum of the thread terms; the workgroup's radius adds
+// u (sum_w 256 |W_w| + |logit|) to their sum, times (1 + 2^-9) for the fp32
+// rounding of these sums, plus 1e-37 for underflow.
+__device__ __forceinline__ float wave_terms(float r, float ra)
+{
+    const float incl = wave_scan_incl_f32(r);
+    return wave_sum(4.f * fabsf(incl - r) + (23.f + cert_c_h(DH)) * ra);
+}
+
 // ---------------------------------------------------------------- kernel
 
 __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
@@ -670,7 +1103,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
         const int tid = opaque((int)threadIdx.x);
         const int lane = tid & (WAVE - 1);
         const DecLayer Ly = load_layer(a, l);
-        const uint32_t tag = a.epoch0 + (uint32_t)l + 1u;
+        const uint32_t tag32 = a.epoch0 + (uint32_t)l + 1u;
         const int par = (int)((a.epoch0 + (uint32_t)l) & 1u);
         float *xout = a.xbuf + par * (G * XREC);     // this layer's output rows
         const int hp = (a.hphase0 + l) % 3;
@@ -692,11 +1125,14 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                 S.gudone = 0;
                 S.lgcnt = 0;
                 S.rlcnt = 0;
+                S.rbcnt = 0;
                 S.dncnt = 0;
                 S.gucnt = 0;
+                S.cert = 0;
             }
         }
         float4 hv = make_float4(0.f, 0.f, 0.f, 0.f);
+        float r, ra;  // x-polling waves: the thread's router partial and its sum of |products|
         if (wid < N_XPOLL) {
             bool ok = true;
             const bool own = (tid >> 1) == g;  // threads 2g, 2g+1 hold rows 8g..8g+7
@@ -736,33 +1172,37 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             }
             *reinterpret_cast<float4 *>(&S.x[4 * tid]) = hv;
             // P2: router / shared-gate partials of the wave's 256 columns,
-            // from the registers that already hold them
-            float r = 0.f, q = 0.f;
+            // from the registers that already hold them.  Wave 0 publishes
+            // the logit as soon as the partials are in, without waiting for
+            // the other waves at the barrier below; its radius (from the
+            // wave terms of r and ra, wave_terms) follows in P3.
+            float q = 0.f;
+            r = 0.f;
+            ra = 0.f;
             if (g < E) {
                 const float4 wr = *reinterpret_cast<const float4 *>(&S.wrow[4 * tid]);
                 r = fmaf(wr.x, hv.x, fmaf(wr.y, hv.y, fmaf(wr.z, hv.z, wr.w * hv.w)));
+                ra = (fabsf(wr.x * hv.x) + fabsf(wr.y * hv.y)) + (fabsf(wr.z * hv.z) + fabsf(wr.w * hv.w));
             }
             if (Ly.shg) {
                 const uint2 hh = *reinterpret_cast<const uint2 *>(&S.shg[4 * tid]);
                 q = fmaf(h2f(hh.x), hv.x, fmaf(h2f(hh.x >> 16), hv.y, fmaf(h2f(hh.y), hv.z, h2f(hh.y >> 16) * hv.w)));
             }
-            r = wave_sum(r);
+            const float rt = wave_sum(r);
             q = wave_sum(q);
             if (lane == 0) {
-                S.rl[wid] = r;
+                S.rl[wid] = rt;
                 S.gl[wid] = q;
                 lds_add(&S.rlcnt, 1);
             }
-            // wave 0 publishes the logit as soon as the partials are in,
-            // without waiting for the other waves at the barrier below
             if (wid == 0 && lds_wait(S, &S.rlcnt, N_XPOLL)) {
                 float logit = 0.f;
 #pragma unroll
                 for (int w = 0; w < N_XPOLL; w++) logit += S.rl[w];
-                if (lane == 0 && g < E)
-                    __hip_atomic_store(a.tlogits + LG_STRIDE * g,
-                                       ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, logit),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (lane == 0) {
+                    S.own_lg = logit;
+                    if (g < E) publish(a.tlogits + LG_STRIDE * g, tag32, logit);
+                }
                 trace_point(a, l, TP_LOGIT);
             }
         }
@@ -770,63 +1210,80 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
         trace_point(a, l, TP_XREADY);
 
         // ---- P3: logits, routing, expert streams
-        if (wid < NPOLL) {
-            float logit = 0.f;
-#pragma unroll
-            for (int w = 0; w < N_XPOLL; w++) logit += S.rl[w];  // as published (own entry)
-            // poll one logit a lane
-            float v = -__builtin_inff();
-            bool ok = true;
-            if (tid < E) {
-                if (tid == g) v = logit;
-                else ok = poll_logit(sy, a.tlogits + LG_STRIDE * tid, tag, v);
+        if (wid < N_XPOLL) {
+            // the radius terms of the router partials; waves 0..3 while
+            // their first logit reads are in flight.  Wave W_RAD then
+            // publishes the radius.
+            const bool other = wid < NPOLL && tid < E && tid != g;
+            const uint64_t w0 = other ? load_word(a.tlogits + LG_STRIDE * tid) : 0;
+            const float rb = wave_terms(r, ra);
+            if (lane == 0) {
+                S.rbw[wid] = rb;
+                lds_add(&S.rbcnt, 1);
             }
-            S.lg[tid] = v;
-            if (!ok) lds_put(&S.abort, 1);
-            if (lane == 0) lds_add(&S.lgcnt, 1);
-            if (wid == 0) {
-                // the selection passes gate every expert stream: let this wave
-                // issue ahead of the other waves on its SIMD
-                __builtin_amdgcn_s_setprio(3);
-                if (lds_wait(S, &S.lgcnt, NPOLL)) {
-                    trace_point(a, l, TP_POLLED);
-                    float p[4];
+            if (wid == W_RAD && lds_wait(S, &S.rbcnt, N_XPOLL)) {
+                float pre = 0.f, scross = 0.f, bsum = 0.f;
 #pragma unroll
-                    for (int vv = 0; vv < 4; vv++) p[vv] = S.lg[lane + WAVE * vv];
-                    uint32_t key[4];
-                    softmax_keys<4>(p, E, key);
-                    Sel sel = sel_init(key);
-#pragma unroll
-                    for (int k = 0; k < MAXK; k++) {
-                        if (k >= K) break;
-                        uint32_t M;
-                        const int win = sel_pass(sel, lane, M);
-                        if (lane == 0) {
-                            S.idx[k] = win < E ? win : 0;
-                            S.key[k] = M;
-                            lds_put(&S.nready, k + 1);
-                        }
-                        if (k == 0) trace_point(a, l, TP_RANK1);
-                    }
-                    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-                    const int my_idx = lane < K ? S.idx[lane] : 0;
-                    const float wk = renorm_weight(lane < K ? S.key[lane] : 0u, K);
-                    float gsh = 0.f;
-#pragma unroll
-                    for (int w = 0; w < N_XPOLL; w++) gsh += S.gl[w];
-                    if (lane < K) S.w[lane] = wk;
-                    if (lane == 0) S.sgsh = sigmoidf_ref(gsh);
-                    if (g == 0) {
-                        const int rl = l * a.rstride;
-                        if (a.idx_out && lane < K) a.idx_out[rl * K + lane] = my_idx;
-                        if (a.w_out && lane < K) a.w_out[rl * K + lane] = wk;
-                        if (a.gsh_out && lane == 0) a.gsh_out[rl] = gsh;
-                    }
-                    trace_point(a, l, TP_ROUTED);
-                } else if (lane == 0) {
-                    lds_put(&S.abort, 1);
+                for (int w = 0; w < N_XPOLL; w++) {
+                    scross += 256.f * fabsf(pre);
+                    pre += S.rl[w];
+                    bsum += S.rbw[w];
                 }
-                __builtin_amdgcn_s_setprio(0);
+                const float radius = (1.0f + 1.0f / 512) * CERT_U * (scross + bsum + fabsf(S.own_lg)) + 1e-37f;
+                if (lane == 0 && g < E) publish(a.tradius + LG_STRIDE * g, tag32, radius);
+            }
+            if (wid < NPOLL) {
+                // poll one logit a lane
+                float v = -__builtin_inff();
+                bool ok = true;
+                if (tid == g) v = S.own_lg;
+                else if (other) ok = poll_word_from(sy, a.tlogits + LG_STRIDE * tid, tag32, v, w0);
+                S.lg[tid] = v;
+                if (!ok) lds_put(&S.abort, 1);
+                if (lane == 0) lds_add(&S.lgcnt, 1);
+                if (wid == 0) {
+                    // the selection passes gate every expert stream: let this wave
+                    // issue ahead of the other waves on its SIMD
+                    __builtin_amdgcn_s_setprio(3);
+                    if (lds_wait(S, &S.lgcnt, NPOLL)) {
+                        trace_point(a, l, TP_POLLED);
+                        float p[4];
+#pragma unroll
+                        for (int vv = 0; vv < 4; vv++) p[vv] = S.lg[lane + WAVE * vv];
+                        uint32_t key[4];
+                        const float2 ms = softmax_keys<4>(p, E, key);
+                        if (lane == 0) S.smax = ms;  // for the certificate's key of rank K
+                        Sel sel = sel_init(key);
+#pragma unroll
+                        for (int k = 0; k < MAXK; k++) {
+                            if (k >= K) break;
+                            uint32_t M;
+                            const int win = sel_pass(sel, lane, M);
+                            if (lane == 0) {
+                                S.idx[k] = win < E ? win : 0;
+                                S.key[k] = M;
+                                lds_put(&S.nready, k + 1);
+                            }
+                            if (k == 0) trace_point(a, l, TP_RANK1);
+                        }
+                        trace_point(a, l, TP_PASSES);
+                        // the weights from these ranks (P7 redoes them if the
+                        // certificate settled the ranks anew)
+                        const float wk = renorm_weight(lane < K ? S.key[lane] : 0u, K);
+                        float gsh = 0.f;
+#pragma unroll
+                        for (int w = 0; w < N_XPOLL; w++) gsh += S.gl[w];
+                        if (lane < K) S.w[lane] = wk;
+                        if (lane == 0) {
+                            S.sgsh = sigmoidf_ref(gsh);
+                            S.gsh = gsh;
+                        }
+                        trace_point(a, l, TP_ROUTED);
+                    } else if (lane == 0) {
+                        lds_put(&S.abort, 1);
+                    }
+                    __builtin_amdgcn_s_setprio(0);
+                }
             }
         }
         if (wid >= W_XQ && wid < W_XQ + N_XQ) {
@@ -836,22 +1293,30 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             if (lane == 0) lds_add(&S.xqcnt, 1);
         }
         if (wid >= W_GU && wid < W_GU + K) {
-            // routed gate/up of slot k = wave, as soon as rank k is known
+            // routed gate/up of slot k = wave, as soon as rank k is known; the
+            // result is published once the ranks are final (certified, or
+            // recomputed exactly, which may change this rank: then redone)
             const int slot = wid - W_GU + 1;
             if (lds_wait(S, &S.nready, slot)) {
-                const int e = S.idx[slot - 1];
-                gu_issue<GR>(Ly.gate_exps + (uint64_t)e * Ly.gate_eb, Ly.up_exps + (uint64_t)e * Ly.up_eb, GR * g,
-                             S.gu[slot - 1]);
-                __builtin_amdgcn_s_waitcnt(0);
-                if (lane == 0) lds_add(&S.gucnt, 1);
-                if (lds_wait(S, &S.xqcnt, N_XQ)) {
-                    float hv[GR];
+                int e = S.idx[slot - 1];
+                float hv[GR];
+                bool done = false;
+                for (int round = 0; round < 2 && !done; round++) {
+                    gu_issue<GR>(Ly.gate_exps + (uint64_t)e * Ly.gate_eb, Ly.up_exps + (uint64_t)e * Ly.up_eb, GR * g,
+                                 S.gu[slot - 1]);
+                    __builtin_amdgcn_s_waitcnt(0);
+                    if (round == 0 && lane == 0) lds_add(&S.gucnt, 1);
+                    if (!lds_wait(S, &S.xqcnt, N_XQ)) break;
                     gu_compute<GR>(S, S.gu[slot - 1], hv);
-                    if (lane == 0) {
-                        cstore2(hcur + XREC * g + GR * slot, hv[0], hv[1]);
-                        if (slot == K) trace_here(a, l, TP_HLAST);
-                        lds_add(&S.gudone, 1);
-                    }
+                    if (!lds_wait(S, &S.cert, 1)) break;
+                    const int ef = S.idx[slot - 1];
+                    done = ef == e;
+                    e = ef;
+                }
+                if (done && lane == 0) {
+                    cstore2(hcur + XREC * g + GR * slot, hv[0], hv[1]);
+                    if (slot == K) trace_here(a, l, TP_HLAST);
+                    lds_add(&S.gudone, 1);
                 }
             }
         }
@@ -870,20 +1335,43 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             const int c0 = WAVE * (wid - W_DN);
             const int ln = opaque(lane);
             // the down bands are not needed before the h exchange: their
-            // loads go out once every rank is known, behind the gate/up loads
-            bool ok = lds_wait(S, &S.nready, K);
-#pragma unroll
-            for (int i = 0; i < DN_LOADS; i++) {
-                const int cw = c0 + N_DN * WAVE * i;  // first chunk of this wave's load
-                if (!ok || cw >= nchunk) break;
-                const int ch = cw + ln;
-                if (ch < nchunk) {
-                    const int sl = ch / BAND16;  // slot - 1
-                    const uint8_t *base = Ly.down_exps + (uint64_t)S.idx[sl] * Ly.down_eb;
-                    lds_load16(base + (size_t)g * BAND + 16 * (ch - sl * BAND16), &S.down[4 * cw]);
+            // loads go out once every rank is known, behind the gate/up
+            // loads, and again if the exact recomputation replaced the ranks
+            // (wave W_CERT certifies the ranks first: its loads wait for it)
+            if (wid == W_CERT) {
+                // as urgent as wave 0's passes (another SIMD)
+                __builtin_amdgcn_s_setprio(3);
+                float lv[4];
+                const float4 cm = cert_prepare(a, S, E, tag32, lv);
+                trace_point_lane0(a, l, TP_PREP);
+                int st = cm.w != 0.f ? cert_fast(S, E, K, cm, lv) : -1;
+                trace_point_lane0(a, l, TP_READY);
+                if (st == 0) {
+                    int wk;
+                    float lk;
+                    uint32_t kK;
+                    st = cert_gather(S, E, K, wk, lk, kK) ? certify(a, Ly, S, g, E, K, tag32, l, cm, wk, lk, kK) : 0;
                 }
+                if (lane == 0) lds_put(st > 0 ? &S.cert : &S.abort, st > 0 ? st : 1);
+                __builtin_amdgcn_s_setprio(0);
+                trace_point_lane0(a, l, TP_CERT);
             }
-            __builtin_amdgcn_s_waitcnt(0);
+            bool ok = lds_wait(S, &S.nready, K);
+            for (int round = 0; round < 2 && ok; round++) {
+#pragma unroll
+                for (int i = 0; i < DN_LOADS; i++) {
+                    const int cw = c0 + N_DN * WAVE * i;  // first chunk of this wave's load
+                    if (cw >= nchunk) break;
+                    const int ch = cw + ln;
+                    if (ch < nchunk) {
+                        const int sl = ch / BAND16;  // slot - 1
+                        const uint8_t *base = Ly.down_exps + (uint64_t)S.idx[sl] * Ly.down_eb;
+                        lds_load16(base + (size_t)g * BAND + 16 * (ch - sl * BAND16), &S.down[4 * cw]);
+                    }
+                }
+                __builtin_amdgcn_s_waitcnt(0);
+                ok = lds_wait(S, &S.cert, 1) && lds_get(&S.cert) == 2 && round == 0;
+            }
             if (lane == 0) lds_add(&S.dncnt, 1);
             // the next layer's routing-independent weights, now that this
             // layer's are consumed (the shared gate/up was used before waves
@@ -976,6 +1464,22 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
         // (one_layer.cu:1443-1471) and publish the rows to the next layer and
         // the caller by wave 0
 
+        if (wid == 0) {
+            // the final ranks' weights, and the routing record
+            const bool anew = lds_get(&S.cert) == 2;
+            float wk = lane < K ? S.w[lane] : 0.f;
+            if (anew) {
+                wk = renorm_weight(lane < K ? S.key[lane] : 0u, K);
+                if (lane < K) S.w[lane] = wk;
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            }
+            if (g == 0) {
+                const int rl = l * a.rstride;
+                if (a.idx_out && lane < K) a.idx_out[rl * K + lane] = S.idx[lane];
+                if (a.w_out && lane < K) a.w_out[rl * K + lane] = wk;
+                if (a.gsh_out && lane == 0) a.gsh_out[rl] = S.gsh;
+            }
+        }
         if (wid == 0 && lane < OR) {
             float d[NSLOT], wt[MAXK];
 #pragma unroll
@@ -1018,6 +1522,12 @@ bool decode_shape_ok(const bread_moe_shape_t &s)
            s.n_experts >= s.top_k && s.top_k >= 1 && s.top_k <= MAXK;
 }
 
+__global__ void k_clear_words(uint64_t *p, int n)
+{
+    const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i < n) p[i] = 0;
+}
+
 bool layer_ok(const bread_moe_layer_t &L)
 {
     // buffer loads and 16-byte band loads assume these alignments
@@ -1041,14 +1551,26 @@ int launch(bread_moe_ctx_t *c, DecArgs &a, hipStream_t st)
     a.E = c->shape.n_experts;
     a.K = c->shape.top_k;
     a.tlogits = c->tlogits;
+    a.texact = c->tlogits + 256 * LG_STRIDE;
+    a.tradius = c->tlogits + 2 * 256 * LG_STRIDE;
     a.xbuf = c->xbuf;
     a.hbuf = c->hbuf;
     a.sync = c->dsync;
     a.trace = (c->trace && (size_t)G * a.L * TP_N <= c->trace_words) ? c->trace : nullptr;
     a.eps = c->shape.rms_eps;
+    bread_clear_stale_error();
+    if (c->epoch > UINT32_MAX - 1u - (uint32_t)a.L) {
+        // the layer tags would wrap past 2^32 in this launch: every tagged
+        // word back to tag 0 and the count restarted, so no word written
+        // before can carry a tag of a later layer (a fill kernel, not a
+        // memset, so that the launch can be captured in a graph)
+        const int n = (int)bread_decode_tlogit_words();
+        hipLaunchKernelGGL(k_clear_words, dim3((n + 255) / 256), dim3(256), 0, st, c->tlogits, n);
+        BREAD_HIP(hipGetLastError());
+        c->epoch = 0;
+    }
     a.epoch0 = c->epoch;
     a.hphase0 = c->hphase;
-    bread_clear_stale_error();
     hipLaunchKernelGGL(k_decode, dim3(G), dim3(NT), 0, st, a);
     BREAD_HIP(hipGetLastError());
     c->epoch += (uint32_t)a.L;
@@ -1145,7 +1667,7 @@ size_t bread_decode_xbuf_floats()
 
 size_t bread_decode_tlogit_words()
 {
-    return 256 * LG_STRIDE;
+    return 3 * 256 * LG_STRIDE;  // logits, exact logits, radii
 }
 
 size_t bread_decode_hbuf_floats()

@@ -30,13 +30,13 @@
 // activation fragment read from LDS serves 32 weight rows.
 //
 // Kernels per layer, stream-ordered:
-//   k_mt_xprep    one workgroup per token: row scale, hi/lo fp16 activations
-//                 in the gate/up operand order, shared-gate logit
-//   k_mt_router   router logits on fp32 MFMA (16 tokens x 16 experts per
-//                 workgroup, K over 16 waves; up to 128 tokens over 4
-//                 workgroups of 4 waves)
-//   k_topk        softmax / top-k / renormalisation (moe.hip, route_dev.h);
-//                 up to 128 tokens k_topk_sum, which first adds the 4 K ranges
+//   k_route_seq   router logits in the reference's sequential order
+//                 (route.hip: one lane a token, one or two router rows a wave)
+//   k_mt_topk_xprep  one workgroup per token: softmax / top-k /
+//                 renormalisation with the host's arithmetic (routing
+//                 bit-identical to the reference's), and the activation
+//                 preparation: row scale, hi/lo fp16 activations in the
+//                 gate/up operand order, shared-gate logit
 //   k_mt_bucket   one workgroup: expert histogram, token lists by expert,
 //                 M-tiles of 32 pairs
 //   k_mt_gateup   per (M-tile, 128 rows): gate and up GEMMs, SwiGLU
@@ -61,8 +61,6 @@ constexpr int GU_WAVES = 8;                      // one 32-row gate or up block 
 constexpr int GU_ROWS = GU_WAVES / 2 * 32;       // SwiGLU rows per gate/up workgroup
 constexpr int DN_WAVES = 8, DN_BLOCKS = 2;       // 32-row down blocks per wave
 constexpr int DN_ROWS = DN_WAVES * DN_BLOCKS * 32;  // output rows per down workgroup
-constexpr int RT_WAVES = 16;                     // router K split
-constexpr int RT_SPLIT = 4;                      // K ranges over workgroups for calls up to 128 tokens
 constexpr int MAX_INTER = 512;                   // largest intermediate size the LDS plan holds
 constexpr uint32_t MAGIC = 0x64646464u;          // fp16 0x64xx = 1024 + xx
 
@@ -297,7 +295,7 @@ __device__ __forceinline__ void mt_xprep(int t, const float *__restrict__ x, con
     const int e = row_exp(fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3])));
     if (threadIdx.x == 0) {
         xexp[t] = e;
-        gsh[t] = shg ? (sdot[0] + sdot[1]) + (sdot[2] + sdot[3]) : 0.f;
+        if (gsh) gsh[t] = shg ? (sdot[0] + sdot[1]) + (sdot[2] + sdot[3]) : 0.f;
     }
     const int nu = H / 8;
     for (int u = threadIdx.x; u < nu; u += 256) {
@@ -313,120 +311,29 @@ __device__ __forceinline__ void mt_xprep(int t, const float *__restrict__ x, con
     }
 }
 
-__global__ __launch_bounds__(256) void k_mt_xprep(const float *__restrict__ x, const uint16_t *__restrict__ shg,
-                                                  int H, uint4 *__restrict__ xhi, uint4 *__restrict__ xlo,
-                                                  int *__restrict__ xexp, float *__restrict__ gsh)
-{
-    mt_xprep((int)blockIdx.x, x, shg, H, xhi, xlo, xexp, gsh);
-}
-
-// Partial router logits part[z][t][e] = router row e . x[t] over K range z of
-// gridDim.z (one_layer.cu:964-971), fp32 products and sums.  A workgroup of
-// nw = RT_WAVES / gridDim.z waves takes one 16-token x 16-expert tile and one
-// K range; wave w covers K [(z nw + w) H/16, +H/16); lane (r, g) feeds token
-// t0 + r and expert e0 + r, 4 consecutive K each 16-element chunk; all of a
-// wave's loads are issued before its MFMAs.  The wave tiles are summed in
-// wave order; k_topk_sum adds the K ranges in order.  Splitting K over
-// workgroups puts a 64-token call on 256 workgroups instead of 64.
-__device__ __forceinline__ void mt_router(int bx, int by, int z, const float *__restrict__ router,
-                                          const float *__restrict__ x, float *__restrict__ part, int H, int E, int T)
-{
-    __shared__ f32x4 wpart[RT_WAVES][WAVE];
-    const int w = wave_id(), lane = lane_id();
-    const int nw = (int)(blockDim.x / WAVE);
-    const int r = lane & 15, g = lane >> 4;
-    const int t0 = bx * 16, e0 = by * 16;
-    const int kq = H / RT_WAVES, nch = kq / 16;
-    const int k0 = (z * nw + w) * kq;
-    const float *xr = x + (size_t)min(t0 + r, T - 1) * H + k0 + 4 * g;
-    const float *wr = router + (size_t)min(e0 + r, E - 1) * H + k0 + 4 * g;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int c0 = 0; c0 < nch; c0 += 8) {
-        float4 a[8], b[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++)
-            if (c0 + u < nch) {
-                a[u] = *reinterpret_cast<const float4 *>(xr + 16 * (c0 + u));
-                b[u] = *reinterpret_cast<const float4 *>(wr + 16 * (c0 + u));
-            }
-#pragma unroll
-        for (int u = 0; u < 8; u++)
-            if (c0 + u < nch) {
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].x, b[u].x, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].y, b[u].y, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].z, b[u].z, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].w, b[u].w, acc, 0, 0, 0);
-            }
-    }
-    wpart[w][lane] = acc;
-    __syncthreads();
-    if (w != 0) return;
-    f32x4 sum = wpart[0][lane];
-    for (int i = 1; i < nw; i++) sum += wpart[i][lane];
-    const int e = e0 + r;
-    float *out = part + (size_t)z * T * E;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int t = t0 + 4 * g + i;
-        if (t < T && e < E) out[(size_t)t * E + e] = sum[i];
-    }
-}
-
-__global__ __launch_bounds__(RT_WAVES * WAVE) void k_mt_router(const float *__restrict__ router,
-                                                               const float *__restrict__ x,
-                                                               float *__restrict__ part, int H, int E, int T)
-{
-    mt_router((int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, router, x, part, H, E, T);
-}
-
-// Small calls: the split router's tiles (RT_SPLIT workgroups of 4 waves each)
-// and the activation preparation in one launch: workgroups [0, nr) are
-// router (tile, K range) pairs, the next T prepare one token each.  Both only
-// read x.
-__global__ __launch_bounds__(RT_WAVES / RT_SPLIT * WAVE) void k_mt_route_prep(
-    const float *__restrict__ router, const float *__restrict__ x, float *__restrict__ part, int H, int E, int T,
-    const uint16_t *__restrict__ shg, uint4 *__restrict__ xhi, uint4 *__restrict__ xlo, int *__restrict__ xexp,
-    float *__restrict__ gsh)
-{
-    const int nbx = (T + 15) / 16, nby = (E + 15) / 16, nr = nbx * nby * RT_SPLIT;
-    const int b = (int)blockIdx.x;
-    if (b < nr) mt_router(b % nbx, (b / nbx) % nby, b / (nbx * nby), router, x, part, H, E, T);
-    else mt_xprep(b - nr, x, shg, H, xhi, xlo, xexp, gsh);
-}
-
-// Per token: the logits as the sum of the RT_SPLIT partial K ranges in order
-// (also stored to logits), then softmax / top-k / renormalisation
-// (route_dev.h).  Every partial load is issued before the first sum (clamped
-// index, no branch), so a lane waits for one round trip.
+// Per token, one workgroup: the activation preparation (row scale, hi/lo
+// fp16 activations in the gate/up operand order, shared-gate logit) and, on
+// wave 0, softmax / top-k / renormalisation with the host's arithmetic on
+// the router logits (route_dev.h topk_wave_exact).
 template <int MAXV>
-__global__ __launch_bounds__(WAVE) void k_topk_sum(const float *__restrict__ part, int T, int E, int K,
-                                                   float *__restrict__ logits, int32_t *__restrict__ idx,
-                                                   float *__restrict__ w)
+__global__ __launch_bounds__(256) void k_mt_topk_xprep(const float *__restrict__ logits, int E, int K,
+                                                       int32_t *__restrict__ idx, float *__restrict__ w,
+                                                       const float *__restrict__ x, const uint16_t *__restrict__ shg,
+                                                       int H, uint4 *__restrict__ xhi, uint4 *__restrict__ xlo,
+                                                       int *__restrict__ xexp, float *__restrict__ gsh)
 {
-    const int t = (int)blockIdx.x, lane = lane_id();
-    float q[RT_SPLIT][MAXV];
-#pragma unroll
-    for (int z = 0; z < RT_SPLIT; z++)
-#pragma unroll
-        for (int v = 0; v < MAXV; v++)
-            q[z][v] = part[((size_t)z * T + t) * E + min(lane + WAVE * v, E - 1)];
-    float p[MAXV];  // lane's entries lane + 64 v, topk_wave's layout
-#pragma unroll
-    for (int v = 0; v < MAXV; v++) {
-        const int e = lane + WAVE * v;
-        float sum = q[0][v];
-#pragma unroll
-        for (int z = 1; z < RT_SPLIT; z++) sum += q[z][v];
-        p[v] = e < E ? sum : -__builtin_inff();
-        if (e < E) logits[(size_t)t * E + e] = sum;
+    __shared__ __attribute__((aligned(16))) float s_e[WAVE * MAXV];
+    const int t = (int)blockIdx.x;
+    if (wave_id() == 0) {
+        int ik;
+        float wk;
+        topk_wave_exact<MAXV>(logits + (size_t)t * E, E, K, s_e, ik, wk);
+        if (lane_id() < K) {
+            idx[(size_t)t * K + lane_id()] = ik;
+            w[(size_t)t * K + lane_id()] = wk;
+        }
     }
-    int ik;
-    float wk;
-    topk_wave_vals<MAXV>(p, E, K, ik, wk);
-    if (lane < K) {
-        idx[(size_t)t * K + lane] = ik;
-        w[(size_t)t * K + lane] = wk;
-    }
+    mt_xprep(t, x, shg, H, xhi, xlo, xexp, gsh);
 }
 
 // ---------------------------------------------------------------------------
@@ -921,35 +828,20 @@ int bread_launch_moe_grouped(bread_moe_ctx_t *c, const bread_moe_layer_t *L, con
     const int Imax = s.expert_inter > s.shared_inter ? s.expert_inter : s.shared_inter;
     bread_grouped_ws &g = c->gws;
     bread_clear_stale_error();
-    // Up to 128 tokens the router tiles are too few for the device: K goes
-    // over RT_SPLIT workgroups per tile, partials in the expert-output buffer
-    // (written only by the down kernel, after the top-k has read them), and
-    // the activation preparation shares the launch.
-    const bool split = T <= 128 && (size_t)(K + 1) * H >= (size_t)RT_SPLIT * E;
-    float *part = split ? g.eo : c->logits;
-    if (split) {
-        const int nr = ((T + 15) / 16) * ((E + 15) / 16) * RT_SPLIT;
-        hipLaunchKernelGGL(k_mt_route_prep, dim3(nr + T), dim3(RT_WAVES / RT_SPLIT * WAVE), 0, st,
-                           (const float *)L->router, x, part, H, E, T, (const uint16_t *)L->shexp_gate,
-                           (uint4 *)g.xhi, (uint4 *)g.xlo, g.xexp, c->gsh);
-    } else {
-        hipLaunchKernelGGL(k_mt_xprep, dim3(T), dim3(256), 0, st, x, (const uint16_t *)L->shexp_gate, H,
-                           (uint4 *)g.xhi, (uint4 *)g.xlo, g.xexp, c->gsh);
-        BREAD_HIP(hipGetLastError());
-        hipLaunchKernelGGL(k_mt_router, dim3((T + 15) / 16, (E + 15) / 16, 1), dim3(RT_WAVES * WAVE), 0, st,
-                           (const float *)L->router, x, part, H, E, T);
-    }
-    BREAD_HIP(hipGetLastError());
-    if (split) {
-        if ((E + WAVE - 1) / WAVE <= 4)
-            hipLaunchKernelGGL(k_topk_sum<4>, dim3(T), dim3(WAVE), 0, st, part, T, E, K, c->logits, c->idx, c->w);
-        else
-            hipLaunchKernelGGL(k_topk_sum<16>, dim3(T), dim3(WAVE), 0, st, part, T, E, K, c->logits, c->idx, c->w);
-        BREAD_HIP(hipGetLastError());
-    } else {
-        const int rc = bread_launch_topk(c->logits, E, K, T, c->idx, c->w, st);
+    // router logits in the reference's order (route.hip), then per token the
+    // exact softmax / top-k with the activation preparation
+    {
+        const int rc = bread_launch_route_logits((const float *)L->router, nullptr, x, c->logits, nullptr, H, E, T,
+                                                 false, st);
         if (rc) return rc;
     }
+    if ((E + WAVE - 1) / WAVE <= 4)
+        hipLaunchKernelGGL(k_mt_topk_xprep<4>, dim3(T), dim3(256), 0, st, c->logits, E, K, c->idx, c->w, x,
+                           (const uint16_t *)L->shexp_gate, H, (uint4 *)g.xhi, (uint4 *)g.xlo, g.xexp, c->gsh);
+    else
+        hipLaunchKernelGGL(k_mt_topk_xprep<16>, dim3(T), dim3(256), 0, st, c->logits, E, K, c->idx, c->w, x,
+                           (const uint16_t *)L->shexp_gate, H, (uint4 *)g.xhi, (uint4 *)g.xlo, g.xexp, c->gsh);
+    BREAD_HIP(hipGetLastError());
     hipLaunchKernelGGL(k_mt_bucket, dim3(1), dim3(1024), 0, st, c->idx, T, K, E, g.pair_tok, g.pos_of,
                        (MtTile *)g.tiles, g.n_tiles);
     BREAD_HIP(hipGetLastError());

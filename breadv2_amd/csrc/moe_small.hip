@@ -13,12 +13,11 @@
 // vector ALUs.
 //
 // Kernels per layer, stream-ordered:
-//   k_sb_router   one router row a workgroup of 4 waves, a quarter of the row
-//                 a wave held in registers, dotted with every token (batches
-//                 of 4 tokens, one batch's activations requested while the
-//                 other's are summed); the extra row E is the fp16
-//                 shared-gate vector.
-//   k_sb_select   one workgroup: softmax / top-k per token, then slots: an
+//   k_route_seq   router logits and shared-gate scores in the reference's
+//                 sequential order (route.hip).
+//   k_sb_select   one workgroup: softmax / top-k per token with the host's
+//                 arithmetic (routing bit-identical to the reference's), then
+//                 slots: an
 //                 expert's tokens in chunks of at most SB_CH (the shared
 //                 expert's chunks first, with every token, then the chosen
 //                 experts in expert order), each with its (token, rank) pairs
@@ -87,7 +86,7 @@ __device__ __forceinline__ void load_row4(const float *p, int lane, int nm, floa
         v[m] = m < nm ? *reinterpret_cast<const float4 *>(p + 4 * lane + 256 * m) : make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
-// Softmax / top-k per token (the routing waves of the other paths), then the
+// Softmax / top-k per token (the host's arithmetic, topk_wave_exact), then the
 // experts chosen by any token numbered into slots in expert order (slot 0 is
 // the shared expert with every token), each slot with its (token, rank)
 // pairs in token order, from per-expert token bitmasks.  One workgroup of
@@ -98,6 +97,7 @@ __device__ void sb_select(const float *__restrict__ logits, int E, int K, int T,
                           int32_t *__restrict__ slot_pair, int32_t *__restrict__ n_slots)
 {
     __shared__ int sidx[SB_MAX_T * MAX_K];
+    __shared__ __attribute__((aligned(16))) float s_e[RT_WAVES][WAVE * MAXV];  // softmax scratch of each wave
     __shared__ uint32_t mask[MAX_E];  // tokens that chose expert e
     __shared__ int slot_of[MAX_E];
     __shared__ int wave_tot[RT_WAVES];
@@ -106,7 +106,7 @@ __device__ void sb_select(const float *__restrict__ logits, int E, int K, int T,
     for (int t = wv; t < T; t += RT_WAVES) {
         int ik;
         float wk;
-        topk_wave<MAXV>(logits + (size_t)t * E, E, K, ik, wk);
+        topk_wave_exact<MAXV>(logits + (size_t)t * E, E, K, s_e[wv], ik, wk);
         if (lane < K) {
             idx[(size_t)t * K + lane] = ik;
             w[(size_t)t * K + lane] = wk;
@@ -160,103 +160,6 @@ __device__ void sb_select(const float *__restrict__ logits, int E, int K, int T,
         slot_pair[(size_t)(slot_of[e] + pos / SB_CH) * SB_CH + pos % SB_CH] = t * (K + 1) + 1 + k;
     }
     for (int t = tid; t < T; t += RT_THREADS) slot_pair[t] = t * (K + 1);  // slot t / SB_CH, place t % SB_CH
-}
-
-// Router rows: one a workgroup of RW waves; wave v holds the 4-column chunks
-// 64 (v + RW m) + lane of the row, so each wave does a quarter of every
-// token's dot (at one wave a row the kernel was bound by the issue of ~120
-// instructions per token at one wave per SIMD).  Row E is the fp16
-// shared-gate vector.  Tokens go in batches of RB through two register
-// buffers in turn, one batch's activations in flight while the other's are
-// summed; the wave partials are added in wave order through LDS.
-constexpr int RB = 4;
-constexpr int RW = 4;                    // waves per router row
-constexpr int RM = MAX_H / (4 * WAVE * RW);  // chunks a lane holds (2)
-
-__device__ __forceinline__ void load_chunks(const float *p, int lane, int wv, int nq, float4 (&v)[RM])
-{
-#pragma unroll
-    for (int m = 0; m < RM; m++) {
-        const int q = lane + WAVE * (wv + RW * m);
-        v[m] = q < nq ? *reinterpret_cast<const float4 *>(p + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-}
-
-__device__ __forceinline__ void load_batch(const float *x, int t0, int T, int H, int lane, int wv,
-                                           float4 (&v)[RB][RM])
-{
-#pragma unroll
-    for (int j = 0; j < RB; j++) load_chunks(x + (size_t)min(t0 + j, T - 1) * H, lane, wv, H / 4, v[j]);
-}
-
-// The batch's RB partial dots advance together (independent chains); tokens
-// past T are computed on a repeated row and not stored.
-__device__ __forceinline__ void dot_batch(const float4 (&r)[RM], const float4 (&v)[RB][RM], int t0, int T, int lane,
-                                          float *part)
-{
-    float acc[RB];
-#pragma unroll
-    for (int j = 0; j < RB; j++) acc[j] = 0.f;
-#pragma unroll
-    for (int m = 0; m < RM; m++) {
-#pragma unroll
-        for (int j = 0; j < RB; j++) {
-            acc[j] = fmaf(r[m].x, v[j][m].x, acc[j]);
-            acc[j] = fmaf(r[m].y, v[j][m].y, acc[j]);
-            acc[j] = fmaf(r[m].z, v[j][m].z, acc[j]);
-            acc[j] = fmaf(r[m].w, v[j][m].w, acc[j]);
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < RB; j++) acc[j] = wave_sum(acc[j]);
-    if (lane == 0) {
-#pragma unroll
-        for (int j = 0; j < RB; j++)
-            if (t0 + j < T) part[t0 + j] = acc[j];
-    }
-}
-
-__global__ __launch_bounds__(RW * WAVE) void k_sb_router(const float *__restrict__ router,
-                                                         const uint16_t *__restrict__ shg,
-                                                         const float *__restrict__ x, float *__restrict__ logits,
-                                                         float *__restrict__ gsh, int H, int E, int T)
-{
-    __shared__ float part[RW][SB_MAX_T];
-    const int wv = wave_id(), lane = lane_id();
-    const int e = (int)blockIdx.x;
-    const int nq = H / 4;
-    float4 r[RM];
-    if (e < E) {
-        load_chunks(router + (size_t)e * H, lane, wv, nq, r);
-    } else {
-#pragma unroll
-        for (int m = 0; m < RM; m++) {
-            const int q = lane + WAVE * (wv + RW * m);
-            r[m] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (q < nq && shg) {
-                const uint2 g = *reinterpret_cast<const uint2 *>(shg + 4 * q);
-                r[m] = make_float4(h2f(g.x), h2f(g.x >> 16), h2f(g.y), h2f(g.y >> 16));
-            }
-        }
-    }
-    float4 xa[RB][RM], xb[RB][RM];
-    load_batch(x, 0, T, H, lane, wv, xa);
-    for (int t0 = 0; t0 < T; t0 += 2 * RB) {
-        load_batch(x, t0 + RB, T, H, lane, wv, xb);
-        dot_batch(r, xa, t0, T, lane, part[wv]);
-        if (t0 + RB >= T) break;
-        load_batch(x, t0 + 2 * RB, T, H, lane, wv, xa);
-        dot_batch(r, xb, t0 + RB, T, lane, part[wv]);
-    }
-    __syncthreads();
-    const int t = (int)threadIdx.x;
-    if (t < T) {
-        float v = part[0][t];
-#pragma unroll
-        for (int w = 1; w < RW; w++) v += part[w][t];
-        if (e < E) logits[(size_t)t * E + e] = v;
-        else gsh[t] = shg ? v : 0.f;
-    }
 }
 
 template <int MAXV>
@@ -1123,8 +1026,9 @@ int bread_launch_moe_small(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const
                      L->gate_expert_bytes, L->up_expert_bytes, L->down_expert_bytes};
     const SbSlots ss{g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots};
     bread_clear_stale_error();
-    hipLaunchKernelGGL(k_sb_router, dim3(E + 1), dim3(RW * WAVE), 0, st, L->router, L->shexp_gate, x, c->logits,
-                       c->gsh, H, E, T);
+    // routing logits and shared-gate scores in the reference's order (route.hip)
+    int rc = bread_launch_route_logits(L->router, L->shexp_gate, x, c->logits, c->gsh, H, E, T, true, st);
+    if (rc) return rc;
     if (E <= 4 * WAVE)
         hipLaunchKernelGGL(k_sb_select<4>, dim3(1), dim3(RT_THREADS), 0, st, c->logits, E, K, T, c->idx, c->w,
                            g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots);

@@ -1,0 +1,104 @@
+// route.hip — routing for the multi-token paths, bit-identical to the
+// reference's host routing (route_layer, one_layer.cu:964-985, with
+// cpu_softmax / cpu_topk, layer_ops.cu:222-250).
+//
+// k_route_seq computes every router logit in the reference's own order:
+//   logits[e] = ((0 + W[e][0] x[0]) + W[e][1] x[1]) + ... + W[e][H-1] x[H-1],
+// each product rounded to fp32, then added, never fused (one_layer.cu:969-971),
+// and the shared-gate score the same way with the fp16 gate widened
+// (one_layer.cu:977-980).  The sum is inherently sequential, so the kernel
+// gives each lane one token and each wave one router row: a lane's 2048
+// dependent adds (~5.5 ns each on gfx950 with the interleaved products, so
+// ~11 us for a 2048-column row: the latency floor of exact routing) run
+// while the 64 tokens of a wave and the rows of the grid run in parallel.  The row is read with scalar
+// loads (one value for the whole wave); the tokens' activations are staged
+// through LDS in chunks of 128 columns, double-buffered, a padded row per
+// token so a lane's 16-byte reads fall in distinct banks.
+//
+// k_topk_exact then runs softmax / top-k / renormalisation per token (one
+// wave) with the host's arithmetic (softmax_keys_exact): given identical
+// logits, indices and weights are bit-identical to the reference's.
+#include "bread_internal.h"
+#include "route_dev.h"
+#include "route_seq.h"
+
+namespace {
+
+using namespace route_seq;
+
+// Grid (ceil(E / (4 NE)) + shg_row, ceil(T / 64)): route_seq_block.
+template <int NE>
+__global__ __launch_bounds__(RS_WAVES * WAVE) void k_route_seq(const float *__restrict__ router,
+                                                              const uint16_t *__restrict__ shg,
+                                                              const float *__restrict__ x, float *__restrict__ logits,
+                                                              float *__restrict__ gsh, int H, int E, int T,
+                                                              int shg_row)
+{
+    __shared__ RsSmem S;
+    route_seq_block<NE>(S, (int)blockIdx.x, (int)blockIdx.y, router, shg, x, logits, gsh, H, E, T, shg_row != 0);
+}
+
+// One wave per token: softmax / top-k / renormalisation with the host's
+// arithmetic on the logits of k_route_seq.
+template <int MAXV>
+__global__ __launch_bounds__(WAVE) void k_topk_exact(const float *__restrict__ logits, int E, int K,
+                                                     int32_t *__restrict__ idx, float *__restrict__ w)
+{
+    __shared__ __attribute__((aligned(16))) float s_e[WAVE * MAXV];
+    const int t = (int)blockIdx.x;
+    int ik;
+    float wk;
+    topk_wave_exact<MAXV>(logits + (size_t)t * E, E, K, s_e, ik, wk);
+    if (lane_id() < K) {
+        idx[(size_t)t * K + lane_id()] = ik;
+        w[(size_t)t * K + lane_id()] = wk;
+    }
+}
+
+} // namespace
+
+// Router rows per wave: one while the grid has at most one workgroup a CU
+// (the latency of a lane's sum is then the kernel's time), two beyond, where
+// two rows sharing each activation read halve the LDS reads per product.
+int bread_route_rows_per_wave(int T, int E)
+{
+    const int tiles = (T + RS_TT - 1) / RS_TT;
+    return (size_t)tiles * ((E + RS_WAVES - 1) / RS_WAVES) <= 256 ? 1 : 2;
+}
+
+int bread_launch_route_logits(const float *router, const uint16_t *shg, const float *x, float *logits, float *gsh,
+                              int H, int E, int T, bool shg_row, hipStream_t st)
+{
+    BREAD_REQUIRE(H % RS_CJ == 0, BREAD_ERR_SHAPE, "hidden must be a multiple of 128");
+    const int ne = bread_route_rows_per_wave(T, E);
+    const dim3 grid((E + RS_WAVES * ne - 1) / (RS_WAVES * ne) + (shg_row ? 1 : 0), (T + RS_TT - 1) / RS_TT);
+    if (ne == 1)
+        hipLaunchKernelGGL(k_route_seq<1>, grid, dim3(RS_WAVES * WAVE), 0, st, router, shg, x, logits, gsh, H, E, T,
+                           shg_row ? 1 : 0);
+    else
+        hipLaunchKernelGGL(k_route_seq<2>, grid, dim3(RS_WAVES * WAVE), 0, st, router, shg, x, logits, gsh, H, E, T,
+                           shg_row ? 1 : 0);
+    BREAD_HIP(hipGetLastError());
+    return BREAD_OK;
+}
+
+int bread_launch_topk(const float *logits, int E, int K, int T, int32_t *idx, float *w, hipStream_t st)
+{
+    const int mv = (E + WAVE - 1) / WAVE;
+    if (mv <= 4)
+        hipLaunchKernelGGL(k_topk_exact<4>, dim3(T), dim3(WAVE), 0, st, logits, E, K, idx, w);
+    else
+        hipLaunchKernelGGL(k_topk_exact<16>, dim3(T), dim3(WAVE), 0, st, logits, E, K, idx, w);
+    BREAD_HIP(hipGetLastError());
+    return BREAD_OK;
+}
+
+int bread_launch_route(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, int T, int32_t *idx,
+                       float *w, float *gsh, hipStream_t st)
+{
+    const bread_moe_shape_t &s = c->shape;
+    bread_clear_stale_error();
+    int rc = bread_launch_route_logits(L->router, L->shexp_gate, x, c->logits, gsh, s.hidden, s.n_experts, T, true, st);
+    if (rc) return rc;
+    return bread_launch_topk(c->logits, s.n_experts, s.top_k, T, idx, w, st);
+}

@@ -370,6 +370,16 @@ void oracle_topk(const float *probs, int n, int K, int *indices, float *weights)
 }
 
 /* layer_ops.cu:252-255 */
+float oracle_expf(float x)
+{
+    return expf(x);
+}
+
+void oracle_expf_array(const float *x, float *out, uint64_t n)
+{
+    for (uint64_t i = 0; i < n; i++) out[i] = expf(x[i]);
+}
+
 float oracle_sigmoid(float x)
 {
     return 1.0f / (1.0f + expf(-x));
@@ -396,6 +406,16 @@ float oracle_route(const oracle_shape_t *s, const oracle_layer_t *L, const float
     oracle_topk(logits, E, s->top_k, idx, w);
     free(logits);
     return gsh;
+}
+
+void oracle_route_batch(const oracle_shape_t *s, const oracle_layer_t *L, const float *x, int n_tokens,
+                        int *idx, float *w, float *gsh, float *logits, int nthreads)
+{
+    const int H = s->hidden, E = s->n_experts, K = s->top_k;
+#pragma omp parallel for schedule(dynamic, 16) num_threads(nthreads)
+    for (int t = 0; t < n_tokens; t++)
+        gsh[t] = oracle_route(s, L, x + (size_t)t * H, idx + (size_t)t * K, w + (size_t)t * K,
+                              logits ? logits + (size_t)t * E : NULL);
 }
 
 static const uint8_t *expert_ptr(const uint8_t *base, uint64_t stride, int e)

@@ -62,6 +62,10 @@ void  oracle_swiglu(const float *gate, const float *up, float *out, int n);
 void  oracle_softmax(float *x, int n);
 void  oracle_topk(const float *probs, int n, int k, int *indices, float *weights);
 float oracle_sigmoid(float x);
+/* The C library's expf, which cpu_softmax / cpu_swiglu / cpu_sigmoid call
+ * (layer_ops.cu:214-255); the array form for checks in bulk. */
+float oracle_expf(float x);
+void  oracle_expf_array(const float *x, float *out, uint64_t n);
 
 /* One MoE layer's weights on the host, native GGUF layout.  Expert e of a
  * stacked tensor starts at base + e * expert_bytes (loader.h:35-47,
@@ -86,6 +90,12 @@ typedef struct {
  * NULL; when given it receives the pre-softmax logits. */
 float oracle_route(const oracle_shape_t *s, const oracle_layer_t *L, const float *x,
                    int *idx, float *w, float *logits);
+
+/* oracle_route for n_tokens tokens (x [T][H]; idx/w [T][K], gsh [T], logits
+ * [T][E] or NULL), tokens spread over `nthreads` OpenMP threads; each token
+ * is exactly oracle_route. */
+void oracle_route_batch(const oracle_shape_t *s, const oracle_layer_t *L, const float *x, int n_tokens,
+                        int *idx, float *w, float *gsh, float *logits, int nthreads);
 
 /* One token through the MoE block in the reference's fp32 order
  * (one_layer.cu:1416-1471): hidden += sigmoid(gsh)*shared(x), then

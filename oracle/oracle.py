@@ -56,6 +56,11 @@ _lib.oracle_sigmoid.restype = c_float
 _lib.oracle_sigmoid.argtypes = [c_float]
 _lib.oracle_route.restype = c_float
 _lib.oracle_route.argtypes = [POINTER(OShape), POINTER(OLayer), c_void_p, c_void_p, c_void_p, c_void_p]
+_lib.oracle_route_batch.argtypes = [POINTER(OShape), POINTER(OLayer), c_void_p, c_int, c_void_p, c_void_p, c_void_p,
+                                    c_void_p, c_int]
+_lib.oracle_expf.restype = c_float
+_lib.oracle_expf.argtypes = [c_float]
+_lib.oracle_expf_array.argtypes = [c_void_p, c_void_p, c_uint64]
 _lib.oracle_moe_token.argtypes = [POINTER(OShape), POINTER(OLayer), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
 _lib.oracle_moe_token_mt.argtypes = [POINTER(OShape), POINTER(OLayer), c_void_p, c_void_p, c_void_p, c_void_p,
                                      c_void_p, c_int]
@@ -186,6 +191,29 @@ def route(layer: HostLayer, x: np.ndarray, want_logits: bool = False):
     g = _lib.oracle_route(ctypes.byref(layer.shape), ctypes.byref(layer.desc),
                           _ptr(np.ascontiguousarray(x, np.float32)), _ptr(idx), _ptr(w), _ptr(logits))
     return (idx, w, g, logits) if want_logits else (idx, w, g)
+
+
+def route_batch(layer: HostLayer, x: np.ndarray, nthreads: int = 16, want_logits: bool = False):
+    """oracle_route for every row of x [T][H]: (idx [T][K], w [T][K], gsh [T]
+    [, logits [T][E]])."""
+    x = np.ascontiguousarray(x, np.float32)
+    T = x.shape[0]
+    K, E = layer.shape.top_k, layer.shape.n_experts
+    idx = np.empty((T, K), np.int32)
+    w = np.empty((T, K), np.float32)
+    g = np.empty(T, np.float32)
+    lg = np.empty((T, E), np.float32) if want_logits else None
+    _lib.oracle_route_batch(ctypes.byref(layer.shape), ctypes.byref(layer.desc), _ptr(x), T, _ptr(idx), _ptr(w),
+                            _ptr(g), _ptr(lg), nthreads)
+    return (idx, w, g, lg) if want_logits else (idx, w, g)
+
+
+def expf(x: np.ndarray) -> np.ndarray:
+    """The C library's expf (the one cpu_softmax calls), elementwise."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    _lib.oracle_expf_array(_ptr(x), _ptr(out), x.size)
+    return out
 
 
 def moe_forward(layer: HostLayer, x: np.ndarray, hidden: np.ndarray, n_tokens: int, nthreads: int = 1):
