@@ -120,6 +120,10 @@ SIGNATURES = {
     "bread_moe_ctx_destroy": (c_int, [c_void_p]),
     "bread_moe_ctx_check": (c_int, [c_void_p, POINTER(c_int)]),
     "bread_route": (c_int, [c_void_p, POINTER(MoeLayer), c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "bread_route_noalloc": (
+        c_int,
+        [POINTER(MoeShape), POINTER(MoeLayer), c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p],
+    ),
     "bread_route_layer": (
         c_int,
         [c_void_p, POINTER(MoeLayer), c_void_p, POINTER(c_int32), POINTER(c_float), POINTER(c_float), c_void_p],

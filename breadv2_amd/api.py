@@ -127,6 +127,18 @@ def shape_bytes(s: MoeShape) -> dict:
     }
 
 
+def route_noalloc(s: MoeShape, layer: MoeLayer, x: torch.Tensor, n_tokens: int, stream=None):
+    """bread_route_noalloc: routing without a context (the library's static
+    device workspace holds the logits; n_tokens * n_experts <= 1048576)."""
+    K = s.top_k
+    idx = torch.empty((n_tokens, K), dtype=torch.int32, device=x.device)
+    w = torch.empty((n_tokens, K), dtype=torch.float32, device=x.device)
+    gsh = torch.empty((n_tokens,), dtype=torch.float32, device=x.device)
+    check(lib.bread_route_noalloc(ctypes.byref(s), ctypes.byref(layer), _p(x), n_tokens, _p(idx), _p(w), _p(gsh),
+                                  _s(stream)), "bread_route_noalloc")
+    return idx, w, gsh
+
+
 @dataclass
 class LayerTensors:
     """One layer's weights as device tensors (keeps them alive)."""

@@ -115,6 +115,7 @@ struct bread_arena {
     int *flags;        // n_layers x BREAD_ARENA_HAS_*
 };
 
+int bread_validate_shape(const bread_moe_shape_t *s);
 int bread_validate_layer(const bread_moe_shape_t *s, const bread_moe_layer_t *L);
 
 // Launchers implemented in the .hip translation units.

@@ -69,7 +69,7 @@ extern "C" void bread_moe_shape_default(bread_moe_shape_t *s)
     s->rms_eps = 1e-6f;     // bread.h:68
 }
 
-static int validate_shape(const bread_moe_shape_t *s)
+int bread_validate_shape(const bread_moe_shape_t *s)
 {
     BREAD_REQUIRE(s, BREAD_ERR_ARG, "NULL shape");
     BREAD_REQUIRE(s->hidden > 0 && s->expert_inter > 0 && s->shared_inter > 0 && s->n_experts > 0 &&
@@ -114,7 +114,7 @@ int bread_validate_layer(const bread_moe_shape_t *s, const bread_moe_layer_t *L)
 
 extern "C" int bread_moe_ctx_create(const bread_moe_shape_t *shape, int max_tokens, bread_moe_ctx_t **out)
 {
-    int rc = validate_shape(shape);
+    int rc = bread_validate_shape(shape);
     if (rc) return rc;
     BREAD_REQUIRE(out && max_tokens > 0, BREAD_ERR_ARG, "out must be non-NULL and max_tokens > 0");
     *out = nullptr;

@@ -18,13 +18,42 @@
 // k_topk_exact then runs softmax / top-k / renormalisation per token (one
 // wave) with the host's arithmetic (softmax_keys_exact): given identical
 // logits, indices and weights are bit-identical to the reference's.
+#include <mutex>
+
 #include "bread_internal.h"
 #include "route_dev.h"
 #include "route_seq.h"
 
+// Logits workspace of bread_route_noalloc: n_tokens x n_experts floats at
+// most (4 MiB; each GPU the library runs on holds one until the process
+// ends).  Every entry a call reads is written by the same call first, so it
+// is never cleared; calls that overlap on one GPU share it and race.
+constexpr size_t SCRATCH_FLOATS = size_t(1) << 20;
+static __device__ __align__(256) float scratch[SCRATCH_FLOATS];
+
 namespace {
 
 using namespace route_seq;
+
+// Device address of `scratch` per device, taken once with that device current.
+constexpr int MAX_DEVICES = 64;
+float *scratch_ptr[MAX_DEVICES];
+std::mutex scratch_mu;
+
+int scratch_for_current_device(float **out)
+{
+    int dev = 0;
+    BREAD_HIP(hipGetDevice(&dev));
+    BREAD_REQUIRE(dev >= 0 && dev < MAX_DEVICES, BREAD_ERR_ARG, "device index beyond the scratch table");
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_ptr[dev]) {
+        void *p = nullptr;
+        BREAD_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        scratch_ptr[dev] = static_cast<float *>(p);
+    }
+    *out = scratch_ptr[dev];
+    return BREAD_OK;
+}
 
 // Grid (ceil(E / (4 NE)) + shg_row, ceil(T / 64)): route_seq_block.
 template <int NE>
@@ -101,4 +130,30 @@ int bread_launch_route(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const flo
     int rc = bread_launch_route_logits(L->router, L->shexp_gate, x, c->logits, gsh, s.hidden, s.n_experts, T, true, st);
     if (rc) return rc;
     return bread_launch_topk(c->logits, s.n_experts, s.top_k, T, idx, w, st);
+}
+
+// bread_route without a context: the logits live in this file's static
+// device workspace, so nothing is allocated on any call.
+extern "C" int bread_route_noalloc(const bread_moe_shape_t *shape, const bread_moe_layer_t *L, const float *x, int T,
+                                   int32_t *idx, float *w, float *gsh, bread_stream_t stream)
+{
+    int rc = bread_validate_shape(shape);
+    if (rc) return rc;
+    BREAD_REQUIRE(x && idx && w && gsh, BREAD_ERR_ARG, "NULL input or output");
+    BREAD_REQUIRE(T >= 0, BREAD_ERR_ARG, "n_tokens < 0");
+    BREAD_REQUIRE((size_t)T * (size_t)shape->n_experts <= SCRATCH_FLOATS, BREAD_ERR_CAPACITY,
+                  "n_tokens * n_experts exceeds the 1048576-float routing workspace");
+    BREAD_REQUIRE(((uintptr_t)x & 15) == 0, BREAD_ERR_ALIGN, "x must be 16-byte aligned");
+    rc = bread_validate_layer(shape, L);
+    if (rc) return rc;
+    if (T == 0) return BREAD_OK;
+    float *logits = nullptr;
+    rc = scratch_for_current_device(&logits);
+    if (rc) return rc;
+    const hipStream_t st = to_hip(stream);
+    bread_clear_stale_error();
+    rc = bread_launch_route_logits(L->router, L->shexp_gate, x, logits, gsh, shape->hidden, shape->n_experts, T,
+                                   true, st);
+    if (rc) return rc;
+    return bread_launch_topk(logits, shape->n_experts, shape->top_k, T, idx, w, st);
 }

@@ -190,6 +190,16 @@ int bread_route(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer, const floa
                 int n_tokens, int32_t *d_idx, float *d_w, float *d_gsh,
                 bread_stream_t stream);
 
+/* bread_route without a context, for callers that cannot allocate (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  The logits workspace is a static device
+ * array of 1,048,576 floats in the library (4 MiB per GPU, held until the
+ * process ends): n_tokens * n_experts above that returns BREAD_ERR_CAPACITY.
+ * Results are bit-identical to bread_route's.  Calls that overlap on one GPU
+ * share the workspace and race; serialise them (one stream, or events). */
+int bread_route_noalloc(const bread_moe_shape_t *shape, const bread_moe_layer_t *layer, const float *d_x,
+                        int n_tokens, int32_t *d_idx, float *d_w, float *d_gsh, bread_stream_t stream);
+
 /* route_layer-compatible shim: one token, results copied to host arrays
  * (idx[K], w[K]) and the raw shared-gate logit returned in *gsh_logit.
  * Synchronises the stream (route_layer does a blocking copy,

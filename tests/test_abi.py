@@ -93,3 +93,16 @@ def test_moe_calls_reject_null_context():
     assert _lib.lib.bread_route(None, ctypes.byref(layer), FAKE, 1, FAKE, FAKE, FAKE, None) == _lib.ERR_ARG
     assert _lib.lib.bread_moe_ctx_check(None, None) == _lib.ERR_ARG
     assert _lib.lib.bread_arena_layer(None, 0, ctypes.byref(layer)) == _lib.ERR_ARG
+
+
+def test_route_noalloc_rejects_beyond_workspace_on_host():
+    """n_tokens * n_experts above the 1048576-float workspace is refused
+    before any device call (and NULL outputs before that)."""
+    from breadv2_amd import api
+    s = api.shape()
+    layer = _lib.MoeLayer()
+    T = (1 << 20) // s.n_experts + 1
+    st = _lib.lib.bread_route_noalloc(ctypes.byref(s), ctypes.byref(layer), FAKE, T, FAKE, FAKE, FAKE, None)
+    assert st == _lib.ERR_CAPACITY
+    st = _lib.lib.bread_route_noalloc(ctypes.byref(s), ctypes.byref(layer), FAKE, 4, None, FAKE, FAKE, None)
+    assert st == _lib.ERR_ARG
