@@ -8,7 +8,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_uint16, c_uint64, c_void_p
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_longlong, c_uint16, c_uint64, c_void_p
 
 # PyTorch ships its own libamdhip64/libhsa-runtime64 (same soname as the
 # system ROCm).  Loading torch first makes libbread_moe bind to that one
@@ -54,8 +54,9 @@ ERR_FORMAT = -9
 
 
 class BreadError(RuntimeError):
-    def __init__(self, status: int, where: str):
+    def __init__(self, status: int, where: str, device_error: int = 0):
         self.status = status
+        self.device_error = device_error  # bread_moe_ctx_check's error word
         detail = lib.bread_last_error().decode(errors="replace")
         super().__init__(f"{where}: {status_str(status)} ({status}): {detail}")
 
@@ -157,6 +158,7 @@ SIGNATURES = {
         c_int, [c_void_p, POINTER(MoeLayer), c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "bread_moe_ctx_set_trace": (c_int, [c_void_p, c_void_p, ctypes.c_size_t, POINTER(c_int)]),
     "bread_moe_ctx_set_path": (c_int, [c_void_p, c_int]),
+    "bread_moe_ctx_set_spin_limit": (c_int, [c_void_p, c_longlong]),
     "bread_small_auto_tokens": (c_int, []),
     "bread_stack_loop_tokens": (c_int, []),
     "bread_rmsnorm_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_void_p]),

@@ -14,7 +14,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from ._lib import MoeLayer, MoeShape, check, lib
+from ._lib import BreadError, MoeLayer, MoeShape, check, lib
 
 QTYPE_Q8_0 = _lib.QTYPE_Q8_0
 QTYPE_Q4_K = _lib.QTYPE_Q4_K
@@ -370,6 +370,12 @@ class MoeContext:
         """bread_moe_ctx_set_path: PATH_AUTO, PATH_DECODE, PATH_GROUPED, PATH_PER_TOKEN or PATH_SMALL."""
         check(lib.bread_moe_ctx_set_path(self._h, path), "bread_moe_ctx_set_path")
 
+    def set_spin_limit(self, n_sleeps: int) -> None:
+        """bread_moe_ctx_set_spin_limit: bound every wait of the decode and
+        small-batch kernels at n_sleeps sleeps after the first look (< 0: the
+        kernels' defaults).  A small bound forces the time-out error paths."""
+        check(lib.bread_moe_ctx_set_spin_limit(self._h, n_sleeps), "bread_moe_ctx_set_spin_limit")
+
     def route(self, layer: MoeLayer, x: torch.Tensor, n_tokens: int, stream=None):
         K = self.shape.top_k
         idx = torch.empty((n_tokens, K), dtype=torch.int32, device=x.device)
@@ -499,8 +505,12 @@ class MoeContext:
         return g.value
 
     def check_device(self) -> int:
+        """bread_moe_ctx_check: 0, or BreadError carrying the kernels' error
+        word in .device_error (the call clears it and resets the context)."""
         e = ctypes.c_int(0)
-        check(lib.bread_moe_ctx_check(self._h, ctypes.byref(e)), "bread_moe_ctx_check")
+        rc = lib.bread_moe_ctx_check(self._h, ctypes.byref(e))
+        if rc != _lib.OK:
+            raise BreadError(int(rc), "bread_moe_ctx_check", e.value)
         return e.value
 
     def close(self) -> None:

@@ -42,6 +42,15 @@ struct alignas(128) bread_line {
     uint32_t pad[31];
 };
 
+// Bits of the context's device error word (bread_moe_ctx_check).
+enum : uint32_t {
+    BREAD_DEV_ERR_HWAIT = 1u,   // decode: a wait for hidden or SwiGLU values ran out
+    BREAD_DEV_ERR_LWAIT = 2u,   // decode: a wait for router logits or their radii ran out
+    BREAD_DEV_ERR_RANGE = 4u,   // grouped: a weight superblock's values exceed fp16's range
+    BREAD_DEV_ERR_PAIR = 8u,    // small batch: a wait on the partner wave ran out
+    BREAD_DEV_ERR_LOCAL = 16u,  // decode: a wait on another wave of the workgroup ran out
+};
+
 // Device-side status of the persistent decode kernel.
 struct bread_decode_sync {
     bread_line error;  // non-zero: a bounded wait expired (sticky until checked)
@@ -96,6 +105,7 @@ struct bread_moe_ctx {
     size_t trace_words;
     bread_grouped_ws gws;
     bread_small_ws sws;
+    int64_t spin_limit = -1;  // sleeps a bounded wait allows; < 0: each kernel's default
 };
 
 // Per-layer arena flags: which optional tensors the layer holds.

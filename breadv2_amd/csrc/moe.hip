@@ -210,6 +210,14 @@ extern "C" int bread_moe_ctx_set_path(bread_moe_ctx_t *c, int path)
     return BREAD_OK;
 }
 
+extern "C" int bread_moe_ctx_set_spin_limit(bread_moe_ctx_t *c, long long n_sleeps)
+{
+    BREAD_REQUIRE(c, BREAD_ERR_ARG, "NULL context");
+    BREAD_REQUIRE(n_sleeps <= (1ll << 24), BREAD_ERR_ARG, "spin limit above 2^24 sleeps");
+    c->spin_limit = n_sleeps < 0 ? -1 : n_sleeps;
+    return BREAD_OK;
+}
+
 extern "C" int bread_moe_ctx_set_trace(bread_moe_ctx_t *c, uint64_t *d_buf, size_t n_words, int *grid_out)
 {
     BREAD_REQUIRE(c, BREAD_ERR_ARG, "NULL context");

@@ -101,7 +101,7 @@ constexpr int N_XPOLL = 8;               // waves 0..7 poll the previous layer's
 constexpr int N_HPOLL = W_PF;            // waves 0..11 poll the SwiGLU outputs
 constexpr int W_RAD = 4;                 // wave 4 publishes the logit's radius
 constexpr int W_CERT = NWV - 1;          // wave 15 certifies the routing (a down wave, idle until the ranks are in)
-constexpr uint32_t SPIN_LIMIT = 1u << 18;
+constexpr uint32_t SPIN_DEFAULT = 1u << 18;  // sleeps a bounded wait allows after its first look
 constexpr uint32_t BUF_WORD3 = 0x00020000u;  // raw buffer descriptor word 3 (gfx9)
 constexpr int AUX_COHERENT = 16;             // sc1: device-coherent access
 constexpr uint32_t SENTINEL = 0x7FA5A5A5u;   // signalling NaN: "not written yet"
@@ -174,6 +174,7 @@ struct DecArgs {
     bread_decode_sync *sync;
     uint64_t *trace;         // [G][L][TP_N] or NULL
     int E, K;
+    uint32_t spin;           // sleeps a bounded wait allows after its first look
 };
 
 struct Smem {
@@ -214,6 +215,8 @@ struct Smem {
     int gudone;                        // routed gate/up waves done computing
     int cert;                          // 0: ranks may still change; 1: certified; 2: recomputed exactly
     int abort;                         // a wait failed: the workgroup leaves
+    int expired;                       // a wait on another wave of the workgroup ran out
+    uint32_t spin;                     // DecArgs::spin
 };
 // more than half of a CU's 160 KB, so the dispatcher puts one workgroup per CU
 static_assert(sizeof(Smem) > 80 * 1024 && sizeof(Smem) <= 160 * 1024, "LDS footprint");
@@ -277,19 +280,31 @@ __device__ __forceinline__ void lds_add(int *p, int v)
     __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Wave-level bounded wait for an LDS flag; false if the workgroup aborts.
-// slow: sleep longer between looks (for waits expected to last microseconds).
-__device__ __forceinline__ bool lds_wait(const Smem &S, const int *p, int target, bool slow = false)
+// A wait on another wave of the workgroup ran out: the workgroup leaves at
+// its next check, which flags BREAD_DEV_ERR_LOCAL.
+__device__ __forceinline__ void lds_expire(Smem &S)
 {
-    for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
+    lds_put(&S.expired, 1);
+    lds_put(&S.abort, 1);
+}
+
+// Wave-level bounded wait for an LDS flag; false if the workgroup aborts or
+// the wait runs out (lds_expire).  slow: sleep longer between looks (for
+// waits expected to last microseconds).
+__device__ __forceinline__ bool lds_wait(Smem &S, const int *p, int target, bool slow = false)
+{
+    const uint32_t lim = S.spin;
+    for (uint32_t it = 0;; it++) {
         if (lds_get(p) >= target) {
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             return true;
         }
         if (lds_get(&S.abort)) return false;
+        if (it >= lim) break;
         if (slow) __builtin_amdgcn_s_sleep(8);
         else __builtin_amdgcn_s_sleep(1);
     }
+    lds_expire(S);
     return false;
 }
 
@@ -360,18 +375,19 @@ __device__ __forceinline__ bool unwritten(float v)
 
 // Per-thread bounded poll of 4 coherent floats at byte offset off of a
 // buffer until none of the checked ones (all four, or the low two when hi is
-// false) is the sentinel.  Returns false on time-out (flagging the error) or
-// when another workgroup flagged one.
+// false) is the sentinel, sleeping at most lim times.  Returns false on
+// time-out (flagging the error) or when another workgroup flagged one.
 __device__ __forceinline__ bool poll4(bread_decode_sync *s, __amdgpu_buffer_rsrc_t r, uint32_t off, float4 &v,
-                                      bool hi = true)
+                                      uint32_t lim, bool hi = true)
 {
-    for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
+    for (uint32_t it = 0;; it++) {
         v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX_COHERENT));
         if (!unwritten(v.x) && !unwritten(v.y) && !(hi && (unwritten(v.z) || unwritten(v.w)))) return true;
+        if (it >= lim) break;
         if ((it & 63) == 63 && has_error(s)) return false;
         __builtin_amdgcn_s_sleep(1);
     }
-    flag_error(s, 1u);
+    flag_error(s, BREAD_DEV_ERR_HWAIT);
     return false;
 }
 
@@ -399,26 +415,29 @@ __device__ __forceinline__ uint64_t load_word(const uint64_t *p)
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Per-thread bounded poll of one tagged word of this layer, w its first read.
+// Per-thread bounded poll of one tagged word of this layer, w its first
+// read, sleeping at most lim times.
 __device__ __forceinline__ bool poll_word_from(bread_decode_sync *s, const uint64_t *p, uint32_t tag, float &v,
-                                               uint64_t w)
+                                               uint64_t w, uint32_t lim)
 {
-    for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
+    for (uint32_t it = 0;; it++) {
         if ((uint32_t)(w >> 32) == tag) {
             v = __builtin_bit_cast(float, (uint32_t)w);
             return true;
         }
+        if (it >= lim) break;
         if ((it & 63) == 63 && has_error(s)) return false;
         __builtin_amdgcn_s_sleep(1);
         w = load_word(p);
     }
-    flag_error(s, 2u);
+    flag_error(s, BREAD_DEV_ERR_LWAIT);
     return false;
 }
 
-__device__ __forceinline__ bool poll_word(bread_decode_sync *s, const uint64_t *p, uint32_t tag, float &v)
+__device__ __forceinline__ bool poll_word(bread_decode_sync *s, const uint64_t *p, uint32_t tag, float &v,
+                                          uint32_t lim)
 {
-    return poll_word_from(s, p, tag, v, load_word(p));
+    return poll_word_from(s, p, tag, v, load_word(p), lim);
 }
 
 // ---------------------------------------------------------------- routing
@@ -745,6 +764,7 @@ __device__ bool exact_routing(const DecArgs &a, const DecLayer &Ly, Smem &S, int
     trace_point_lane0(a, l, TP_XDOT);
     float p[4];
     bool ok = true;
+    const uint32_t lim = S.spin;
 #pragma unroll
     for (int vv = 0; vv < 4; vv++) {
         const int e = lane + WAVE * vv;
@@ -754,7 +774,7 @@ __device__ bool exact_routing(const DecArgs &a, const DecLayer &Ly, Smem &S, int
                 p[vv] = acc;
             } else {
                 float v = 0.f;
-                ok = poll_word(a.sync, a.texact + LG_STRIDE * e, tag32, v) && ok;
+                ok = poll_word(a.sync, a.texact + LG_STRIDE * e, tag32, v, lim) && ok;
                 p[vv] = v;
             }
         }
@@ -806,7 +826,8 @@ __device__ float4 cert_prepare(const DecArgs &a, Smem &S, int E, uint32_t tag32,
         w[vv] = e < E ? load_word(a.tradius + LG_STRIDE * e) : tag_word(tag32, 0.f);
     }
     bool ok = false;
-    for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
+    const uint32_t lim = S.spin;
+    for (uint32_t it = 0;; it++) {
         bool mine = true;
 #pragma unroll
         for (int vv = 0; vv < 4; vv++) mine = mine && (uint32_t)(w[vv] >> 32) == tag32;
@@ -814,6 +835,7 @@ __device__ float4 cert_prepare(const DecArgs &a, Smem &S, int E, uint32_t tag32,
             ok = true;
             break;
         }
+        if (it >= lim) break;
         if ((it & 63) == 63 && has_error(a.sync)) break;
         __builtin_amdgcn_s_sleep(1);
 #pragma unroll
@@ -823,7 +845,7 @@ __device__ float4 cert_prepare(const DecArgs &a, Smem &S, int E, uint32_t tag32,
         }
     }
     if (!ok) {
-        if (!has_error(a.sync)) flag_error(a.sync, 2u);
+        if (!has_error(a.sync)) flag_error(a.sync, BREAD_DEV_ERR_LWAIT);
         return make_float4(0.f, 0.f, 0.f, 0.f);
     }
     float rm = 0.f, am = 0.f;
@@ -861,7 +883,8 @@ __device__ int cert_fast(Smem &S, int E, int K, float4 cm, const float (&lv)[4])
     bool good = cm.z != 0.f;
     int have = 0;
     float prev = 0.f;
-    for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
+    const uint32_t lim = S.spin;
+    for (uint32_t it = 0;; it++) {
         const int n = lds_get(&S.nready);
         if (n > have) {
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -874,9 +897,12 @@ __device__ int cert_fast(Smem &S, int E, int K, float4 cm, const float (&lv)[4])
         }
         if (have >= K) break;
         if (lds_get(&S.abort)) return -1;
+        if (it >= lim) {
+            lds_expire(S);
+            return -1;
+        }
         __builtin_amdgcn_s_sleep(1);
     }
-    if (have < K) return -1;
     if (!good) return 0;
     if (K >= E) return 1;
     const float lo = prev - T;
@@ -889,38 +915,20 @@ __device__ int cert_fast(Smem &S, int E, int K, float4 cm, const float (&lv)[4])
     return cnt == K ? 1 : 0;
 }
 
-// Run by wave W_CERT once the K + 1 selection passes are published: the
-// fast logits order the top K + 1 as the reference's sums would (route_dev.h
-// gives each logit a radius around the reference's sequential sum).
-//   1. One radius for all: every consecutive gap of the top K + 1 exceeds
-//      2 R_max + tau (tau: the softmax rounding, so that strictly separated
-//      sums give strictly ordered probabilities).
-//   2. Each expert's own radius: with lo_k / hi_k = logit -/+ radius of rank
-//      k and M_k the largest hi of every expert ranked below k, ranks 0..k
-//      are certainly above the rest when min(lo_0..lo_k) > M_k + tau' (tau
-//      plus the rounding of lo and hi); certified when that holds for
-//      k = 0..K-1.
-//   3. If the only doubt is the order of two adjacent ranks j, j+1 (j + 1 <=
-//      K, separated from everything else), both logits are computed in the
-//      reference's order here (their router rows staged in S.wrow and S.nw,
-//      the products formed in place, then one lane's sequential sum each):
-//      equal logits tie (the lower index first, as cpu_topk's strict '>'
-//      takes it), logits more than tau apart order strictly.
-//   4. Otherwise exact_routing (every logit in the reference's order).
-// Returns 1 (certified), 2 (ranks settled anew) or 0 (a wait failed).
 // Wave W_CERT's wait for the K ranks, gathering each rank's expert and
 // logit into lane k as the ranks arrive (the LDS reads overlap the passes),
 // then rank K: the largest logit not selected, the lowest such index (its
-// probability key is the one the passes would give it: wk_key).  False if
+// probability key is the one the passes would give it: key_of).  False if
 // the workgroup aborts.
-__device__ bool cert_gather(Smem &S, int E, int K, int &wk, float &lk, uint32_t &kK)
+__device__ bool cert_gather(Smem &S, int E, int K, int &wk, float &lk)
 {
     const int lane = opaque(lane_id());
     int have = 0;
     wk = 0;
     lk = 0.f;
     bool ok = false;
-    for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
+    const uint32_t lim = S.spin;
+    for (uint32_t it = 0;; it++) {
         const int n = lds_get(&S.nready);
         if (n > have) {
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -935,10 +943,13 @@ __device__ bool cert_gather(Smem &S, int E, int K, int &wk, float &lk, uint32_t 
             break;
         }
         if (lds_get(&S.abort)) return false;
+        if (it >= lim) break;
         __builtin_amdgcn_s_sleep(1);
     }
-    if (!ok) return false;
-    kK = 0u;
+    if (!ok) {
+        lds_expire(S);
+        return false;
+    }
     if (K >= E) return true;
     int ws[MAXK];
 #pragma unroll
@@ -962,17 +973,42 @@ __device__ bool cert_gather(Smem &S, int E, int K, int &wk, float &lk, uint32_t 
     const uint64_t at = __builtin_amdgcn_ballot_w64(bi < E && bm == m);
     const int wl = at ? (int)__builtin_ctzll(at) : 0;
     const int eK = __builtin_amdgcn_readlane(bi, wl);
-    const float2 ms = S.smax;
     if (lane == K) {
         wk = eK < E ? eK : 0;
         lk = m;
     }
-    kK = prob_key(expf(m - ms.x) / ms.y);
     return true;
 }
 
+// The probability key the selection passes give a logit m (rank K's, when
+// the certificate moves it into the top K).
+__device__ __forceinline__ uint32_t key_of(const Smem &S, float m)
+{
+    const float2 ms = S.smax;
+    return prob_key(expf(m - ms.x) / ms.y);
+}
+
+// Run by wave W_CERT once the K + 1 selection passes are published: the
+// fast logits order the top K + 1 as the reference's sums would (route_dev.h
+// gives each logit a radius around the reference's sequential sum).
+//   1. One radius for all: every consecutive gap of the top K + 1 exceeds
+//      2 R_max + tau (tau: the softmax rounding, so that strictly separated
+//      sums give strictly ordered probabilities).
+//   2. Each expert's own radius: with lo_k / hi_k = logit -/+ radius of rank
+//      k and M_k the largest hi of every expert ranked below k, ranks 0..k
+//      are certainly above the rest when min(lo_0..lo_k) > M_k + tau' (tau
+//      plus the rounding of lo and hi); certified when that holds for
+//      k = 0..K-1.
+//   3. If the only doubt is the order of two adjacent ranks j, j+1 (j + 1 <=
+//      K, separated from everything else), both logits are computed in the
+//      reference's order here (their router rows staged in S.wrow and S.nw,
+//      the products formed in place, then one lane's sequential sum each):
+//      equal logits tie (the lower index first, as cpu_topk's strict '>'
+//      takes it), logits more than tau apart order strictly.
+//   4. Otherwise exact_routing (every logit in the reference's order).
+// Returns 1 (certified), 2 (ranks settled anew) or 0 (a wait failed).
 __device__ int certify(const DecArgs &a, const DecLayer &Ly, Smem &S, int g, int E, int K, uint32_t tag32, int l,
-                       float4 cm, int wk, float lk, uint32_t kK)
+                       float4 cm, int wk, float lk)
 {
 #pragma clang fp contract(off)
     const int lane = opaque(lane_id());  // not hoisted out of the layer loop
@@ -1042,8 +1078,9 @@ __device__ int certify(const DecArgs &a, const DecLayer &Ly, Smem &S, int g, int
             trace_point_lane0(a, l, TP_XDOT);
             if (__builtin_isfinite(la) && __builtin_isfinite(lb) && (la == lb || fabsf(la - lb) > tau)) {
                 const bool swap = la == lb ? eb < ea : lb > la;
+                const float lK = lane_f(lk, K);
                 if (swap && lane == 0) {
-                    const uint32_t kb = j + 1 < K ? S.key[j + 1] : kK;
+                    const uint32_t kb = j + 1 < K ? S.key[j + 1] : key_of(S, lK);
                     if (j + 1 < K) {
                         S.idx[j + 1] = ea;
                         S.key[j + 1] = S.key[j];
@@ -1093,9 +1130,13 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
     const float sent = __builtin_bit_cast(float, SENTINEL);
     // No barrier here: one would wait for the prefetch (a barrier waits for
     // the wave's direct-to-LDS loads), serialising it with layer 0's input
-    // load.  P1's barrier publishes S.abort = 0; layer 0 never polls, so no
-    // wave sets S.abort before it.
-    if (tid == 0) S.abort = 0;
+    // load.  P1's barrier publishes these three; layer 0 neither polls nor
+    // waits before it, so no wave reads or sets them earlier.
+    if (tid == 0) {
+        S.abort = 0;
+        S.expired = 0;
+        S.spin = a.spin;
+    }
     prefetch(S, load_layer(a, 0), g, E, wid, 0);
 
     for (int l = 0; l < a.L; l++) {
@@ -1144,7 +1185,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                         *reinterpret_cast<const float4 *>(a.hidden + 4 * tid);
             } else {
                 const auto r = rsrc(a.xbuf + (par ^ 1) * (G * XREC), G * XREC * 4);
-                ok = poll4(sy, r, 4u * (uint32_t)(XREC * (tid >> 1) + 4 * (tid & 1)), hv);
+                ok = poll4(sy, r, 4u * (uint32_t)(XREC * (tid >> 1) + 4 * (tid & 1)), hv, S.spin);
             }
             if (own && !(l == 0 && a.x0)) *reinterpret_cast<float4 *>(&S.hown[4 * (tid & 1)]) = hv;
             const float ss = wave_sum(fmaf(hv.x, hv.x, fmaf(hv.y, hv.y, fmaf(hv.z, hv.z, hv.w * hv.w))));
@@ -1156,7 +1197,10 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             __builtin_amdgcn_s_waitcnt(0);
         }
         __syncthreads();
-        if (S.abort) break;
+        if (S.abort) {
+            if (tid == 0 && S.expired) flag_error(sy, BREAD_DEV_ERR_LOCAL);
+            break;
+        }
         if (wid < N_XPOLL) {
             if (!(l == 0 && a.x0)) {
                 float ss = 0.f;
@@ -1237,7 +1281,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                 float v = -__builtin_inff();
                 bool ok = true;
                 if (tid == g) v = S.own_lg;
-                else if (other) ok = poll_word_from(sy, a.tlogits + LG_STRIDE * tid, tag32, v, w0);
+                else if (other) ok = poll_word_from(sy, a.tlogits + LG_STRIDE * tid, tag32, v, w0, S.spin);
                 S.lg[tid] = v;
                 if (!ok) lds_put(&S.abort, 1);
                 if (lane == 0) lds_add(&S.lgcnt, 1);
@@ -1349,8 +1393,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                 if (st == 0) {
                     int wk;
                     float lk;
-                    uint32_t kK;
-                    st = cert_gather(S, E, K, wk, lk, kK) ? certify(a, Ly, S, g, E, K, tag32, l, cm, wk, lk, kK) : 0;
+                    st = cert_gather(S, E, K, wk, lk) ? certify(a, Ly, S, g, E, K, tag32, l, cm, wk, lk) : 0;
                 }
                 if (lane == 0) lds_put(st > 0 ? &S.cert : &S.abort, st > 0 ? st : 1);
                 __builtin_amdgcn_s_setprio(0);
@@ -1416,10 +1459,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
         }
         if (hpoll) {
             bool ok = true;
-            for (uint32_t it = 0; it < SPIN_LIMIT; it++) {
+            const uint32_t lim = S.spin;
+            for (uint32_t it = 0;; it++) {
                 if (!r0) r0 = !unwritten(v0.x) && !unwritten(v0.y) && !(hi0 && (unwritten(v0.z) || unwritten(v0.w)));
                 if (!r1) r1 = !unwritten(v1.x) && !unwritten(v1.y) && !(hi1 && (unwritten(v1.z) || unwritten(v1.w)));
                 if (r0 && r1) break;
+                if (it >= lim) break;
                 if ((it & 63) == 63 && has_error(sy)) break;
                 __builtin_amdgcn_s_sleep(1);
                 if (!r0)
@@ -1430,7 +1475,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                                                         hr, (int)(4 * (XREC * wb + 4 * q1)), 0, AUX_COHERENT));
             }
             if (!(r0 && r1)) {
-                if (!has_error(sy)) flag_error(sy, 1u);
+                if (!has_error(sy)) flag_error(sy, BREAD_DEV_ERR_HWAIT);
                 ok = false;
             }
             // columns 2w, 2w+1 stay adjacent in the hpos layout
@@ -1447,7 +1492,10 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             if (!ok) S.abort = 1;
         }
         __syncthreads();
-        if (S.abort) break;
+        if (S.abort) {
+            if (tid == 0 && S.expired) flag_error(sy, BREAD_DEV_ERR_LOCAL);
+            break;
+        }
         trace_point(a, l, TP_HREADY);
 
         // ---- P6: down dots
@@ -1558,6 +1606,7 @@ int launch(bread_moe_ctx_t *c, DecArgs &a, hipStream_t st)
     a.sync = c->dsync;
     a.trace = (c->trace && (size_t)G * a.L * TP_N <= c->trace_words) ? c->trace : nullptr;
     a.eps = c->shape.rms_eps;
+    a.spin = c->spin_limit >= 0 ? (uint32_t)c->spin_limit : SPIN_DEFAULT;
     bread_clear_stale_error();
     if (c->epoch > UINT32_MAX - 1u - (uint32_t)a.L) {
         // the layer tags would wrap past 2^32 in this launch: every tagged

@@ -76,10 +76,6 @@ struct MtTile {
     int pad;
 };
 
-// Device error word bit: a weight superblock whose dequantised values do
-// not fit fp16 (the grouped path's MFMA operand type).
-constexpr uint32_t DEV_ERR_RANGE = 4u;
-
 struct MtArgs {
     bread_moe_layer_t L;
     uint32_t *err;           // device error word of the context
@@ -187,7 +183,7 @@ __device__ __forceinline__ f32x16 mfma32(const uint4 &w, const uint4 &x, f32x16 
 //                                               the fp16 rounding of dmin * m)
 // Valid while d * 945 and dmin * 63 stay inside fp16's range (|d| < 64,
 // |dmin| < 1024), which fp16 weights need anyway; superblocks outside it
-// raise DEV_ERR_RANGE.
+// raise BREAD_DEV_ERR_RANGE.
 struct Q4Pk {
     half2v sc[4], nsc[4], m[4], d;
 };
@@ -511,7 +507,7 @@ __global__ __launch_bounds__(GU_WAVES * WAVE, 2) void k_mt_gateup(const MtArgs a
     };
     auto compute = [&](int st, const uint4 (&B)[5]) {
         if (__builtin_amdgcn_ballot_w64(!q4k_pk_ok(B[0])) != 0 && lane == 0)
-            __hip_atomic_fetch_or(a.err, DEV_ERR_RANGE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_or(a.err, BREAD_DEV_ERR_RANGE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const Q4Pk pk = q4k_lane_pk(B[0], (uint32_t)g);
         ksteps(st, B, [&](uint32_t v, int q) {
             const uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
@@ -698,7 +694,7 @@ __global__ __launch_bounds__(DN_WAVES * WAVE, 2) void k_mt_down(const MtArgs a)
             }
         }
         if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0)
-            __hip_atomic_fetch_or(a.err, DEV_ERR_RANGE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_or(a.err, BREAD_DEV_ERR_RANGE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (b == nb - 1) {
             if (r < tl.nr) {
                 const int e = sexp[r];

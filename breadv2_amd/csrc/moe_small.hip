@@ -786,17 +786,28 @@ struct SwDnSmem {
     float dot[SW_MAX_P][8];                // per pair: the workgroup's eight output rows
     int hin[SW_NW];                        // per wave: rounds whose loads have landed
     int hout[SW_NW];                       // per wave: rounds whose SwiGLU rows it has used
+    int bad;                               // a wait on a partner wave ran out: no output
 };
 static_assert(sizeof(SwDnSmem) <= 160 * 1024, "LDS");
 
-// Bounded wait on a partner wave's LDS round counter.
-__device__ __forceinline__ void sw_wait(const int *p, int target)
+// Sleeps a partner wait allows after its first look, by default.
+constexpr uint32_t SW_SPIN_DEFAULT = 1u << 20;
+
+// Bounded wait on a partner wave's LDS round counter, sleeping at most lim
+// times; false when it runs out.
+__device__ __forceinline__ bool sw_wait(const int *p, int target, uint32_t lim)
 {
-    for (uint32_t it = 0; it < (1u << 20); it++) {
-        if (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+    bool ok = false;
+    for (uint32_t it = 0;; it++) {
+        if (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) {
+            ok = true;
+            break;
+        }
+        if (it >= lim) break;
         __builtin_amdgcn_s_sleep(1);
     }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    return ok;
 }
 
 __device__ __forceinline__ void sw_put(int *p, int v)
@@ -814,10 +825,13 @@ __device__ __forceinline__ void sw_put(int *p, int v)
 // bytes 64n + 32 (l / 8) + 4 (l % 8) + k and bit pairs s of the qh bytes
 // 32n + 4 (l % 8) + k, with scales 8n + (l % 8) / 4 + 2s
 // (dequant_q4k_cpu.c:155-170).
+// A partner wait that runs out (after spin sleeps) leaves that round's dots
+// unstored; the workgroup then writes none of its rows of hidden and sets
+// BREAD_DEV_ERR_PAIR in *err.
 __global__ __launch_bounds__(SW_NT, 1) void k_sw_down(SbLayer L, const float *__restrict__ h, SbSlots S,
                                                       float *__restrict__ hidden, const float *__restrict__ w,
                                                       const float *__restrict__ gsh, int E, int K, int T,
-                                                      int max_slots)
+                                                      int max_slots, uint32_t *err, uint32_t spin)
 {
     __shared__ SwDnSmem M;
     const int g = (int)blockIdx.x, tid = (int)threadIdx.x, wid = tid / WAVE, lane = lane_id();
@@ -827,6 +841,7 @@ __global__ __launch_bounds__(SW_NT, 1) void k_sw_down(SbLayer L, const float *__
         M.hin[tid] = 0;
         M.hout[tid] = 0;
     }
+    if (tid == 0) M.bad = 0;
     int ns = *S.n;
     ns = ns < max_slots ? (ns > 0 ? ns : 0) : max_slots;
     const int m2 = wid >> 1, u = wid & 1, pw = wid ^ 1;
@@ -878,7 +893,8 @@ __global__ __launch_bounds__(SW_NT, 1) void k_sw_down(SbLayer L, const float *__
         meta(s + SW_NW / 2, en, cntn, prn);
         __builtin_amdgcn_s_waitcnt(0);  // this round's band and this wave's SwiGLU rows
         if (lane == 0) sw_put(&M.hin[wid], rnd + 1);
-        sw_wait(&M.hin[pw], rnd + 1);
+        const bool in = sw_wait(&M.hin[pw], rnd + 1, spin);
+        if (!in && lane == 0) sw_put(&M.bad, 1);
         if (cnt > 0) {
             // pre-decode the lane's 32 weights of row rr: w[4 jj + k] = (d sc)
             // (q - 32) as fma(q, ds, -32 ds), one rounding
@@ -920,7 +936,7 @@ __global__ __launch_bounds__(SW_NT, 1) void k_sw_down(SbLayer L, const float *__
                     acc = fmaf(wq[4 * jj + 3], hv.w, acc);
                 }
                 acc = sum16(acc);
-                if (l == 0) M.dot[pr[k]][4 * u + rr] = acc;
+                if (l == 0 && in) M.dot[pr[k]][4 * u + rr] = acc;
             }
         } else if (cntn > 0) {
             issue_band(en);
@@ -928,7 +944,7 @@ __global__ __launch_bounds__(SW_NT, 1) void k_sw_down(SbLayer L, const float *__
         // both waves are done with this round's SwiGLU rows: the next round's
         __builtin_amdgcn_s_waitcnt(WAITCNT_LGKM0);
         if (lane == 0) sw_put(&M.hout[wid], rnd + 1);
-        sw_wait(&M.hout[pw], rnd + 1);
+        if (!sw_wait(&M.hout[pw], rnd + 1, spin) && lane == 0) sw_put(&M.bad, 1);
         if (cntn > 0) issue_h(prn);
         e = en;
         cnt = cntn;
@@ -936,6 +952,10 @@ __global__ __launch_bounds__(SW_NT, 1) void k_sw_down(SbLayer L, const float *__
         for (int k = 0; k < SB_CH; k++) pr[k] = prn[k];
     }
     __syncthreads();
+    if (M.bad) {
+        if (tid == 0) __hip_atomic_fetch_or(err, BREAD_DEV_ERR_PAIR, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     // combine in the reference order (one_layer.cu:1443-1471): shared expert
     // first, then the routed experts by rank
     if (tid < T * 8) {
@@ -1038,8 +1058,9 @@ int bread_launch_moe_small(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const
     if (H == SW_H && I == SW_I && Ish == SW_I && K <= SW_K && T <= SW_MAX_T) {
         // the decode shape: every workgroup owns a slice of every slot
         hipLaunchKernelGGL(k_sw_gateup, dim3(SW_G), dim3(SW_NT), 0, st, sl, x, ss, c->h, E, K, T, S);
+        const uint32_t spin = c->spin_limit >= 0 ? (uint32_t)c->spin_limit : SW_SPIN_DEFAULT;
         hipLaunchKernelGGL(k_sw_down, dim3(SW_G), dim3(SW_NT), 0, st, sl, c->h, ss, hidden, c->w, c->gsh, E, K, T,
-                           S);
+                           S, &c->dsync->error.v, spin);
         BREAD_HIP(hipGetLastError());
         return BREAD_OK;
     }

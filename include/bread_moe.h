@@ -164,6 +164,13 @@ typedef enum {
 } bread_moe_path_t;
 
 int bread_moe_ctx_set_path(bread_moe_ctx_t *ctx, int path);
+/* Bounds every wait of the decode and small-batch kernels on this context
+ * at n_sleeps sleeps after the first look (n_sleeps < 0: each kernel's
+ * default, 2^18 and 2^20; at most 2^24).  A wait that runs out sets its bit
+ * of the error word (bread_moe_ctx_check) and the kernel exits normally.  No
+ * reference counterpart: a small limit forces those error paths from the
+ * host, for tests. */
+int bread_moe_ctx_set_spin_limit(bread_moe_ctx_t *ctx, long long n_sleeps);
 /* Largest n_tokens the automatic choice sends to the small-batch path. */
 int bread_small_auto_tokens(void);
 /* Largest n_tokens for which bread_moe_stack_forward's automatic choice runs
@@ -174,10 +181,15 @@ int bread_stack_loop_tokens(void);
 /* Synchronises the context's last stream and returns BREAD_ERR_DEVICE (and
  * the kernel's error word in *device_error, if given) when a kernel flagged
  * a fault.  Bits: 1 = the decode kernel's bounded wait for hidden or SwiGLU
- * values expired, 2 = its wait for router logits expired (both: a launch that
- * could not get every CU), 4 = the grouped path met a weight superblock whose
- * dequantised values exceed fp16's range (Q4_K d >= 64 or dmin >= 1024,
- * Q6_K |d*sc| >= 2047).  Clears the word. */
+ * values expired, 2 = its wait for router logits or their radii expired
+ * (both: a launch that could not get every CU), 4 = the grouped path met a
+ * weight superblock whose dequantised values exceed fp16's range (Q4_K
+ * d >= 64 or dmin >= 1024, Q6_K |d*sc| >= 2047), 8 = the small-batch down
+ * kernel's wait on a partner wave expired (the workgroup then writes none of
+ * its rows of hidden), 16 = a decode workgroup's wait on another of its own
+ * waves expired.  Outputs of a launch that set a bit are unspecified.  Clears
+ * the word and resets the decode exchange state, so the context is usable
+ * again. */
 int bread_moe_ctx_check(bread_moe_ctx_t *ctx, int *device_error);
 
 /* Routing for n_tokens tokens on the device: router GEMV (fp32), softmax,

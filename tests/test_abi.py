@@ -92,6 +92,7 @@ def test_moe_calls_reject_null_context():
     assert _lib.lib.bread_moe_forward(None, ctypes.byref(layer), FAKE, FAKE, 1, None, None, None, None) == _lib.ERR_ARG
     assert _lib.lib.bread_route(None, ctypes.byref(layer), FAKE, 1, FAKE, FAKE, FAKE, None) == _lib.ERR_ARG
     assert _lib.lib.bread_moe_ctx_check(None, None) == _lib.ERR_ARG
+    assert _lib.lib.bread_moe_ctx_set_spin_limit(None, 0) == _lib.ERR_ARG
     assert _lib.lib.bread_arena_layer(None, 0, ctypes.byref(layer)) == _lib.ERR_ARG
 
 
