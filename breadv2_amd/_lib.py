@@ -20,7 +20,8 @@ except ImportError:  # plain C/ctypes users without torch: the system runtime is
     pass
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libbread_moe.so")
+# BREAD_MOE_LIB: another build of the library (the sanitizer build of tests/sanitize.sh)
+LIB_PATH = os.environ.get("BREAD_MOE_LIB") or os.path.join(HERE, "libbread_moe.so")
 
 QTYPE_F32 = 0
 QTYPE_F16 = 1

@@ -12,7 +12,8 @@ from ctypes import POINTER, c_float, c_int, c_uint8, c_uint16, c_uint64, c_void_
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+# BREAD_ORACLE_LIB: another build of the oracle (the sanitizer build of tests/sanitize.sh)
+LIB_PATH = os.environ.get("BREAD_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 REF_PATH = os.path.join(HERE, "_ref", "libref_dequant.so")
 
 QTYPE_F32, QTYPE_F16, QTYPE_Q8_0, QTYPE_Q4_K, QTYPE_Q6_K = 0, 1, 8, 12, 14
