@@ -183,6 +183,7 @@ SIGNATURES = {
     "bread_ggml_type_size": (c_uint64, [ctypes.c_uint32, c_uint64]),
     "bread_gguf_moe_shape": (c_int, [c_void_p, c_int, POINTER(MoeShape)]),
     "bread_arena_load_gguf": (c_int, [c_void_p, c_int, c_void_p, c_int]),
+    "bread_arena_set_layer_types": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
 }
 
 

@@ -112,19 +112,42 @@ def shape(hidden=2048, expert_inter=512, shared_inter=512, n_experts=256, top_k=
     return MoeShape(hidden, expert_inter, shared_inter, n_experts, top_k, rms_eps)
 
 
-def shape_bytes(s: MoeShape) -> dict:
+# Expert tensor types of a layer: gate, up, down, gate_shexp, up_shexp,
+# down_shexp.  STANDARD_TYPES is the mix the reference GPU path hardcodes and
+# the specialised kernels take; each entry may be Q4_K or Q6_K.
+STANDARD_TYPES = (QTYPE_Q4_K, QTYPE_Q4_K, QTYPE_Q6_K, QTYPE_Q4_K, QTYPE_Q4_K, QTYPE_Q6_K)
+BLOCK_BYTES = {QTYPE_Q4_K: 144, QTYPE_Q6_K: 210}
+
+
+def row_bytes(qtype: int, cols: int) -> int:
+    """Bytes of one Q4_K or Q6_K row of cols columns."""
+    return (cols // 256) * BLOCK_BYTES[qtype]
+
+
+def layer_types(d: MoeLayer) -> tuple:
+    return (d.gate_type, d.up_type, d.down_type, d.gate_shexp_type, d.up_shexp_type, d.down_shexp_type)
+
+
+def shape_bytes(s: MoeShape, types=STANDARD_TYPES) -> dict:
     """Byte sizes of one layer's tensors (native GGUF layout)."""
     H, I, Ish, E = s.hidden, s.expert_inter, s.shared_inter, s.n_experts
+    g, u, d, gs, us, ds = types
     return {
-        "gate_expert": I * (H // 256) * 144,
-        "up_expert": I * (H // 256) * 144,
-        "down_expert": H * (I // 256) * 210,
-        "gate_sh": Ish * (H // 256) * 144,
-        "up_sh": Ish * (H // 256) * 144,
-        "down_sh": H * (Ish // 256) * 210,
+        "gate_expert": I * row_bytes(g, H),
+        "up_expert": I * row_bytes(u, H),
+        "down_expert": H * row_bytes(d, I),
+        "gate_sh": Ish * row_bytes(gs, H),
+        "up_sh": Ish * row_bytes(us, H),
+        "down_sh": H * row_bytes(ds, Ish),
         "router": E * H * 4,
         "shgate": H * 2,
     }
+
+
+def synth_quant(dst, qtype: int, nbytes: int, seed: int, stream=None) -> None:
+    """Fill nbytes of Q4_K or Q6_K superblocks with the device generator."""
+    fn = synth_q4k if qtype == QTYPE_Q4_K else synth_q6k
+    fn(dst, nbytes // BLOCK_BYTES[qtype], seed, stream)
 
 
 def route_noalloc(s: MoeShape, layer: MoeLayer, x: torch.Tensor, n_tokens: int, stream=None):
@@ -152,15 +175,17 @@ class LayerTensors:
     down_sh: torch.Tensor
     router: torch.Tensor
     shgate: torch.Tensor | None
+    types: tuple = STANDARD_TYPES
 
     def desc(self) -> MoeLayer:
-        b = shape_bytes(self.shape)
+        b = shape_bytes(self.shape, self.types)
+        g, u, d, gs, us, ds = self.types
         return MoeLayer(
             self.gate_exps.data_ptr(), self.up_exps.data_ptr(), self.down_exps.data_ptr(),
             b["gate_expert"], b["up_expert"], b["down_expert"],
-            QTYPE_Q4_K, QTYPE_Q4_K, QTYPE_Q6_K,
+            g, u, d,
             self.gate_sh.data_ptr(), self.up_sh.data_ptr(), self.down_sh.data_ptr(),
-            QTYPE_Q4_K, QTYPE_Q4_K, QTYPE_Q6_K,
+            gs, us, ds,
             self.router.data_ptr(),
             self.shgate.data_ptr() if self.shgate is not None else None,
             None,
@@ -174,9 +199,11 @@ def layer_seeds(seed: int, layer: int) -> dict:
 
 
 def synth_layer_tensors(s: MoeShape, seed: int, layer: int = 0, router_std: float = 0.02,
-                        shgate_std: float = 0.02, device="cuda", stream=None) -> LayerTensors:
-    """Allocate one layer with torch and fill it with the device generator."""
-    b = shape_bytes(s)
+                        shgate_std: float = 0.02, device="cuda", stream=None, types=STANDARD_TYPES) -> LayerTensors:
+    """Allocate one layer with torch and fill it with the device generator
+    (types: the six expert tensor types, each Q4_K or Q6_K)."""
+    types = tuple(types)
+    b = shape_bytes(s, types)
     E = s.n_experts
     sd = layer_seeds(seed, layer)
     u8 = dict(dtype=torch.uint8, device=device)
@@ -190,13 +217,15 @@ def synth_layer_tensors(s: MoeShape, seed: int, layer: int = 0, router_std: floa
         torch.empty(b["down_sh"], **u8),
         torch.empty(E * s.hidden, dtype=torch.float32, device=device),
         torch.empty(s.hidden, dtype=torch.float16, device=device),
+        types,
     )
-    synth_q4k(t.gate_exps, E * b["gate_expert"] // 144, sd["gate_exps"], stream)
-    synth_q4k(t.up_exps, E * b["up_expert"] // 144, sd["up_exps"], stream)
-    synth_q6k(t.down_exps, E * b["down_expert"] // 210, sd["down_exps"], stream)
-    synth_q4k(t.gate_sh, b["gate_sh"] // 144, sd["gate_sh"], stream)
-    synth_q4k(t.up_sh, b["up_sh"] // 144, sd["up_sh"], stream)
-    synth_q6k(t.down_sh, b["down_sh"] // 210, sd["down_sh"], stream)
+    g, u, d, gs, us, ds = types
+    synth_quant(t.gate_exps, g, E * b["gate_expert"], sd["gate_exps"], stream)
+    synth_quant(t.up_exps, u, E * b["up_expert"], sd["up_exps"], stream)
+    synth_quant(t.down_exps, d, E * b["down_expert"], sd["down_exps"], stream)
+    synth_quant(t.gate_sh, gs, b["gate_sh"], sd["gate_sh"], stream)
+    synth_quant(t.up_sh, us, b["up_sh"], sd["up_sh"], stream)
+    synth_quant(t.down_sh, ds, b["down_sh"], sd["down_sh"], stream)
     synth_normal_f32(t.router, E * s.hidden, sd["router"], 0.0, router_std, stream)
     synth_normal_f16(t.shgate, s.hidden, sd["shgate"], 0.0, shgate_std, stream)
     return t
@@ -304,23 +333,31 @@ class Arena:
         check(lib.bread_arena_layer(self._h, l, ctypes.byref(d)), "bread_arena_layer")
         return d
 
+    def set_layer_types(self, l: int, types) -> None:
+        """bread_arena_set_layer_types: the six expert tensor types of layer l
+        (gate, up, down, gate_shexp, up_shexp, down_shexp; Q4_K or Q6_K)."""
+        check(lib.bread_arena_set_layer_types(self._h, l, *[int(t) for t in types]), "bread_arena_set_layer_types")
+
     def synth_layer(self, l: int, seed: int, router_std=0.02, shgate_std=0.02, stream=None) -> None:
         d = self.layer(l)
         s = self.shape
-        b = shape_bytes(s)
+        types = layer_types(d)
+        b = shape_bytes(s, types)
         E = s.n_experts
         sd = layer_seeds(seed, l)
         st = _s(stream)
 
-        def q(fn, ptr, nb, sv):
-            check(fn(ctypes.c_void_p(ptr), nb, sv, st), fn.__name__)
+        def q(qtype, ptr, nbytes, sv):
+            fn = lib.bread_synth_q4k if qtype == QTYPE_Q4_K else lib.bread_synth_q6k
+            check(fn(ctypes.c_void_p(ptr), nbytes // BLOCK_BYTES[qtype], sv, st), fn.__name__)
 
-        q(lib.bread_synth_q4k, d.gate_exps, E * b["gate_expert"] // 144, sd["gate_exps"])
-        q(lib.bread_synth_q4k, d.up_exps, E * b["up_expert"] // 144, sd["up_exps"])
-        q(lib.bread_synth_q6k, d.down_exps, E * b["down_expert"] // 210, sd["down_exps"])
-        q(lib.bread_synth_q4k, d.gate_shexp, b["gate_sh"] // 144, sd["gate_sh"])
-        q(lib.bread_synth_q4k, d.up_shexp, b["up_sh"] // 144, sd["up_sh"])
-        q(lib.bread_synth_q6k, d.down_shexp, b["down_sh"] // 210, sd["down_sh"])
+        g, u, dn, gs, us, ds = types
+        q(g, d.gate_exps, E * b["gate_expert"], sd["gate_exps"])
+        q(u, d.up_exps, E * b["up_expert"], sd["up_exps"])
+        q(dn, d.down_exps, E * b["down_expert"], sd["down_exps"])
+        q(gs, d.gate_shexp, b["gate_sh"], sd["gate_sh"])
+        q(us, d.up_shexp, b["up_sh"], sd["up_sh"])
+        q(ds, d.down_shexp, b["down_sh"], sd["down_sh"])
         check(lib.bread_synth_normal_f32(ctypes.c_void_p(d.router), E * s.hidden, sd["router"], 0.0, router_std, st),
               "bread_synth_normal_f32")
         if d.shexp_gate:

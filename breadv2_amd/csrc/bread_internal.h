@@ -114,16 +114,51 @@ enum : int {
     BREAD_ARENA_HAS_NORM = 2,    // fp32 post-attention norm weight (otherwise unit)
 };
 
+// Where one arena layer's tensors sit in its allocation, for its weight types.
+struct bread_arena_layout {
+    int types[6];  // gate, up, down, gate_sh, up_sh, down_sh: BREAD_QTYPE_Q4_K or _Q6_K
+    uint64_t layer_bytes;
+    uint64_t off_gate, off_up, off_down, off_gate_sh, off_up_sh, off_down_sh, off_router, off_shgate, off_norm;
+    uint64_t gate_expert_bytes, up_expert_bytes, down_expert_bytes;
+};
+
 struct bread_arena {
     bread_moe_shape_t shape;
     int n_layers;
     int device;
-    uint64_t layer_bytes;
-    uint64_t off_gate, off_up, off_down, off_gate_sh, off_up_sh, off_down_sh, off_router, off_shgate, off_norm;
-    uint64_t gate_expert_bytes, up_expert_bytes, down_expert_bytes;
-    uint8_t **layers;  // n_layers device allocations
-    int *flags;        // n_layers x BREAD_ARENA_HAS_*
+    bread_arena_layout *lay;  // n_layers layouts
+    uint8_t **layers;         // n_layers device allocations
+    int *flags;               // n_layers x BREAD_ARENA_HAS_*
 };
+
+// Layout of a layer with the given types; re-lays out (and reallocates)
+// layer l of the arena when its types differ (synth.hip).
+bread_arena_layout bread_arena_plan(const bread_moe_shape_t &s, const int types[6]);
+int bread_arena_relayout(bread_arena_t *a, int l, const int types[6]);
+
+// Expert tensor types: each of gate, up and down, routed and shared, is
+// Q4_K or Q6_K (loader.c:191-193 records them per tensor; the fp32 path
+// dispatches on them, one_layer.cu:1465-1468 and layer_ops.cu:169-189).
+__host__ __device__ inline bool bread_expert_qtype(int t)
+{
+    return t == BREAD_QTYPE_Q4_K || t == BREAD_QTYPE_Q6_K;
+}
+
+// Bytes of one row of `cols` columns (a multiple of 256) of a Q4_K or Q6_K tensor.
+__host__ __device__ inline uint64_t bread_expert_row_bytes(int t, int cols)
+{
+    return (uint64_t)(cols / 256) * (t == BREAD_QTYPE_Q4_K ? 144u : 210u);
+}
+
+// The layout the specialised kernels (decode, small-batch, grouped) take:
+// Q4_K gate and up, Q6_K down, for the routed experts and the shared one.
+// Other mixes run on the per-token kernels.
+inline bool bread_standard_qtypes(const bread_moe_layer_t *L)
+{
+    return L->gate_type == BREAD_QTYPE_Q4_K && L->up_type == BREAD_QTYPE_Q4_K && L->down_type == BREAD_QTYPE_Q6_K &&
+           L->gate_shexp_type == BREAD_QTYPE_Q4_K && L->up_shexp_type == BREAD_QTYPE_Q4_K &&
+           L->down_shexp_type == BREAD_QTYPE_Q6_K;
+}
 
 int bread_validate_shape(const bread_moe_shape_t *s);
 int bread_validate_layer(const bread_moe_shape_t *s, const bread_moe_layer_t *L);
@@ -157,6 +192,10 @@ int bread_launch_moe_decode(bread_moe_ctx_t *ctx, const bread_moe_layer_t *L, co
 // Routing outputs of layer l at idx + l * rstride * K (w alike, gsh + l * rstride).
 int bread_launch_decode_layers(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layers, int n, float *hidden,
                                int32_t *idx, float *w, float *gsh, hipStream_t st, int rstride = 1);
+// The same for any mix of weight types (verify.hip): runs of layers with the
+// decode kernel's types in one launch each, other layers on the per-token kernels.
+int bread_launch_decode_runs(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layers, int n, float *hidden,
+                             int32_t *idx, float *w, float *gsh, hipStream_t st, int rstride);
 int bread_decode_max_blocks(int *out);
 int bread_decode_grid(const bread_moe_shape_t &s);
 int bread_decode_trace_points();

@@ -401,7 +401,8 @@ extern "C" int bread_gguf_moe_shape(const bread_gguf_t *g, int layer, bread_moe_
 }
 
 // One layer's MoE tensors into layer `arena_layer` of the arena: routed and
-// shared gate/up/down (Q4_K, Q4_K, Q6_K), the fp32 router, the optional fp16
+// shared gate/up/down (each Q4_K or Q6_K, as the file gives them; the arena
+// layer is re-laid out for those types), the fp32 router, the optional fp16
 // shared gate and the optional fp32 post-attention norm weight.
 extern "C" int bread_arena_load_gguf(bread_arena_t *a, int arena_layer, const bread_gguf_t *g, int gguf_layer)
 {
@@ -410,25 +411,26 @@ extern "C" int bread_arena_load_gguf(bread_arena_t *a, int arena_layer, const br
     const bread_moe_shape_t &s = a->shape;
     const uint64_t H = (uint64_t)s.hidden, I = (uint64_t)s.expert_inter, Ish = (uint64_t)s.shared_inter;
     const uint64_t E = (uint64_t)s.n_experts;
+    constexpr uint32_t EXPERT = 0xFFFFFFFFu;  // Q4_K or Q6_K
     struct Want {
         const char *suffix;
         uint32_t type;
         uint64_t d0, d1, d2;  // expected dims (d2 = 0: 2-d, d1 = 0: 1-d)
-        uint64_t off;
         bool optional;
     };
     const Want want[] = {
-        {"ffn_gate_exps.weight", BREAD_QTYPE_Q4_K, H, I, E, a->off_gate, false},
-        {"ffn_up_exps.weight", BREAD_QTYPE_Q4_K, H, I, E, a->off_up, false},
-        {"ffn_down_exps.weight", BREAD_QTYPE_Q6_K, I, H, E, a->off_down, false},
-        {"ffn_gate_shexp.weight", BREAD_QTYPE_Q4_K, H, Ish, 0, a->off_gate_sh, false},
-        {"ffn_up_shexp.weight", BREAD_QTYPE_Q4_K, H, Ish, 0, a->off_up_sh, false},
-        {"ffn_down_shexp.weight", BREAD_QTYPE_Q6_K, Ish, H, 0, a->off_down_sh, false},
-        {"ffn_gate_inp.weight", 0 /* F32 */, H, E, 0, a->off_router, false},
-        {"ffn_gate_inp_shexp.weight", 1 /* F16 */, H, 0, 0, a->off_shgate, true},
-        {"post_attention_norm.weight", 0 /* F32 */, H, 0, 0, a->off_norm, true},
+        {"ffn_gate_exps.weight", EXPERT, H, I, E, false},
+        {"ffn_up_exps.weight", EXPERT, H, I, E, false},
+        {"ffn_down_exps.weight", EXPERT, I, H, E, false},
+        {"ffn_gate_shexp.weight", EXPERT, H, Ish, 0, false},
+        {"ffn_up_shexp.weight", EXPERT, H, Ish, 0, false},
+        {"ffn_down_shexp.weight", EXPERT, Ish, H, 0, false},
+        {"ffn_gate_inp.weight", 0 /* F32 */, H, E, 0, false},
+        {"ffn_gate_inp_shexp.weight", 1 /* F16 */, H, 0, 0, true},
+        {"post_attention_norm.weight", 0 /* F32 */, H, 0, 0, true},
     };
     const Tensor *found[9];
+    int types[6];
     for (int i = 0; i < 9; i++) {
         const Want &w = want[i];
         const Tensor *t = find(g, layer_name(gguf_layer, w.suffix).c_str());
@@ -437,7 +439,12 @@ extern "C" int bread_arena_load_gguf(bread_arena_t *a, int arena_layer, const br
             BREAD_REQUIRE(w.optional, BREAD_ERR_SHAPE, "a MoE tensor of the layer is missing");
             continue;
         }
-        BREAD_REQUIRE(t->type == w.type, BREAD_ERR_QTYPE, "tensor type differs from the device path's");
+        if (w.type == EXPERT) {
+            BREAD_REQUIRE(bread_expert_qtype((int)t->type), BREAD_ERR_QTYPE, "expert tensors must be Q4_K or Q6_K");
+            types[i] = (int)t->type;
+        } else {
+            BREAD_REQUIRE(t->type == w.type, BREAD_ERR_QTYPE, "router, shared gate and norm must be F32, F16, F32");
+        }
         const uint32_t nd = w.d2 ? 3 : (w.d1 ? 2 : 1);
         // vectors may carry trailing unit dimensions ([H] or [H, 1])
         bool dims_ok = (nd == 1 ? t->n_elems == w.d0 : t->n_dims == nd) && t->dims[0] == w.d0;
@@ -445,10 +452,15 @@ extern "C" int bread_arena_load_gguf(bread_arena_t *a, int arena_layer, const br
         if (nd == 3) dims_ok = dims_ok && t->dims[2] == w.d2;
         BREAD_REQUIRE(dims_ok && t->size > 0, BREAD_ERR_SHAPE, "tensor dimensions differ from the arena's shape");
     }
+    const int rc = bread_arena_relayout(a, arena_layer, types);
+    if (rc) return rc;
+    const bread_arena_layout &p = a->lay[arena_layer];
+    const uint64_t off[9] = {p.off_gate,    p.off_up,     p.off_down,   p.off_gate_sh, p.off_up_sh,
+                             p.off_down_sh, p.off_router, p.off_shgate, p.off_norm};
     uint8_t *base = a->layers[arena_layer];
     for (int i = 0; i < 9; i++) {
         if (!found[i]) continue;
-        BREAD_HIP(hipMemcpy(base + want[i].off, g->map + g->data_off + found[i]->offset, found[i]->size,
+        BREAD_HIP(hipMemcpy(base + off[i], g->map + g->data_off + found[i]->offset, found[i]->size,
                             hipMemcpyHostToDevice));
     }
     a->flags[arena_layer] = (found[7] ? BREAD_ARENA_HAS_SHGATE : 0) | (found[8] ? BREAD_ARENA_HAS_NORM : 0);

@@ -89,21 +89,26 @@ int bread_validate_layer(const bread_moe_shape_t *s, const bread_moe_layer_t *L)
     BREAD_REQUIRE(L->gate_exps && L->up_exps && L->down_exps && L->gate_shexp && L->up_shexp &&
                       L->down_shexp && L->router,
                   BREAD_ERR_ARG, "NULL weight pointer in layer");
-    BREAD_REQUIRE(L->gate_type == BREAD_QTYPE_Q4_K && L->up_type == BREAD_QTYPE_Q4_K &&
-                      L->down_type == BREAD_QTYPE_Q6_K && L->gate_shexp_type == BREAD_QTYPE_Q4_K &&
-                      L->up_shexp_type == BREAD_QTYPE_Q4_K && L->down_shexp_type == BREAD_QTYPE_Q6_K,
-                  BREAD_ERR_QTYPE, "device MoE path takes Q4_K gate/up and Q6_K down");
-    const uint64_t gb = (uint64_t)s->expert_inter * (s->hidden / QK) * Q4K_BYTES;
-    const uint64_t db = (uint64_t)s->hidden * (s->expert_inter / QK) * Q6K_BYTES;
-    BREAD_REQUIRE(L->gate_expert_bytes >= gb && L->up_expert_bytes >= gb && L->down_expert_bytes >= db,
+    // per tensor: pointer, expert stride (0: the shared expert), type
+    const struct {
+        const void *p;
+        uint64_t stride;
+        int type;
+    } ts[6] = {{L->gate_exps, L->gate_expert_bytes, L->gate_type}, {L->up_exps, L->up_expert_bytes, L->up_type},
+               {L->down_exps, L->down_expert_bytes, L->down_type}, {L->gate_shexp, 0, L->gate_shexp_type},
+               {L->up_shexp, 0, L->up_shexp_type},                 {L->down_shexp, 0, L->down_shexp_type}};
+    for (const auto &t : ts)
+        BREAD_REQUIRE(bread_expert_qtype(t.type), BREAD_ERR_QTYPE, "expert tensors must be Q4_K or Q6_K");
+    const int H = s->hidden, I = s->expert_inter;
+    BREAD_REQUIRE(L->gate_expert_bytes >= (uint64_t)I * bread_expert_row_bytes(L->gate_type, H) &&
+                      L->up_expert_bytes >= (uint64_t)I * bread_expert_row_bytes(L->up_type, H) &&
+                      L->down_expert_bytes >= (uint64_t)H * bread_expert_row_bytes(L->down_type, I),
                   BREAD_ERR_SHAPE, "expert stride smaller than one expert");
-    const uintptr_t a16 = (uintptr_t)L->gate_exps | (uintptr_t)L->up_exps | (uintptr_t)L->gate_shexp |
-                          (uintptr_t)L->up_shexp | (uintptr_t)L->router | L->gate_expert_bytes |
-                          L->up_expert_bytes;
-    BREAD_REQUIRE((a16 & 15) == 0, BREAD_ERR_ALIGN, "Q4_K experts and router must be 16-byte aligned");
-    const uintptr_t a4 = (uintptr_t)L->down_exps | (uintptr_t)L->down_shexp | L->down_expert_bytes |
-                         (uintptr_t)L->shexp_gate;
-    BREAD_REQUIRE((a4 & 3) == 0, BREAD_ERR_ALIGN, "Q6_K experts must be 4-byte aligned");
+    // Q4_K superblocks are read in 16-byte units, Q6_K ones in 4-byte units
+    for (const auto &t : ts)
+        BREAD_REQUIRE((((uintptr_t)t.p | t.stride) & (t.type == BREAD_QTYPE_Q4_K ? 15u : 3u)) == 0, BREAD_ERR_ALIGN,
+                      "Q4_K tensors and strides must be 16-byte aligned, Q6_K ones 4-byte aligned");
+    BREAD_REQUIRE(((uintptr_t)L->router & 15) == 0, BREAD_ERR_ALIGN, "router must be 16-byte aligned");
     BREAD_REQUIRE(((uintptr_t)L->shexp_gate & 7) == 0, BREAD_ERR_ALIGN, "shexp_gate must be 8-byte aligned");
     return BREAD_OK;
 }
@@ -231,7 +236,15 @@ extern "C" int bread_moe_ctx_set_trace(bread_moe_ctx_t *c, uint64_t *d_buf, size
 // Per-token expert kernels (routing: route.hip)
 // ---------------------------------------------------------------------------
 
-// One wave per (token, slot, row): gate and up rows, then SwiGLU.
+// One wave's partial dot of a Q4_K or Q6_K row (nb superblocks) with x.
+__device__ __forceinline__ float kq_row_partial(int type, const uint8_t *row, int nb, const float *x, int lane)
+{
+    return type == BREAD_QTYPE_Q4_K ? q4k_row_partial(row, nb, x, lane) : q6k_row_partial(row, nb, x, lane);
+}
+
+// One wave per (token, slot, row): gate and up rows, then SwiGLU.  Each
+// tensor has its own type (Q4_K or Q6_K), as in the reference's
+// cpu_tensor_matvec dispatch (one_layer.cu:1465-1468).
 __global__ __launch_bounds__(256) void k_gateup(bread_moe_layer_t L, const float *__restrict__ x,
                                                 const int32_t *__restrict__ idx, float *__restrict__ h, int H,
                                                 int I, int Ish, int K, int T)
@@ -244,20 +257,24 @@ __global__ __launch_bounds__(256) void k_gateup(bread_moe_layer_t L, const float
     const int slot = (int)((v % per_tok) / Imax);
     const int r = (int)(v % Imax);
     if (r >= (slot ? I : Ish)) return;
-    const uint64_t rb = (uint64_t)(H / QK) * Q4K_BYTES;
     const uint8_t *g, *u;
+    int gt, ut;
     if (slot == 0) {
         g = (const uint8_t *)L.gate_shexp;
         u = (const uint8_t *)L.up_shexp;
+        gt = L.gate_shexp_type;
+        ut = L.up_shexp_type;
     } else {
         const int e = idx[(size_t)t * K + slot - 1];
         g = (const uint8_t *)L.gate_exps + (uint64_t)e * L.gate_expert_bytes;
         u = (const uint8_t *)L.up_exps + (uint64_t)e * L.up_expert_bytes;
+        gt = L.gate_type;
+        ut = L.up_type;
     }
     const float *xt = x + (size_t)t * H;
     const int lane = lane_id();
-    const float gv = wave_sum(q4k_row_partial(g + r * rb, H / QK, xt, lane));
-    const float uv = wave_sum(q4k_row_partial(u + r * rb, H / QK, xt, lane));
+    const float gv = wave_sum(kq_row_partial(gt, g + r * bread_expert_row_bytes(gt, H), H / QK, xt, lane));
+    const float uv = wave_sum(kq_row_partial(ut, u + r * bread_expert_row_bytes(ut, H), H / QK, xt, lane));
     if (lane == 0) h[((size_t)t * (K + 1) + slot) * Imax + r] = silu_mul(gv, uv);
 }
 
@@ -275,15 +292,16 @@ __global__ __launch_bounds__(256) void k_down(bread_moe_layer_t L, const int32_t
     const int r = (int)(v % H);
     const int lane = lane_id();
     const float *ht = h + (size_t)t * (K + 1) * Imax;
-    const float sh = wave_sum(q6k_row_partial((const uint8_t *)L.down_shexp + (uint64_t)r * (Ish / QK) * Q6K_BYTES,
-                                              Ish / QK, ht, lane));
+    const int st = L.down_shexp_type, dt = L.down_type;
+    const float sh = wave_sum(kq_row_partial(
+        st, (const uint8_t *)L.down_shexp + (uint64_t)r * bread_expert_row_bytes(st, Ish), Ish / QK, ht, lane));
     float acc = hidden[(size_t)t * H + r];
     acc += sigmoidf_ref(gsh[t]) * sh;
-    const uint64_t rb = (uint64_t)(I / QK) * Q6K_BYTES;
+    const uint64_t rb = bread_expert_row_bytes(dt, I);
     for (int k = 0; k < K; k++) {
         const int e = idx[(size_t)t * K + k];
         const uint8_t *d = (const uint8_t *)L.down_exps + (uint64_t)e * L.down_expert_bytes + r * rb;
-        const float eo = wave_sum(q6k_row_partial(d, I / QK, ht + (size_t)(k + 1) * Imax, lane));
+        const float eo = wave_sum(kq_row_partial(dt, d, I / QK, ht + (size_t)(k + 1) * Imax, lane));
         acc += w[(size_t)t * K + k] * eo;
     }
     if (lane == 0) hidden[(size_t)t * H + r] = acc;
@@ -505,6 +523,10 @@ extern "C" int bread_moe_forward(bread_moe_ctx_t *c, const bread_moe_layer_t *L,
     if (T == 0) return BREAD_OK;
     hipStream_t st = to_hip(stream);
     c->last_stream = st;
+    if (c->path == BREAD_PATH_DECODE || c->path == BREAD_PATH_GROUPED || c->path == BREAD_PATH_SMALL)
+        BREAD_REQUIRE(bread_standard_qtypes(L), BREAD_ERR_QTYPE,
+                      "the decode, small-batch and grouped kernels take Q4_K gate/up and Q6_K down "
+                      "(BREAD_PATH_PER_TOKEN and BREAD_PATH_AUTO take any mix of Q4_K and Q6_K)");
     switch (c->path) {
     case BREAD_PATH_DECODE:
         BREAD_REQUIRE(T == 1, BREAD_ERR_SHAPE, "the decode path takes one token");
@@ -579,7 +601,7 @@ extern "C" int bread_moe_decode_layers(bread_moe_ctx_t *c, const bread_moe_layer
     if (n == 0) return BREAD_OK;
     hipStream_t st = to_hip(stream);
     c->last_stream = st;
-    int rc = bread_launch_decode_layers(c, layers, n, hidden, idx, w, gsh, st);
+    int rc = bread_launch_decode_runs(c, layers, n, hidden, idx, w, gsh, st, 1);
     if (rc == BREAD_ERR_SHAPE) return bread_fail(rc, "bread_moe_decode_layers", "shape not supported by the decode kernel");
     return rc;
 }

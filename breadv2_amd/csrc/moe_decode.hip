@@ -1578,6 +1578,7 @@ __global__ void k_clear_words(uint64_t *p, int n)
 
 bool layer_ok(const bread_moe_layer_t &L)
 {
+    if (!bread_standard_qtypes(&L)) return false;
     // buffer loads and 16-byte band loads assume these alignments
     const uintptr_t m = (uintptr_t)L.gate_exps | (uintptr_t)L.up_exps | (uintptr_t)L.down_exps |
                         (uintptr_t)L.gate_shexp | (uintptr_t)L.up_shexp | (uintptr_t)L.down_shexp |

@@ -808,7 +808,7 @@ void bread_grouped_free(bread_moe_ctx_t *c)
 
 bool bread_grouped_supported(const bread_moe_shape_t &s, const bread_moe_layer_t *L)
 {
-    if (s.expert_inter > MAX_INTER || s.shared_inter > MAX_INTER) return false;
+    if (s.expert_inter > MAX_INTER || s.shared_inter > MAX_INTER || !bread_standard_qtypes(L)) return false;
     // Q6_K expert blocks must end 16-byte aligned (see the down operand order)
     const uintptr_t a16 = (uintptr_t)L->down_exps | (uintptr_t)L->down_shexp | L->down_expert_bytes;
     return (a16 & 15) == 0;

@@ -977,10 +977,8 @@ bool bread_small_supported(const bread_moe_shape_t &s, const bread_moe_layer_t *
     const bool io = (s.expert_inter == 256 || s.expert_inter == 512) &&
                     (s.shared_inter == 256 || s.shared_inter == 512);
     return s.hidden % QK == 0 && s.hidden <= MAX_H && io && s.n_experts <= MAX_E && s.top_k <= MAX_K &&
-           L->gate_type == BREAD_QTYPE_Q4_K && L->up_type == BREAD_QTYPE_Q4_K && L->down_type == BREAD_QTYPE_Q6_K &&
-           L->gate_shexp_type == BREAD_QTYPE_Q4_K && L->up_shexp_type == BREAD_QTYPE_Q4_K &&
-           L->down_shexp_type == BREAD_QTYPE_Q6_K && (((uintptr_t)L->down_exps | (uintptr_t)L->down_shexp |
-                                                       L->down_expert_bytes) & 15) == 0;
+           bread_standard_qtypes(L) &&
+           (((uintptr_t)L->down_exps | (uintptr_t)L->down_shexp | L->down_expert_bytes) & 15) == 0;
 }
 
 int bread_small_max_tokens()

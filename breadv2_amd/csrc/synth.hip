@@ -183,6 +183,34 @@ extern "C" int bread_synth_normal_f16(uint16_t *dst, uint64_t n, uint64_t seed, 
 // Arena
 // ---------------------------------------------------------------------------
 
+bread_arena_layout bread_arena_plan(const bread_moe_shape_t &s, const int types[6])
+{
+    bread_arena_layout p{};
+    for (int i = 0; i < 6; i++) p.types[i] = types[i];
+    const uint64_t H = s.hidden, I = s.expert_inter, Ish = s.shared_inter, E = s.n_experts;
+    p.gate_expert_bytes = I * bread_expert_row_bytes(types[0], (int)H);
+    p.up_expert_bytes = I * bread_expert_row_bytes(types[1], (int)H);
+    p.down_expert_bytes = H * bread_expert_row_bytes(types[2], (int)I);
+    uint64_t o = 0;
+    p.off_gate = o; o = align256(o + E * p.gate_expert_bytes);
+    p.off_up = o; o = align256(o + E * p.up_expert_bytes);
+    p.off_down = o; o = align256(o + E * p.down_expert_bytes);
+    p.off_gate_sh = o; o = align256(o + Ish * bread_expert_row_bytes(types[3], (int)H));
+    p.off_up_sh = o; o = align256(o + Ish * bread_expert_row_bytes(types[4], (int)H));
+    p.off_down_sh = o; o = align256(o + H * bread_expert_row_bytes(types[5], (int)Ish));
+    p.off_router = o; o = align256(o + E * H * 4);
+    p.off_shgate = o; o = align256(o + H * 2);
+    p.off_norm = o; o = align256(o + H * 4);
+    p.layer_bytes = o;
+    return p;
+}
+
+namespace {
+// the reference GPU path's mix (one_layer.cu:1966-1977)
+constexpr int STANDARD_TYPES[6] = {BREAD_QTYPE_Q4_K, BREAD_QTYPE_Q4_K, BREAD_QTYPE_Q6_K,
+                                   BREAD_QTYPE_Q4_K, BREAD_QTYPE_Q4_K, BREAD_QTYPE_Q6_K};
+}  // namespace
+
 extern "C" int bread_arena_create(const bread_moe_shape_t *s, int n_layers, bread_arena_t **out)
 {
     BREAD_REQUIRE(s && out && n_layers > 0, BREAD_ERR_ARG, "NULL shape/out or n_layers <= 0");
@@ -194,27 +222,17 @@ extern "C" int bread_arena_create(const bread_moe_shape_t *s, int n_layers, brea
     BREAD_REQUIRE(a, BREAD_ERR_NOMEM, "host allocation");
     a->shape = *s;
     a->n_layers = n_layers;
-    const uint64_t H = s->hidden, I = s->expert_inter, Ish = s->shared_inter, E = s->n_experts;
-    a->gate_expert_bytes = I * (H / QK) * Q4K_BYTES;
-    a->up_expert_bytes = a->gate_expert_bytes;
-    a->down_expert_bytes = H * (I / QK) * Q6K_BYTES;
-    uint64_t o = 0;
-    a->off_gate = o; o = align256(o + E * a->gate_expert_bytes);
-    a->off_up = o; o = align256(o + E * a->up_expert_bytes);
-    a->off_down = o; o = align256(o + E * a->down_expert_bytes);
-    a->off_gate_sh = o; o = align256(o + Ish * (H / QK) * Q4K_BYTES);
-    a->off_up_sh = o; o = align256(o + Ish * (H / QK) * Q4K_BYTES);
-    a->off_down_sh = o; o = align256(o + H * (Ish / QK) * Q6K_BYTES);
-    a->off_router = o; o = align256(o + E * H * 4);
-    a->off_shgate = o; o = align256(o + H * 2);
-    a->off_norm = o; o = align256(o + H * 4);
-    a->layer_bytes = o;
+    a->lay = (bread_arena_layout *)calloc((size_t)n_layers, sizeof(bread_arena_layout));
     a->layers = (uint8_t **)calloc((size_t)n_layers, sizeof(uint8_t *));
     a->flags = (int *)calloc((size_t)n_layers, sizeof(int));
     hipError_t e = hipGetDevice(&a->device);
-    if (!a->layers || !a->flags) e = hipErrorOutOfMemory;
-    for (int l = 0; l < n_layers && a->flags; l++) a->flags[l] = BREAD_ARENA_HAS_SHGATE;
-    for (int l = 0; l < n_layers && e == hipSuccess; l++) e = hipMalloc((void **)&a->layers[l], a->layer_bytes);
+    if (!a->lay || !a->layers || !a->flags) e = hipErrorOutOfMemory;
+    const bread_arena_layout std_lay = bread_arena_plan(*s, STANDARD_TYPES);
+    for (int l = 0; l < n_layers && e == hipSuccess; l++) {
+        a->lay[l] = std_lay;
+        a->flags[l] = BREAD_ARENA_HAS_SHGATE;
+        e = hipMalloc((void **)&a->layers[l], std_lay.layer_bytes);
+    }
     if (e != hipSuccess) {
         bread_arena_destroy(a);
         return bread_fail(e == hipErrorOutOfMemory ? BREAD_ERR_NOMEM : BREAD_ERR_HIP, "bread_arena_create",
@@ -231,13 +249,48 @@ extern "C" int bread_arena_destroy(bread_arena_t *a)
         for (int l = 0; l < a->n_layers; l++) (void)hipFree(a->layers[l]);
     free(a->layers);
     free(a->flags);
+    free(a->lay);
     free(a);
     return BREAD_OK;
 }
 
+int bread_arena_relayout(bread_arena_t *a, int l, const int types[6])
+{
+    bool same = true;
+    for (int i = 0; i < 6; i++) same = same && a->lay[l].types[i] == types[i];
+    if (same) return BREAD_OK;
+    const bread_arena_layout p = bread_arena_plan(a->shape, types);
+    if (p.layer_bytes != a->lay[l].layer_bytes) {
+        uint8_t *nb = nullptr;
+        const hipError_t e = hipMalloc((void **)&nb, p.layer_bytes);
+        if (e != hipSuccess)
+            return bread_fail(e == hipErrorOutOfMemory ? BREAD_ERR_NOMEM : BREAD_ERR_HIP, "bread_arena_relayout",
+                              hipGetErrorString(e));
+        BREAD_HIP(hipDeviceSynchronize());  // no launch may still read the old block
+        BREAD_HIP(hipFree(a->layers[l]));
+        a->layers[l] = nb;
+    }
+    a->lay[l] = p;
+    return BREAD_OK;
+}
+
+extern "C" int bread_arena_set_layer_types(bread_arena_t *a, int layer, int gate_type, int up_type, int down_type,
+                                           int gate_shexp_type, int up_shexp_type, int down_shexp_type)
+{
+    BREAD_REQUIRE(a, BREAD_ERR_ARG, "NULL arena");
+    BREAD_REQUIRE(layer >= 0 && layer < a->n_layers, BREAD_ERR_ARG, "layer out of range");
+    const int types[6] = {gate_type, up_type, down_type, gate_shexp_type, up_shexp_type, down_shexp_type};
+    for (int i = 0; i < 6; i++)
+        BREAD_REQUIRE(bread_expert_qtype(types[i]), BREAD_ERR_QTYPE, "expert tensors must be Q4_K or Q6_K");
+    return bread_arena_relayout(a, layer, types);
+}
+
 extern "C" uint64_t bread_arena_layer_bytes(const bread_arena_t *a)
 {
-    return a ? a->layer_bytes : 0;
+    if (!a) return 0;
+    uint64_t m = 0;
+    for (int l = 0; l < a->n_layers; l++) m = a->lay[l].layer_bytes > m ? a->lay[l].layer_bytes : m;
+    return m;
 }
 
 extern "C" int bread_arena_layer(const bread_arena_t *a, int layer, bread_moe_layer_t *L)
@@ -245,21 +298,24 @@ extern "C" int bread_arena_layer(const bread_arena_t *a, int layer, bread_moe_la
     BREAD_REQUIRE(a && L, BREAD_ERR_ARG, "NULL arena or descriptor");
     BREAD_REQUIRE(layer >= 0 && layer < a->n_layers, BREAD_ERR_ARG, "layer out of range");
     uint8_t *b = a->layers[layer];
-    L->gate_exps = b + a->off_gate;
-    L->up_exps = b + a->off_up;
-    L->down_exps = b + a->off_down;
-    L->gate_expert_bytes = a->gate_expert_bytes;
-    L->up_expert_bytes = a->up_expert_bytes;
-    L->down_expert_bytes = a->down_expert_bytes;
-    L->gate_type = L->up_type = BREAD_QTYPE_Q4_K;
-    L->down_type = BREAD_QTYPE_Q6_K;
-    L->gate_shexp = b + a->off_gate_sh;
-    L->up_shexp = b + a->off_up_sh;
-    L->down_shexp = b + a->off_down_sh;
-    L->gate_shexp_type = L->up_shexp_type = BREAD_QTYPE_Q4_K;
-    L->down_shexp_type = BREAD_QTYPE_Q6_K;
-    L->router = (const float *)(b + a->off_router);
-    L->shexp_gate = (a->flags[layer] & BREAD_ARENA_HAS_SHGATE) ? (const uint16_t *)(b + a->off_shgate) : nullptr;
-    L->post_norm_w = (a->flags[layer] & BREAD_ARENA_HAS_NORM) ? (const float *)(b + a->off_norm) : nullptr;
+    const bread_arena_layout &p = a->lay[layer];
+    L->gate_exps = b + p.off_gate;
+    L->up_exps = b + p.off_up;
+    L->down_exps = b + p.off_down;
+    L->gate_expert_bytes = p.gate_expert_bytes;
+    L->up_expert_bytes = p.up_expert_bytes;
+    L->down_expert_bytes = p.down_expert_bytes;
+    L->gate_type = p.types[0];
+    L->up_type = p.types[1];
+    L->down_type = p.types[2];
+    L->gate_shexp = b + p.off_gate_sh;
+    L->up_shexp = b + p.off_up_sh;
+    L->down_shexp = b + p.off_down_sh;
+    L->gate_shexp_type = p.types[3];
+    L->up_shexp_type = p.types[4];
+    L->down_shexp_type = p.types[5];
+    L->router = (const float *)(b + p.off_router);
+    L->shexp_gate = (a->flags[layer] & BREAD_ARENA_HAS_SHGATE) ? (const uint16_t *)(b + p.off_shgate) : nullptr;
+    L->post_norm_w = (a->flags[layer] & BREAD_ARENA_HAS_NORM) ? (const float *)(b + p.off_norm) : nullptr;
     return BREAD_OK;
 }

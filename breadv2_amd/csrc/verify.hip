@@ -98,6 +98,40 @@ __global__ __launch_bounds__(AM_THREADS) void k_argmax_f16(const uint16_t *__res
 
 }  // namespace
 
+// One token through layers[0..n): each run of consecutive layers with the
+// decode kernel's weight types is one persistent launch; any other layer
+// (another mix of Q4_K and Q6_K) is the RMSNorm kernel followed by the
+// per-token kernels.  Routing outputs go to record l * rstride of layer l,
+// as in bread_launch_decode_layers.
+int bread_launch_decode_runs(bread_moe_ctx_t *c, const bread_moe_layer_t *layers, int n, float *hidden,
+                             int32_t *idx, float *w, float *gsh, hipStream_t st, int rstride)
+{
+    const int H = c->shape.hidden, K = c->shape.top_k;
+    for (int l = 0; l < n;) {
+        const size_t r = (size_t)l * rstride;
+        if (bread_standard_qtypes(&layers[l])) {
+            int m = l + 1;
+            while (m < n && bread_standard_qtypes(&layers[m])) m++;
+            const int rc = bread_launch_decode_layers(c, layers + l, m - l, hidden, idx ? idx + r * K : nullptr,
+                                                      w ? w + r * K : nullptr, gsh ? gsh + r : nullptr, st, rstride);
+            if (rc) return rc;
+            l = m;
+            continue;
+        }
+        bread_clear_stale_error();
+        hipLaunchKernelGGL(k_norm_rows<float>, dim3(1), dim3(256), 0, st, hidden, layers[l].post_norm_w, c->x32, H,
+                           c->shape.rms_eps);
+        BREAD_HIP(hipGetLastError());
+        const int rc = bread_launch_moe_multi(c, &layers[l], c->x32, hidden, 1, st);
+        if (rc) return rc;
+        if (idx) BREAD_HIP(hipMemcpyAsync(idx + r * K, c->idx, K * sizeof(int32_t), hipMemcpyDeviceToDevice, st));
+        if (w) BREAD_HIP(hipMemcpyAsync(w + r * K, c->w, K * sizeof(float), hipMemcpyDeviceToDevice, st));
+        if (gsh) BREAD_HIP(hipMemcpyAsync(gsh + r, c->gsh, sizeof(float), hipMemcpyDeviceToDevice, st));
+        l++;
+    }
+    return BREAD_OK;
+}
+
 extern "C" int bread_moe_stack_forward(bread_moe_ctx_t *c, const bread_moe_layer_t *layers, int n, float *hidden,
                                        int T, int32_t *idx, float *w, float *gsh, bread_stream_t stream)
 {
@@ -123,8 +157,8 @@ extern "C" int bread_moe_stack_forward(bread_moe_ctx_t *c, const bread_moe_layer
             c->last_stream = st;
             int rc = BREAD_OK;
             for (int t = 0; t < T && rc == BREAD_OK; t++)
-                rc = bread_launch_decode_layers(c, layers, n, hidden + (size_t)t * H, idx ? idx + (size_t)t * K : nullptr,
-                                                w ? w + (size_t)t * K : nullptr, gsh ? gsh + t : nullptr, st, T);
+                rc = bread_launch_decode_runs(c, layers, n, hidden + (size_t)t * H, idx ? idx + (size_t)t * K : nullptr,
+                                              w ? w + (size_t)t * K : nullptr, gsh ? gsh + t : nullptr, st, T);
             if (rc != BREAD_ERR_SHAPE || c->path == BREAD_PATH_DECODE) return rc;
             bread_clear_stale_error();
         }

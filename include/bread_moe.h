@@ -119,10 +119,15 @@ void bread_moe_shape_default(bread_moe_shape_t *shape);
  * GGUF layout the reference slices (loader.h:35-47, loader.c:187-190); the
  * shared expert and router mirror wc_layer_t (loader.h:86-109) and the
  * tensors route_layer reads (one_layer.cu:964-980).
- * Supported types on the device path: gate/up Q4_K, down Q6_K (the qtypes the
- * reference GPU path hardcodes, one_layer.cu:1966-1977); router F32 [E][H];
- * shexp_gate F16 [H] or NULL (NULL means a zero logit, sigmoid 0.5, as when
- * the reference finds no tensor, one_layer.cu:974-976). */
+ * Types: each of the six expert tensors is BREAD_QTYPE_Q4_K or BREAD_QTYPE_Q6_K,
+ * given per tensor as the reference records them (loader.c:191-193) and as its
+ * fp32 path dispatches on them (one_layer.cu:1465-1468, layer_ops.cu:169-189).
+ * Q4_K tensors and expert strides are 16-byte aligned, Q6_K ones 4-byte
+ * aligned.  The decode, small-batch and grouped kernels take the mix the
+ * reference GPU path hardcodes (gate/up Q4_K, down Q6_K, routed and shared,
+ * one_layer.cu:1966-1977); any other mix runs on the per-token kernels.
+ * router F32 [E][H]; shexp_gate F16 [H] or NULL (NULL means a zero logit,
+ * sigmoid 0.5, as when the reference finds no tensor, one_layer.cu:974-976). */
 typedef struct {
     const void *gate_exps;
     const void *up_exps;
@@ -247,7 +252,9 @@ int bread_route_layer_f16(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer, 
  * it, fp32; H <= 2048, intermediate sizes 256 or 512); larger batches run the
  * grouped path (tokens bucketed by expert, expert GEMMs on the matrix cores
  * with fp16 operands and fp32 accumulation; intermediate sizes <= 512 and
- * 16-byte aligned Q6_K down weights); other shapes run the per-token path. */
+ * 16-byte aligned Q6_K down weights); other shapes and weight-type mixes run
+ * the per-token path.  A pinned path that cannot take the layer's weight
+ * types returns BREAD_ERR_QTYPE. */
 int bread_moe_forward(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer,
                       const float *d_x_normed, float *d_hidden, int n_tokens,
                       int32_t *d_idx, float *d_w, float *d_gsh, bread_stream_t stream);
@@ -320,6 +327,9 @@ int bread_spec_accept(const int32_t *pred, const int32_t *draft, int n_draft, in
  * shared-gate logits); NULL skips them.  Needs the shape the persistent
  * kernel is built for (H 2048, I = I_sh = 512, E <= 256, K <= 8), 16-byte
  * aligned weights and n_layers <= 256; returns BREAD_ERR_SHAPE otherwise.
+ * Layers with another weight-type mix than the kernel's (see
+ * bread_moe_layer_t) split the stack: each run of the kernel's layers is one
+ * launch, each other layer the RMSNorm and per-token kernels.
  * For n_layers > 1 the host layer array is copied into the context; a
  * different array than the previous call's costs one synchronous upload.
  * The kernel runs one 1024-thread workgroup per CU and every workgroup waits
@@ -363,8 +373,15 @@ int bread_arena_destroy(bread_arena_t *arena);
  * and post_norm_w are NULL when the layer holds no such tensor (a layer
  * loaded from a file without them). */
 int bread_arena_layer(const bread_arena_t *arena, int layer, bread_moe_layer_t *out);
-/* Bytes of one layer's allocation. */
+/* Bytes of the largest layer allocation. */
 uint64_t bread_arena_layer_bytes(const bread_arena_t *arena);
+/* Weight types of layer `layer` (each BREAD_QTYPE_Q4_K or BREAD_QTYPE_Q6_K;
+ * a new arena's layers are Q4_K, Q4_K, Q6_K for gate, up, down, routed and
+ * shared).  A change re-lays out the layer and reallocates it when its size
+ * changes (synchronous); its contents are then undefined until written.
+ * The reference keeps each tensor's type per layer (loader.c:191-193). */
+int bread_arena_set_layer_types(bread_arena_t *arena, int layer, int gate_type, int up_type, int down_type,
+                                int gate_shexp_type, int up_shexp_type, int down_shexp_type);
 
 /* ------------------------------------------------------------------ */
 /* GGUF model files                                                    */
@@ -415,12 +432,14 @@ uint64_t bread_ggml_type_size(uint32_t type, uint64_t n_elems);
 int bread_gguf_moe_shape(const bread_gguf_t *file, int layer, bread_moe_shape_t *shape);
 
 /* Copies block `gguf_layer`'s MoE tensors into arena layer `arena_layer`:
- * blk.N.ffn_{gate,up,down}_exps (Q4_K, Q4_K, Q6_K; experts at stride
- * tensor.size / n_experts, loader.c:188-190), ffn_{gate,up,down}_shexp,
- * ffn_gate_inp (F32 router) and, when present, ffn_gate_inp_shexp (F16) and
- * post_attention_norm (F32), which bread_arena_layer then exposes as
- * shexp_gate and post_norm_w.  Types and dimensions must match the arena's
- * shape (BREAD_ERR_QTYPE / BREAD_ERR_SHAPE).  Synchronous. */
+ * blk.N.ffn_{gate,up,down}_exps (each Q4_K or Q6_K; experts at stride
+ * tensor.size / n_experts, loader.c:188-190), ffn_{gate,up,down}_shexp (each
+ * Q4_K or Q6_K), ffn_gate_inp (F32 router) and, when present,
+ * ffn_gate_inp_shexp (F16) and post_attention_norm (F32), which
+ * bread_arena_layer then exposes as shexp_gate and post_norm_w.  The arena
+ * layer takes the file's expert types (bread_arena_set_layer_types).  Other
+ * types return BREAD_ERR_QTYPE, dimensions other than the arena's shape
+ * BREAD_ERR_SHAPE.  Synchronous. */
 int bread_arena_load_gguf(bread_arena_t *arena, int arena_layer, const bread_gguf_t *file, int gguf_layer);
 
 /* ------------------------------------------------------------------ */

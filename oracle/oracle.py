@@ -168,19 +168,23 @@ def sigmoid(x: float) -> float:
 class HostLayer:
     """A layer's weights on the host (numpy), native GGUF layout."""
 
-    def __init__(self, shape: OShape, gate_exps, up_exps, down_exps, gate_sh, up_sh, down_sh, router, shgate):
+    def __init__(self, shape: OShape, gate_exps, up_exps, down_exps, gate_sh, up_sh, down_sh, router, shgate,
+                 types=(QTYPE_Q4_K, QTYPE_Q4_K, QTYPE_Q6_K, QTYPE_Q4_K, QTYPE_Q4_K, QTYPE_Q6_K)):
+        """types: gate, up, down, gate_shexp, up_shexp, down_shexp (each Q4_K
+        or Q6_K), as the reference records per tensor (loader.c:191-193)."""
         self.shape = shape
+        self.types = tuple(int(t) for t in types)
         self.arrays = [np.ascontiguousarray(a) for a in (gate_exps, up_exps, down_exps, gate_sh, up_sh, down_sh)]
         self.router = np.ascontiguousarray(router, np.float32)
         self.shgate = None if shgate is None else np.ascontiguousarray(shgate, np.uint16)
         H, I = shape.hidden, shape.expert_inter
-        ge = I * (H // 256) * 144
-        de = H * (I // 256) * 210
+        tg, tu, td, tgs, tus, tds = self.types
         g, u, d, gs, us, ds = self.arrays
-        self.desc = OLayer(g.ctypes.data, u.ctypes.data, d.ctypes.data, ge, ge, de,
-                           QTYPE_Q4_K, QTYPE_Q4_K, QTYPE_Q6_K,
+        self.desc = OLayer(g.ctypes.data, u.ctypes.data, d.ctypes.data,
+                           I * row_bytes(tg, H), I * row_bytes(tu, H), H * row_bytes(td, I),
+                           tg, tu, td,
                            gs.ctypes.data, us.ctypes.data, ds.ctypes.data,
-                           QTYPE_Q4_K, QTYPE_Q4_K, QTYPE_Q6_K,
+                           tgs, tus, tds,
                            self.router.ctypes.data, None if self.shgate is None else self.shgate.ctypes.data)
 
 

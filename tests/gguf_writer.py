@@ -69,19 +69,27 @@ def write_gguf(path: str, kvs: list, tensors: list, version: int = 3, alignment:
     return {"offsets": offsets, "data_offset": data_off}
 
 
-def moe_layer_tensors(layer: int, H: int, I: int, Ish: int, E: int, seed: int, with_shgate=True, with_norm=True):
+def moe_layer_tensors(layer: int, H: int, I: int, Ish: int, E: int, seed: int, with_shgate=True, with_norm=True,
+                      types=None):
     """The MoE tensors of block `layer` (names of loader.c:162-164,
-    :559-569 and one_layer.cu:964-975, :1413), synthetic values."""
+    :559-569 and one_layer.cu:964-975, :1413), synthetic values.  types:
+    ggml types of gate, up, down, gate_shexp, up_shexp, down_shexp (each
+    Q4_K or Q6_K; default Q4_K, Q4_K, Q6_K for both)."""
     from breadv2_amd import synth
+
+    tg, tu, td, tgs, tus, tds = types or (GGML_Q4_K, GGML_Q4_K, GGML_Q6_K, GGML_Q4_K, GGML_Q4_K, GGML_Q6_K)
+
+    def q(qtype, n_blocks, sd):
+        return synth.synth_q4k(n_blocks, sd) if qtype == GGML_Q4_K else synth.synth_q6k(n_blocks, sd)
 
     rng = np.random.default_rng(seed)
     t = [
-        (f"blk.{layer}.ffn_gate_exps.weight", GGML_Q4_K, [H, I, E], synth.synth_q4k(E * I * H // 256, seed + 1)),
-        (f"blk.{layer}.ffn_up_exps.weight", GGML_Q4_K, [H, I, E], synth.synth_q4k(E * I * H // 256, seed + 2)),
-        (f"blk.{layer}.ffn_down_exps.weight", GGML_Q6_K, [I, H, E], synth.synth_q6k(E * H * I // 256, seed + 3)),
-        (f"blk.{layer}.ffn_gate_shexp.weight", GGML_Q4_K, [H, Ish], synth.synth_q4k(Ish * H // 256, seed + 4)),
-        (f"blk.{layer}.ffn_up_shexp.weight", GGML_Q4_K, [H, Ish], synth.synth_q4k(Ish * H // 256, seed + 5)),
-        (f"blk.{layer}.ffn_down_shexp.weight", GGML_Q6_K, [Ish, H], synth.synth_q6k(H * Ish // 256, seed + 6)),
+        (f"blk.{layer}.ffn_gate_exps.weight", tg, [H, I, E], q(tg, E * I * H // 256, seed + 1)),
+        (f"blk.{layer}.ffn_up_exps.weight", tu, [H, I, E], q(tu, E * I * H // 256, seed + 2)),
+        (f"blk.{layer}.ffn_down_exps.weight", td, [I, H, E], q(td, E * H * I // 256, seed + 3)),
+        (f"blk.{layer}.ffn_gate_shexp.weight", tgs, [H, Ish], q(tgs, Ish * H // 256, seed + 4)),
+        (f"blk.{layer}.ffn_up_shexp.weight", tus, [H, Ish], q(tus, Ish * H // 256, seed + 5)),
+        (f"blk.{layer}.ffn_down_shexp.weight", tds, [Ish, H], q(tds, H * Ish // 256, seed + 6)),
         (f"blk.{layer}.ffn_gate_inp.weight", GGML_F32, [H, E],
          (0.02 * rng.standard_normal(E * H)).astype(np.float32).view(np.uint8)),
     ]

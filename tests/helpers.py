@@ -18,7 +18,7 @@ def host_layer(t, drop_shgate: bool = False) -> "O.HostLayer":
         oshape(t.shape),
         t.gate_exps.cpu().numpy(), t.up_exps.cpu().numpy(), t.down_exps.cpu().numpy(),
         t.gate_sh.cpu().numpy(), t.up_sh.cpu().numpy(), t.down_sh.cpu().numpy(),
-        t.router.cpu().numpy(), sh,
+        t.router.cpu().numpy(), sh, types=t.types,
     )
 
 
@@ -57,14 +57,17 @@ def arena_host_layer(s, d) -> "O.HostLayer":
     """Host copy (for the oracle) of one arena layer descriptor."""
     from breadv2_amd import api
 
-    b = api.shape_bytes(s)
+    types = api.layer_types(d)
+    b = api.shape_bytes(s, types)
     E = s.n_experts
     return O.HostLayer(
         oshape(s),
         d2h(d.gate_exps, E * b["gate_expert"]), d2h(d.up_exps, E * b["up_expert"]),
         d2h(d.down_exps, E * b["down_expert"]), d2h(d.gate_shexp, b["gate_sh"]),
         d2h(d.up_shexp, b["up_sh"]), d2h(d.down_shexp, b["down_sh"]),
-        d2h(d.router, b["router"]).view(np.float32), d2h(d.shexp_gate, b["shgate"]).view(np.uint16),
+        d2h(d.router, b["router"]).view(np.float32),
+        d2h(d.shexp_gate, b["shgate"]).view(np.uint16) if d.shexp_gate else None,
+        types=types,
     )
 
 

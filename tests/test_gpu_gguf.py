@@ -27,11 +27,13 @@ DEV = "cuda:0"
 
 def host_from_tensors(s, tensors, layer):
     by = {n.split(".", 2)[2]: d for n, _, _, d in tensors if n.startswith(f"blk.{layer}.")}
+    ty = {n.split(".", 2)[2]: t for n, t, _, _ in tensors if n.startswith(f"blk.{layer}.")}
+    names = ["ffn_gate_exps", "ffn_up_exps", "ffn_down_exps", "ffn_gate_shexp", "ffn_up_shexp", "ffn_down_shexp"]
     sg = by.get("ffn_gate_inp_shexp.weight")
-    return O.HostLayer(oshape(s), by["ffn_gate_exps.weight"], by["ffn_up_exps.weight"], by["ffn_down_exps.weight"],
-                       by["ffn_gate_shexp.weight"], by["ffn_up_shexp.weight"], by["ffn_down_shexp.weight"],
+    return O.HostLayer(oshape(s), *[by[f"{n}.weight"] for n in names],
                        np.asarray(by["ffn_gate_inp.weight"]).view(np.float32),
-                       None if sg is None else np.asarray(sg).view(np.uint16))
+                       None if sg is None else np.asarray(sg).view(np.uint16),
+                       types=[ty[f"{n}.weight"] for n in names])
 
 
 def forward(s, d, x, hidden, path):
