@@ -7,14 +7,11 @@
 // each product rounded to fp32, then added, never fused (one_layer.cu:969-971),
 // and the shared-gate score the same way with the fp16 gate widened
 // (one_layer.cu:977-980).  The sum is inherently sequential, so the kernel
-// gives each lane one token and each wave one router row: a lane's 2048
-// dependent adds (~5.5 ns each on gfx950 with the interleaved products, so
-// ~11 us for a 2048-column row: the latency floor of exact routing) run
-// while the 64 tokens of a wave and the rows of the grid run in parallel.  The row is read with scalar
-// loads (one value for the whole wave); the tokens' activations are staged
-// through LDS in chunks of 128 columns, double-buffered, a padded row per
-// token so a lane's 16-byte reads fall in distinct banks.
-//
+// gives each lane one token and each wave one router row (two beyond 64
+// tokens per CU): a lane's 2048 dependent (product, add) pairs are the
+// latency floor of exact routing, and route_seq.h keeps every other cost
+// (activation staging, router weights by DPP broadcast) off that chain.
+
 // k_topk_exact then runs softmax / top-k / renormalisation per token (one
 // wave) with the host's arithmetic (softmax_keys_exact): given identical
 // logits, indices and weights are bit-identical to the reference's.
@@ -92,7 +89,7 @@ __global__ __launch_bounds__(WAVE) void k_topk_exact(const float *__restrict__ l
 int bread_route_rows_per_wave(int T, int E)
 {
     const int tiles = (T + RS_TT - 1) / RS_TT;
-    return (size_t)tiles * ((E + RS_WAVES - 1) / RS_WAVES) <= 256 ? 1 : 2;
+    return E < 2 || (size_t)tiles * ((E + RS_WAVES - 1) / RS_WAVES) <= 256 ? 1 : 2;
 }
 
 int bread_launch_route_logits(const float *router, const uint16_t *shg, const float *x, float *logits, float *gsh,
