@@ -121,6 +121,8 @@ SIGNATURES = {
     "bread_moe_ctx_create": (c_int, [POINTER(MoeShape), c_int, POINTER(c_void_p)]),
     "bread_moe_ctx_destroy": (c_int, [c_void_p]),
     "bread_moe_ctx_check": (c_int, [c_void_p, POINTER(c_int)]),
+    "bread_moe_expert_block": (c_int, [c_void_p, POINTER(MoeLayer), c_void_p, c_void_p, c_int, c_void_p, c_void_p,
+                                       c_void_p]),
     "bread_route": (c_int, [c_void_p, POINTER(MoeLayer), c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
     "bread_route_noalloc": (
         c_int,

@@ -457,6 +457,14 @@ class MoeContext:
                                     _p(gsh), _s(stream)), "bread_moe_forward")
         return idx, w, gsh
 
+    def expert_block(self, layer: MoeLayer, x: torch.Tensor, hidden: torch.Tensor, n_tokens: int,
+                     idx: torch.Tensor, w: torch.Tensor, stream=None) -> None:
+        """bread_moe_expert_block: hidden += sum_k w[t][k] * expert_{idx[t][k]}(x_t),
+        routed experts only, with the caller's routing (device int32 / fp32 [n_tokens][K])."""
+        assert idx.dtype == torch.int32 and w.dtype == torch.float32
+        check(lib.bread_moe_expert_block(self._h, ctypes.byref(layer), _p(x), _p(hidden), n_tokens, _p(idx),
+                                         _p(w), _s(stream)), "bread_moe_expert_block")
+
     def forward_f16(self, layer: MoeLayer, hidden: torch.Tensor, normed: torch.Tensor, n_tokens: int,
                     norm_w=None, want_routing: bool = False, stream=None):
         """bread_moe_forward_f16: the MoE block on fp16 hidden / normed

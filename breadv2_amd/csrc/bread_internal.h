@@ -49,6 +49,7 @@ enum : uint32_t {
     BREAD_DEV_ERR_RANGE = 4u,   // grouped: a weight superblock's values exceed fp16's range
     BREAD_DEV_ERR_PAIR = 8u,    // small batch: a wait on the partner wave ran out
     BREAD_DEV_ERR_LOCAL = 16u,  // decode: a wait on another wave of the workgroup ran out
+    BREAD_DEV_ERR_INDEX = 32u,  // expert block: a caller's expert index outside [0, n_experts)
 };
 
 // Device-side status of the persistent decode kernel.

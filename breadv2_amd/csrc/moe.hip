@@ -242,12 +242,23 @@ __device__ __forceinline__ float kq_row_partial(int type, const uint8_t *row, in
     return type == BREAD_QTYPE_Q4_K ? q4k_row_partial(row, nb, x, lane) : q6k_row_partial(row, nb, x, lane);
 }
 
+// Expert of an index the caller handed in: clamped to [0, E) so that no
+// load leaves the tensor, with BREAD_DEV_ERR_INDEX set when it was outside.
+__device__ __forceinline__ int checked_expert(int e, int E, uint32_t *err)
+{
+    if (e >= 0 && e < E) return e;
+    __hip_atomic_fetch_or(err, BREAD_DEV_ERR_INDEX, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return e < 0 ? 0 : E - 1;
+}
+
 // One wave per (token, slot, row): gate and up rows, then SwiGLU.  Each
 // tensor has its own type (Q4_K or Q6_K), as in the reference's
-// cpu_tensor_matvec dispatch (one_layer.cu:1465-1468).
+// cpu_tensor_matvec dispatch (one_layer.cu:1465-1468).  Slot 0 (the shared
+// expert) only when `shared`.
 __global__ __launch_bounds__(256) void k_gateup(bread_moe_layer_t L, const float *__restrict__ x,
                                                 const int32_t *__restrict__ idx, float *__restrict__ h, int H,
-                                                int I, int Ish, int K, int T)
+                                                int I, int Ish, int K, int T, int E, int shared,
+                                                uint32_t *__restrict__ err)
 {
     const int Imax = I > Ish ? I : Ish;
     const int64_t v = (int64_t)((blockIdx.x * (uint64_t)blockDim.x + threadIdx.x) / WAVE);
@@ -256,7 +267,7 @@ __global__ __launch_bounds__(256) void k_gateup(bread_moe_layer_t L, const float
     const int t = (int)(v / per_tok);
     const int slot = (int)((v % per_tok) / Imax);
     const int r = (int)(v % Imax);
-    if (r >= (slot ? I : Ish)) return;
+    if (r >= (slot ? I : Ish) || (slot == 0 && !shared)) return;
     const uint8_t *g, *u;
     int gt, ut;
     if (slot == 0) {
@@ -265,7 +276,7 @@ __global__ __launch_bounds__(256) void k_gateup(bread_moe_layer_t L, const float
         gt = L.gate_shexp_type;
         ut = L.up_shexp_type;
     } else {
-        const int e = idx[(size_t)t * K + slot - 1];
+        const int e = checked_expert(idx[(size_t)t * K + slot - 1], E, err);
         g = (const uint8_t *)L.gate_exps + (uint64_t)e * L.gate_expert_bytes;
         u = (const uint8_t *)L.up_exps + (uint64_t)e * L.up_expert_bytes;
         gt = L.gate_type;
@@ -279,11 +290,13 @@ __global__ __launch_bounds__(256) void k_gateup(bread_moe_layer_t L, const float
 }
 
 // One wave per (token, output row): down rows of every slot, combined in the
-// reference order (one_layer.cu:1447-1469).
+// reference order (one_layer.cu:1447-1469): the shared expert (when
+// `shared`), then the routed experts by rank.
 __global__ __launch_bounds__(256) void k_down(bread_moe_layer_t L, const int32_t *__restrict__ idx,
                                               const float *__restrict__ w, const float *__restrict__ gsh,
                                               const float *__restrict__ h, float *__restrict__ hidden, int H,
-                                              int I, int Ish, int K, int T)
+                                              int I, int Ish, int K, int T, int E, int shared,
+                                              uint32_t *__restrict__ err)
 {
     const int Imax = I > Ish ? I : Ish;
     const int64_t v = (int64_t)((blockIdx.x * (uint64_t)blockDim.x + threadIdx.x) / WAVE);
@@ -293,13 +306,15 @@ __global__ __launch_bounds__(256) void k_down(bread_moe_layer_t L, const int32_t
     const int lane = lane_id();
     const float *ht = h + (size_t)t * (K + 1) * Imax;
     const int st = L.down_shexp_type, dt = L.down_type;
-    const float sh = wave_sum(kq_row_partial(
-        st, (const uint8_t *)L.down_shexp + (uint64_t)r * bread_expert_row_bytes(st, Ish), Ish / QK, ht, lane));
     float acc = hidden[(size_t)t * H + r];
-    acc += sigmoidf_ref(gsh[t]) * sh;
+    if (shared) {
+        const float sh = wave_sum(kq_row_partial(
+            st, (const uint8_t *)L.down_shexp + (uint64_t)r * bread_expert_row_bytes(st, Ish), Ish / QK, ht, lane));
+        acc += sigmoidf_ref(gsh[t]) * sh;
+    }
     const uint64_t rb = bread_expert_row_bytes(dt, I);
     for (int k = 0; k < K; k++) {
-        const int e = idx[(size_t)t * K + k];
+        const int e = checked_expert(idx[(size_t)t * K + k], E, err);
         const uint8_t *d = (const uint8_t *)L.down_exps + (uint64_t)e * L.down_expert_bytes + r * rb;
         const float eo = wave_sum(kq_row_partial(dt, d, I / QK, ht + (size_t)(k + 1) * Imax, lane));
         acc += w[(size_t)t * K + k] * eo;
@@ -439,11 +454,12 @@ int bread_launch_moe_multi(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const
     const int Imax = s.expert_inter > s.shared_inter ? s.expert_inter : s.shared_inter;
     const uint64_t gu_waves = (uint64_t)T * (s.top_k + 1) * Imax;
     hipLaunchKernelGGL(k_gateup, dim3((unsigned)((gu_waves + 3) / 4)), dim3(256), 0, st, *L, x, c->idx, c->h,
-                       s.hidden, s.expert_inter, s.shared_inter, s.top_k, T);
+                       s.hidden, s.expert_inter, s.shared_inter, s.top_k, T, s.n_experts, 1, &c->dsync->error.v);
     BREAD_HIP(hipGetLastError());
     const uint64_t dn_waves = (uint64_t)T * s.hidden;
     hipLaunchKernelGGL(k_down, dim3((unsigned)((dn_waves + 3) / 4)), dim3(256), 0, st, *L, c->idx, c->w, c->gsh,
-                       c->h, hidden, s.hidden, s.expert_inter, s.shared_inter, s.top_k, T);
+                       c->h, hidden, s.hidden, s.expert_inter, s.shared_inter, s.top_k, T, s.n_experts, 1,
+                       &c->dsync->error.v);
     BREAD_HIP(hipGetLastError());
     return BREAD_OK;
 }
@@ -555,6 +571,34 @@ extern "C" int bread_moe_forward(bread_moe_ctx_t *c, const bread_moe_layer_t *L,
     if (idx) BREAD_HIP(hipMemcpyAsync(idx, c->idx, (size_t)T * K * sizeof(int32_t), hipMemcpyDeviceToDevice, st));
     if (w) BREAD_HIP(hipMemcpyAsync(w, c->w, (size_t)T * K * sizeof(float), hipMemcpyDeviceToDevice, st));
     if (gsh) BREAD_HIP(hipMemcpyAsync(gsh, c->gsh, (size_t)T * sizeof(float), hipMemcpyDeviceToDevice, st));
+    return BREAD_OK;
+}
+
+// The routed experts with the caller's routing (the reference's expert-block
+// harness, expert_bench.cu:123-151, and the routed loop of one_layer.cu:
+// 1455-1470): per-token kernels without the shared slot.
+extern "C" int bread_moe_expert_block(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x,
+                                      float *hidden, int T, const int32_t *idx, const float *w,
+                                      bread_stream_t stream)
+{
+    int rc = check_tokens(c, L, x, T);
+    if (rc) return rc;
+    BREAD_REQUIRE(hidden && idx && w, BREAD_ERR_ARG, "NULL hidden or routing");
+    if (T == 0) return BREAD_OK;
+    const hipStream_t st = to_hip(stream);
+    c->last_stream = st;
+    const bread_moe_shape_t &s = c->shape;
+    const int Imax = s.expert_inter > s.shared_inter ? s.expert_inter : s.shared_inter;
+    bread_clear_stale_error();
+    const uint64_t gu_waves = (uint64_t)T * (s.top_k + 1) * Imax;
+    hipLaunchKernelGGL(k_gateup, dim3((unsigned)((gu_waves + 3) / 4)), dim3(256), 0, st, *L, x, idx, c->h,
+                       s.hidden, s.expert_inter, s.shared_inter, s.top_k, T, s.n_experts, 0, &c->dsync->error.v);
+    BREAD_HIP(hipGetLastError());
+    const uint64_t dn_waves = (uint64_t)T * s.hidden;
+    hipLaunchKernelGGL(k_down, dim3((unsigned)((dn_waves + 3) / 4)), dim3(256), 0, st, *L, idx, w, c->gsh, c->h,
+                       hidden, s.hidden, s.expert_inter, s.shared_inter, s.top_k, T, s.n_experts, 0,
+                       &c->dsync->error.v);
+    BREAD_HIP(hipGetLastError());
     return BREAD_OK;
 }
 

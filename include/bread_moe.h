@@ -192,7 +192,8 @@ int bread_stack_loop_tokens(void);
  * d >= 64 or dmin >= 1024, Q6_K |d*sc| >= 2047), 8 = the small-batch down
  * kernel's wait on a partner wave expired (the workgroup then writes none of
  * its rows of hidden), 16 = a decode workgroup's wait on another of its own
- * waves expired.  Outputs of a launch that set a bit are unspecified.  Clears
+ * waves expired, 32 = bread_moe_expert_block met an expert index outside
+ * [0, n_experts).  Outputs of a launch that set a bit are unspecified.  Clears
  * the word and resets the decode exchange state, so the context is usable
  * again. */
 int bread_moe_ctx_check(bread_moe_ctx_t *ctx, int *device_error);
@@ -258,6 +259,20 @@ int bread_route_layer_f16(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer, 
 int bread_moe_forward(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer,
                       const float *d_x_normed, float *d_hidden, int n_tokens,
                       int32_t *d_idx, float *d_w, float *d_gsh, bread_stream_t stream);
+
+/* The routed experts of the MoE block with the caller's routing:
+ *   hidden[t] += sum_k w[t][k] * expert_{idx[t][k]}(x_t)
+ * in rank order, with no router and no shared expert: the block the
+ * reference's expert benchmark times (bread_benchmark_expert_block,
+ * expert_bench.cu:60-239, experts idx, weights w; its serial GPU loop of
+ * :123-151) and the routed loop of one_layer.cu:1455-1470.  d_x fp32
+ * [n_tokens][H], d_hidden fp32 [n_tokens][H] in/out, d_idx int32 and d_w
+ * fp32 [n_tokens][K] on the device.  Runs the per-token kernels (any mix of
+ * Q4_K and Q6_K).  An index outside [0, n_experts) is clamped and sets bit
+ * 32 of the error word (bread_moe_ctx_check). */
+int bread_moe_expert_block(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer, const float *d_x,
+                           float *d_hidden, int n_tokens, const int32_t *d_idx, const float *d_w,
+                           bread_stream_t stream);
 
 /* The MoE block of one_layer_forward on the reference's fp16 residual stream
  * (one_layer.cu:1800-1986, the d_hidden / d_normed2 interface of :1812-1815).

@@ -221,6 +221,28 @@ def expf(x: np.ndarray) -> np.ndarray:
     return out
 
 
+def expert_block(layer: HostLayer, x: np.ndarray, hidden: np.ndarray, idx: np.ndarray, w: np.ndarray,
+                 nthreads: int = 1) -> None:
+    """hidden[t] += sum_k w[t][k] * expert_{idx[t][k]}(x[t]) in rank order, the
+    routed experts alone with given routing: the CPU side of the reference's
+    expert benchmark (expert_bench.cu:127-144: gate/up matvecs, SwiGLU, down,
+    scaled by the weight and summed in k order) and the routed loop of
+    one_layer.cu:1455-1470.  Each term is rounded before it is added."""
+    s = layer.shape
+    H, I = s.hidden, s.expert_inter
+    tg, tu, td = layer.types[:3]
+    g, u, d = layer.arrays[:3]
+    gb, ub, db = I * row_bytes(tg, H), I * row_bytes(tu, H), H * row_bytes(td, I)
+    for t in range(x.shape[0]):
+        xt = np.ascontiguousarray(x[t], np.float32)
+        for k in range(idx.shape[1]):
+            e = int(idx[t, k])
+            eg = matvec(g[e * gb:(e + 1) * gb], tg, xt, I, H, nthreads)
+            eu = matvec(u[e * ub:(e + 1) * ub], tu, xt, I, H, nthreads)
+            eo = matvec(d[e * db:(e + 1) * db], td, swiglu(eg, eu), H, I, nthreads)
+            hidden[t] += np.float32(w[t, k]) * eo
+
+
 def moe_forward(layer: HostLayer, x: np.ndarray, hidden: np.ndarray, n_tokens: int, nthreads: int = 1):
     """hidden (float32 [T][H]) is updated in place; returns (idx, w, gsh)."""
     K = layer.shape.top_k

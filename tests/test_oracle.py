@@ -389,6 +389,51 @@ def test_moe_null_shared_gate_uses_half():
     assert g == 0.0
 
 
+def test_expert_block_is_moe_without_the_shared_expert():
+    """With the shared expert's down weights all zero (Q6_K d = 0), the MoE
+    block adds exactly 0 for it, so its output must equal the routed-only
+    block run with the same routing, bit for bit."""
+    L = small_layer(E=16, K=4, seed=60)
+    L.arrays[5][:] = 0
+    x = np.random.default_rng(18).standard_normal(512).astype(np.float32)
+    h = np.zeros(512, np.float32)
+    idx, w, _ = O.moe_token(L, x, h)
+    h2 = np.zeros((1, 512), np.float32)
+    O.expert_block(L, x[None], h2, np.asarray(idx)[None], np.asarray(w)[None])
+    assert np.array_equal(h, h2[0])
+
+
+def test_expert_block_vs_fp64_with_given_routing():
+    """The reference benchmark's block (experts 0..K-1, weight 1/K) and an
+    arbitrary routing with repeats, against numpy fp64 on the dequantised
+    weights; the residual accumulates."""
+    L = small_layer(E=8, K=4, H=512, I=256, seed=61)
+    s = L.shape
+    H, I = s.hidden, s.expert_inter
+    g, u, d = L.arrays[:3]
+    ge, de = I * (H // 256) * 144, H * (I // 256) * 210
+
+    def dq(a, qt, rows, cols):
+        return O.dequant_rows(np.ascontiguousarray(a), qt, rows, cols).astype(np.float64)
+
+    rng = np.random.default_rng(19)
+    x = rng.standard_normal((2, H)).astype(np.float32)
+    idx = np.array([[0, 1, 2, 3], [5, 5, 0, 7]], np.int32)
+    w = np.array([[0.25] * 4, [0.5, -0.25, 1.0, 0.125]], np.float32)
+    base = rng.standard_normal((2, H)).astype(np.float32)
+    h = base.copy()
+    O.expert_block(L, x, h, idx, w)
+    for t in range(2):
+        ref = base[t].astype(np.float64)
+        xd = x[t].astype(np.float64)
+        for k in range(4):
+            e = idx[t, k]
+            gg = dq(g[e * ge:(e + 1) * ge], O.QTYPE_Q4_K, I, H) @ xd
+            uu = dq(u[e * ge:(e + 1) * ge], O.QTYPE_Q4_K, I, H) @ xd
+            ref += np.float64(w[t, k]) * (dq(d[e * de:(e + 1) * de], O.QTYPE_Q6_K, H, I) @ (gg / (1 + np.exp(-gg)) * uu))
+        assert np.linalg.norm(h[t] - ref) / np.linalg.norm(ref - base[t]) < 1e-5
+
+
 def test_moe_threaded_is_bit_identical_and_residual_accumulates():
     L = small_layer(E=16, K=4, seed=50)
     rng = np.random.default_rng(17)
