@@ -98,12 +98,13 @@ __device__ __forceinline__ uint32_t ld_b32(const uint8_t *p)
 // is read.  Q6_K and Q8_0 blocks (210 and 34 bytes) are only 2-byte aligned.
 __device__ __forceinline__ uint2 ld8_a2(const uint8_t *p)
 {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint8_t *b = reinterpret_cast<const uint8_t *>(a & ~(uintptr_t)3);
-    const uint32_t sh = (uint32_t)(a & 3u);
+    // aligned down by pointer arithmetic, which keeps the global address
+    // space (a pointer rebuilt from an integer gets flat loads)
+    const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3u);
+    const uint8_t *b = p - sh;
     const uint32_t w0 = ld_b32(b);
     const uint32_t w1 = ld_b32(b + 4);
-    const uint32_t w2 = ld_b32(reinterpret_cast<const uint8_t *>((a + 7) & ~(uintptr_t)3));
+    const uint32_t w2 = ld_b32(b + (sh ? 8 : 4));
     uint2 r;
     r.x = __builtin_amdgcn_alignbyte(w1, w0, sh);
     r.y = __builtin_amdgcn_alignbyte(w2, w1, sh);
@@ -113,9 +114,9 @@ __device__ __forceinline__ uint2 ld8_a2(const uint8_t *p)
 // 16-bit value at a 2-byte aligned address.
 __device__ __forceinline__ uint32_t ld16_a2(const uint8_t *p)
 {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t w = ld_b32(reinterpret_cast<const uint8_t *>(a & ~(uintptr_t)3));
-    return (w >> (8u * (uint32_t)(a & 3u))) & 0xFFFFu;
+    const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3u);
+    const uint32_t w = ld_b32(p - sh);
+    return (w >> (8u * sh)) & 0xFFFFu;
 }
 
 // 8 bytes at a 2-byte aligned byte offset of a dword array (LDS), from

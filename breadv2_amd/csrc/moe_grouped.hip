@@ -246,8 +246,10 @@ struct Q6Raw {
 
 __device__ __forceinline__ void q6k_load(const uint8_t *sb, int g, Q6Raw &R)
 {
-    const uintptr_t base = reinterpret_cast<uintptr_t>(sb) & ~(uintptr_t)3;
-    const uint8_t *p = reinterpret_cast<const uint8_t *>(base);
+    // aligned down by pointer arithmetic: a pointer rebuilt from an integer
+    // is generic to the compiler, which would emit flat loads (counted on
+    // lgkmcnt too, so every LDS wait would also wait for these)
+    const uint8_t *p = sb - (reinterpret_cast<uintptr_t>(sb) & 3u);
     const uint8_t *ql = p + 64 * g, *qh = p + 128 + 32 * g, *sc = p + 192;
 #pragma unroll
     for (int i = 0; i < 4; i++) R.ql[i] = *reinterpret_cast<const uint4 *>(ql + 16 * i);
@@ -659,10 +661,12 @@ __global__ __launch_bounds__(DN_WAVES * WAVE, 2) void k_mt_down(const MtArgs a)
                                  R.ql[3].x, R.ql[3].y, R.ql[3].z, R.ql[3].w, R.ql4};
         const uint32_t hw[9] = {R.qh[0].x, R.qh[0].y, R.qh[0].z, R.qh[0].w, R.qh[1].x,
                                 R.qh[1].y, R.qh[1].z, R.qh[1].w, R.qh2};
-        const uint32_t sw[5] = {R.sc.x, R.sc.y, R.sc.z, R.sc.w, R.sc1};
-        const uint32_t s0 = __builtin_amdgcn_alignbyte(sw[2 * g + 1], sw[2 * g], sh8);      // sc[8g .. 8g+3]
-        const uint32_t s1 = __builtin_amdgcn_alignbyte(sw[2 * g + 2], sw[2 * g + 1], sh8);  // sc[8g+4 .. 8g+7]
-        const float d = h2f(sw[4] >> (8 * sh8));
+        // sc[8g .. 8g+3] and sc[8g+4 .. 8g+7]; g is per lane, so the words
+        // are picked by selects rather than by an indexed array
+        const uint32_t w0 = g ? R.sc.z : R.sc.x, w1 = g ? R.sc.w : R.sc.y, w2 = g ? R.sc1 : R.sc.z;
+        const uint32_t s0 = __builtin_amdgcn_alignbyte(w1, w0, sh8);
+        const uint32_t s1 = __builtin_amdgcn_alignbyte(w2, w1, sh8);
+        const float d = h2f(R.sc1 >> (8 * sh8));
         const int b = it % nb;
         bool bad = false;  // |d sc| * 32 beyond fp16's range
         // K-steps t and t + 8 use the same ql bytes (low and high nibbles)
