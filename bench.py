@@ -48,21 +48,29 @@ def log(msg: str) -> None:
 
 
 def measured_traffic():
-    """HBM bytes per k_decode launch from the committed rocprofv3 PMC summary
-    (FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by what the
-    same counter reads for a device copy of known size)."""
+    """HBM bytes per k_decode launch from the committed rocprofv3 PMC summary:
+    reads from the L2's memory read requests by size (TCC_EA0_RDREQ_32B/64B/
+    128B, unscaled; they read a device copy's bytes exactly), writes from
+    WRITE_SIZE scaled by what it reads for that copy.  Without the request
+    counts, FETCH_SIZE scaled the same way."""
     path = os.path.join(ROOT, "profiles", "k_decode_traffic.json")
     try:
         with open(path) as f:
             t = json.load(f)
     except (OSError, ValueError):
         return None, "no PMC summary", None
-    fs = t["calib_copy_kib"] / t["calib_fetch_kib"]
     ws = t["calib_copy_kib"] / t["calib_write_kib"]
-    kib = t["fetch_kib_per_dispatch"] * fs + t["write_kib_per_dispatch"] * ws
-    note = (f"profiles/k_decode_traffic.json: FETCH_SIZE {t['fetch_kib_per_dispatch']} KiB x {fs:.3f} + "
-            f"WRITE_SIZE {t['write_kib_per_dispatch']} KiB x {ws:.3f} (scales from a {t['calib_copy_kib']} KiB copy)")
-    return int(round(kib * 1024)), note, t.get("rocprof_single_layer_avg_us")
+    wkib = t["write_kib_per_dispatch"] * ws
+    if "ea_read_kib_per_dispatch" in t:
+        rkib = t["ea_read_kib_per_dispatch"]
+        note = (f"profiles/k_decode_traffic.json: reads {rkib} KiB (TCC_EA0_RDREQ_32B/64B/128B, unscaled) + "
+                f"WRITE_SIZE {t['write_kib_per_dispatch']} KiB x {ws:.3f} (scale from a {t['calib_copy_kib']} KiB copy)")
+    else:
+        fs = t["calib_copy_kib"] / t["calib_fetch_kib"]
+        rkib = t["fetch_kib_per_dispatch"] * fs
+        note = (f"profiles/k_decode_traffic.json: FETCH_SIZE {t['fetch_kib_per_dispatch']} KiB x {fs:.3f} + "
+                f"WRITE_SIZE {t['write_kib_per_dispatch']} KiB x {ws:.3f} (scales from a {t['calib_copy_kib']} KiB copy)")
+    return int(round((rkib + wkib) * 1024)), note, t.get("rocprof_single_layer_avg_us")
 
 
 def cpu_baseline(arena, s, seconds: float):
