@@ -65,6 +65,8 @@ struct bread_grouped_ws {
     int *pos_of = nullptr;                // sorted position of pair (t, k) [max_tokens*K]
     void *tiles = nullptr;                // M-tiles of the expert GEMMs
     int *n_tiles = nullptr;
+    int *work = nullptr;                  // per-XCD work lists of the two expert GEMMs
+    int *n_work = nullptr;                // their lengths [2][8]
     float *eo = nullptr;                  // expert outputs by pair [max_tokens*(K+1)][H]
     void *hhi = nullptr, *hlo = nullptr;  // SwiGLU outputs as hi/lo fp16 by pair [max_tokens*(K+1)][Imax]
     int *hexp = nullptr;                  // their row scale exponents [max_tokens*(K+1)]

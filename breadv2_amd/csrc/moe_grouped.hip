@@ -62,6 +62,8 @@ constexpr int GU_ROWS = GU_WAVES / 2 * 32;       // SwiGLU rows per gate/up work
 constexpr int DN_WAVES = 8, DN_BLOCKS = 2;       // 32-row down blocks per wave
 constexpr int DN_ROWS = DN_WAVES * DN_BLOCKS * 32;  // output rows per down workgroup
 constexpr int MAX_INTER = 512;                   // largest intermediate size the LDS plan holds
+constexpr int NXCD = 8;                          // L2 domains; workgroup L runs on XCD L % 8
+constexpr int SEG = 4;                           // tiles of one expert kept on one XCD
 constexpr uint32_t MAGIC = 0x64646464u;          // fp16 0x64xx = 1024 + xx
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -85,6 +87,9 @@ struct MtArgs {
     const int *pair_tok;     // [T*K + T] token of each sorted pair
     const MtTile *tiles;
     const int *n_tiles;
+    const int *work_gu, *work_dn;  // per-XCD work items (tile << 8 | chunk) of the two GEMMs
+    const int *n_work;             // [2][NXCD] items per XCD (gate/up, down)
+    int slots_gu, slots_dn;        // list capacity per XCD
     float *h;                // [T*K + T][Imax] SwiGLU outputs by pair
     const uint4 *hhi, *hlo;  // the same as hi/lo fp16 units in the down operand order
     const int *hexp;         // [T*K + T] their row scale exponents
@@ -376,10 +381,14 @@ __device__ __forceinline__ void block_scan2(int a, int b, int *wsa, int *wsb, in
 // (-1 for an index outside [0, E), which the combine skips).
 __global__ __launch_bounds__(1024) void k_mt_bucket(const int32_t *__restrict__ idx, int T, int K, int E,
                                                     int *__restrict__ pair_tok, int *__restrict__ pos_of,
-                                                    MtTile *__restrict__ tiles, int *__restrict__ n_tiles)
+                                                    MtTile *__restrict__ tiles, int *__restrict__ n_tiles,
+                                                    int *__restrict__ work_gu, int *__restrict__ work_dn,
+                                                    int *__restrict__ n_work, int c_gu, int c_dn, int slots_gu,
+                                                    int slots_dn)
 {
     __shared__ int cnt[1024], base[1024], cur[1024];
     __shared__ int wsa[16], wsb[16];
+    __shared__ int xfirst[NXCD + 1];
     const int tid = threadIdx.x;
     cnt[tid] = 0;
     cur[tid] = 0;
@@ -409,7 +418,68 @@ __global__ __launch_bounds__(1024) void k_mt_bucket(const int32_t *__restrict__ 
     const int nsh = (T + MT - 1) / MT;
     for (int i = tid; i < nsh; i += 1024) tiles[tt + i] = {E, P + i * MT, min(MT, T - i * MT), 0};
     for (int t = tid; t < T; t += 1024) pair_tok[P + t] = t;
-    if (tid == 0) *n_tiles = tt + nsh;
+    const int N = tt + nsh;
+    if (tid == 0) *n_tiles = N;
+
+    // Work lists.  Segments of at most SEG consecutive tiles of one expert
+    // (the shared expert's after the routed ones) stay on one XCD, so the
+    // expert's weights are fetched into that L2 once per segment instead of
+    // once per tile, while a hot expert's segments still spread over the
+    // XCDs.  The segment starting at tile s0 goes to XCD floor(8 s0 / N),
+    // and XCD x holds tiles [A(x), A(x + 1)) with A(x) the first segment
+    // start >= ceil(x N / 8).  Per XCD, items run segment by segment,
+    // chunk-major: (tile s0 + i, chunk c) at (s0 - A(x)) C + c n + i.
+    // A(x + 1) - A(x) <= ceil(N / 8) + SEG, which the host sizes the lists
+    // for; writes beyond a list are dropped regardless.
+    cnt[tid] = xt;  // each expert's first tile (the counts are used up)
+    if (tid <= NXCD) xfirst[tid] = N;
+    __syncthreads();
+    auto xcd_of = [&](int start) { return min(NXCD - 1, (int)(((long long)start * NXCD) / N)); };
+    // tile q's segment: start and length.  Below tt the expert is the last
+    // one whose first tile is <= q (an empty expert shares its first tile
+    // with the next, so that one is never empty).
+    auto segment = [&](int q, int &start, int &len) {
+        int first = tt, ntiles = nsh;
+        if (q < tt) {
+            int lo = 0, hi = E - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (cnt[mid] <= q) lo = mid;
+                else hi = mid - 1;
+            }
+            first = cnt[lo];
+            ntiles = (cur[lo] + MT - 1) / MT;
+        }
+        start = first + (q - first) / SEG * SEG;
+        len = min(SEG, first + ntiles - start);
+    };
+    for (int q = tid; q < N; q += 1024) {
+        int start, len;
+        segment(q, start, len);
+        if (q == start) atomicMin(&xfirst[xcd_of(q)], q);
+    }
+    __syncthreads();
+    if (tid == 0)
+        for (int x = NXCD - 1; x >= 0; x--) xfirst[x] = min(xfirst[x], xfirst[x + 1]);
+    __syncthreads();
+    for (int q = tid; q < N; q += 1024) {
+        int start, len;
+        segment(q, start, len);
+        const int x = xcd_of(start), b = start - xfirst[x], i = q - start;
+        for (int cc = 0; cc < c_gu; cc++) {
+            const int j = b * c_gu + cc * len + i;
+            if (j < slots_gu) work_gu[x * slots_gu + j] = (q << 8) | cc;
+        }
+        for (int cc = 0; cc < c_dn; cc++) {
+            const int j = b * c_dn + cc * len + i;
+            if (j < slots_dn) work_dn[x * slots_dn + j] = (q << 8) | cc;
+        }
+    }
+    if (tid < NXCD) {
+        const int nx = xfirst[tid + 1] - xfirst[tid];
+        n_work[tid] = min(nx * c_gu, slots_gu);
+        n_work[NXCD + tid] = min(nx * c_dn, slots_dn);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -424,17 +494,17 @@ __global__ __launch_bounds__(1024) void k_mt_bucket(const int32_t *__restrict__ 
 // ---------------------------------------------------------------------------
 
 // Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its
-// own L2.  The C chunks (row blocks) of one M-tile read the same activation
-// rows, so they are given linear ids L with the same L mod 8: one L2 fetches
-// the tile's activations for all of them.  L = 8 q + x gives tile
-// 8 (q / C) + x and chunk q mod C, a bijection onto the tiles padded to a
-// multiple of 8.
-__device__ __forceinline__ void xcd_tile(int C, int &tile, int &chunk)
+// own L2.  Workgroup L takes item L / 8 of XCD L % 8's list (k_mt_bucket);
+// false when that list is shorter.
+__device__ __forceinline__ bool xcd_item(const int *work, const int *n_work, int slots, int &tile, int &chunk)
 {
     const int L = (int)blockIdx.x;
-    const int q = L >> 3;
-    tile = (q / C) * 8 + (L & 7);
-    chunk = q % C;
+    const int x = L & (NXCD - 1), j = L / NXCD;
+    if (j >= n_work[x]) return false;
+    const int v = work[x * slots + j];
+    tile = v >> 8;
+    chunk = v & 255;
+    return true;
 }
 
 __global__ __launch_bounds__(GU_WAVES * WAVE, 2) void k_mt_gateup(const MtArgs a)
@@ -442,8 +512,7 @@ __global__ __launch_bounds__(GU_WAVES * WAVE, 2) void k_mt_gateup(const MtArgs a
     __shared__ uint4 sA[2][2][1024];  // [buffer][hi, lo][unit (s, g, n)]
     __shared__ int stok[MT], sexp[MT];
     int tile, chunk;
-    xcd_tile(a.Imax / GU_ROWS, tile, chunk);
-    if (tile >= *a.n_tiles) return;
+    if (!xcd_item(a.work_gu, a.n_work, a.slots_gu, tile, chunk) || tile >= *a.n_tiles) return;
     const MtTile tl = a.tiles[tile];
     const bool sh = tl.e == a.E;
     const int I = sh ? a.Ish : a.I;
@@ -614,8 +683,7 @@ __global__ __launch_bounds__(DN_WAVES * WAVE, 2) void k_mt_down(const MtArgs a)
     __shared__ uint4 sA[2][(MAX_INTER / 8) * MT];  // [hi, lo][unit ((16b + t)*2 + g)*32 + n]
     __shared__ int sexp[MT];
     int tile, chunk;
-    xcd_tile((a.H + DN_ROWS - 1) / DN_ROWS, tile, chunk);
-    if (tile >= *a.n_tiles) return;
+    if (!xcd_item(a.work_dn, a.n_work + NXCD, a.slots_dn, tile, chunk) || tile >= *a.n_tiles) return;
     const MtTile tl = a.tiles[tile];
     const bool sh = tl.e == a.E;
     const int I = sh ? a.Ish : a.I;
@@ -765,6 +833,23 @@ int max_tiles(const bread_moe_shape_t &s, int T)
     return P / MT + (P < s.n_experts ? P : s.n_experts) + (T + MT - 1) / MT;
 }
 
+// Tiles one XCD's list can hold: an eighth of the tiles plus one segment.
+int xcd_tiles(const bread_moe_shape_t &s, int T)
+{
+    return (max_tiles(s, T) + NXCD - 1) / NXCD + SEG;
+}
+
+int chunks_gu(const bread_moe_shape_t &s)
+{
+    const int Imax = s.expert_inter > s.shared_inter ? s.expert_inter : s.shared_inter;
+    return (Imax + GU_ROWS - 1) / GU_ROWS;
+}
+
+int chunks_dn(const bread_moe_shape_t &s)
+{
+    return (s.hidden + DN_ROWS - 1) / DN_ROWS;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -785,6 +870,9 @@ int bread_grouped_alloc(bread_moe_ctx_t *c)
     if (e == hipSuccess) e = hipMalloc((void **)&g.pos_of, T * K * sizeof(int));
     if (e == hipSuccess) e = hipMalloc(&g.tiles, (size_t)max_tiles(s, c->max_tokens) * sizeof(MtTile));
     if (e == hipSuccess) e = hipMalloc((void **)&g.n_tiles, sizeof(int));
+    const size_t xt = (size_t)xcd_tiles(s, c->max_tokens);
+    if (e == hipSuccess) e = hipMalloc((void **)&g.work, NXCD * xt * (chunks_gu(s) + chunks_dn(s)) * sizeof(int));
+    if (e == hipSuccess) e = hipMalloc((void **)&g.n_work, 2 * NXCD * sizeof(int));
     if (e == hipSuccess) e = hipMalloc((void **)&g.eo, P * H * sizeof(float));
     const size_t Imax = (size_t)(s.expert_inter > s.shared_inter ? s.expert_inter : s.shared_inter);
     if (e == hipSuccess) e = hipMalloc(&g.hhi, P * Imax * 2);
@@ -803,6 +891,8 @@ void bread_grouped_free(bread_moe_ctx_t *c)
     (void)hipFree(g.pos_of);
     (void)hipFree(g.tiles);
     (void)hipFree(g.n_tiles);
+    (void)hipFree(g.work);
+    (void)hipFree(g.n_work);
     (void)hipFree(g.eo);
     (void)hipFree(g.hhi);
     (void)hipFree(g.hlo);
@@ -842,8 +932,11 @@ int bread_launch_moe_grouped(bread_moe_ctx_t *c, const bread_moe_layer_t *L, con
         hipLaunchKernelGGL(k_mt_topk_xprep<16>, dim3(T), dim3(256), 0, st, c->logits, E, K, c->idx, c->w, x,
                            (const uint16_t *)L->shexp_gate, H, (uint4 *)g.xhi, (uint4 *)g.xlo, g.xexp, c->gsh);
     BREAD_HIP(hipGetLastError());
+    const int cgu = chunks_gu(s), cdn = chunks_dn(s);
+    const int slots_gu = xcd_tiles(s, T) * cgu, slots_dn = xcd_tiles(s, T) * cdn;
+    int *work_gu = g.work, *work_dn = g.work + (size_t)NXCD * slots_gu;
     hipLaunchKernelGGL(k_mt_bucket, dim3(1), dim3(1024), 0, st, c->idx, T, K, E, g.pair_tok, g.pos_of,
-                       (MtTile *)g.tiles, g.n_tiles);
+                       (MtTile *)g.tiles, g.n_tiles, work_gu, work_dn, g.n_work, cgu, cdn, slots_gu, slots_dn);
     BREAD_HIP(hipGetLastError());
     MtArgs a;
     a.L = *L;
@@ -861,20 +954,23 @@ int bread_launch_moe_grouped(bread_moe_ctx_t *c, const bread_moe_layer_t *L, con
     a.pair_tok = g.pair_tok;
     a.tiles = (const MtTile *)g.tiles;
     a.n_tiles = g.n_tiles;
+    a.work_gu = work_gu;
+    a.work_dn = work_dn;
+    a.n_work = g.n_work;
+    a.slots_gu = slots_gu;
+    a.slots_dn = slots_dn;
     a.h = c->h;
     a.hhi = (const uint4 *)g.hhi;
     a.hlo = (const uint4 *)g.hlo;
     a.hexp = g.hexp;
     a.eo = g.eo;
-    const int nt = max_tiles(s, T);
-    const int nt8 = (nt + 7) / 8 * 8;  // tiles padded for the XCD-aware mapping
-    hipLaunchKernelGGL(k_mt_gateup, dim3(nt8 * (Imax / GU_ROWS)), dim3(GU_WAVES * WAVE), 0, st, a);
+    hipLaunchKernelGGL(k_mt_gateup, dim3(NXCD * slots_gu), dim3(GU_WAVES * WAVE), 0, st, a);
     BREAD_HIP(hipGetLastError());
     const int rows = T * (K + 1);
     hipLaunchKernelGGL(k_mt_hprep, dim3((rows + 3) / 4), dim3(256), 0, st, c->h, rows, T * K, s.expert_inter,
                        s.shared_inter, Imax, (uint4 *)g.hhi, (uint4 *)g.hlo, g.hexp);
     BREAD_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_mt_down, dim3(nt8 * ((H + DN_ROWS - 1) / DN_ROWS)), dim3(DN_WAVES * WAVE), 0, st, a);
+    hipLaunchKernelGGL(k_mt_down, dim3(NXCD * slots_dn), dim3(DN_WAVES * WAVE), 0, st, a);
     BREAD_HIP(hipGetLastError());
     hipLaunchKernelGGL(k_mt_combine, dim3(T, (H / 4 + 255) / 256), dim3(256), 0, st, g.eo, g.pos_of, c->w, c->gsh,
                        hidden, H, K, T);
