@@ -356,12 +356,17 @@ int bread_moe_decode_layers(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layer
                             bread_stream_t stream);
 
 /* Timeline of the decode kernel: when d_buf is non-NULL, every launch with
- * grid * n_layers * 12 <= n_words records 64-bit wall-clock stamps (100 MHz)
- * at d_buf[(workgroup * n_layers + layer) * 12 + point], points 0 layer
+ * grid * n_layers * 18 <= n_words records 64-bit wall-clock stamps (100 MHz)
+ * at d_buf[(workgroup * n_layers + layer) * 18 + point], points 0 layer
  * start, 1 input normalised, 2 own logit published, 3 every logit seen,
  * 4 rank-1 expert known, 5 routing done, 6 own down dots done, 7 every down
  * dot done, 8 every SwiGLU output seen, 9 output rows stored, 10 the last
- * routed slot's SwiGLU outputs stored, 11 every routed down band loaded.
+ * routed slot's SwiGLU outputs stored, 11 every routed down band loaded,
+ * 12 last selection pass done, 13 ranks final (certified or recomputed),
+ * 14 and 15 (uncertified layers only) own logit in the reference's order
+ * done and every such logit seen, 16 the certificate's radii and maxima
+ * settled, 17 every selection pass seen by the certificate.  Points a
+ * layer does not reach keep their old value (clear the buffer first).
  * *grid_out receives the launch's workgroup count.  NULL turns it off. */
 int bread_moe_ctx_set_trace(bread_moe_ctx_t *ctx, uint64_t *d_buf, size_t n_words, int *grid_out);
 
