@@ -7,8 +7,8 @@
 // each product rounded to fp32, then added, never fused (one_layer.cu:969-971),
 // and the shared-gate score the same way with the fp16 gate widened
 // (one_layer.cu:977-980).  The sum is inherently sequential, so the kernel
-// gives each lane one token and each wave one router row (two beyond 64
-// tokens per CU): a lane's 2048 dependent (product, add) pairs are the
+// gives each lane one token and each wave one router row (two beyond two
+// workgroups per CU): a lane's 2048 dependent (product, add) pairs are the
 // latency floor of exact routing, and route_seq.h keeps every other cost
 // (activation staging, router weights by DPP broadcast) off that chain.
 
@@ -83,13 +83,14 @@ __global__ __launch_bounds__(WAVE) void k_topk_exact(const float *__restrict__ l
 
 } // namespace
 
-// Router rows per wave: one while the grid has at most one workgroup a CU
-// (the latency of a lane's sum is then the kernel's time), two beyond, where
-// two rows sharing each activation read halve the LDS reads per product.
+// Router rows per wave: one while the grid has at most two workgroups a CU
+// (64 KB of LDS each, so both are resident and the latency of a lane's sum
+// is the kernel's time), two beyond, where two rows sharing each activation
+// read halve the LDS reads per product.
 int bread_route_rows_per_wave(int T, int E)
 {
     const int tiles = (T + RS_TT - 1) / RS_TT;
-    return E < 2 || (size_t)tiles * ((E + RS_WAVES - 1) / RS_WAVES) <= 256 ? 1 : 2;
+    return E < 2 || (size_t)tiles * ((E + RS_WAVES - 1) / RS_WAVES) <= 512 ? 1 : 2;
 }
 
 int bread_launch_route_logits(const float *router, const uint16_t *shg, const float *x, float *logits, float *gsh,

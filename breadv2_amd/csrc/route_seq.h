@@ -35,7 +35,7 @@ namespace route_seq {
 constexpr int RS_WAVES = 4;              // waves per workgroup
 constexpr int RS_TT = WAVE;              // tokens per tile, one a lane
 constexpr int RS_CJ = 128;               // columns per staged chunk
-constexpr int RS_NB = 4;                 // chunk buffers: loads run RS_NB - 1 chunks ahead
+constexpr int RS_NB = 2;                 // chunk buffers (2 or 4): loads run RS_NB - 1 chunks ahead
 constexpr int RS_BLK = 16;               // columns per block of the pipelined inner loop
 constexpr int RS_XI = RS_TT / 2 / RS_WAVES;  // activation loads a wave issues per chunk (8)
 
@@ -224,10 +224,11 @@ __device__ __forceinline__ void chunk_dot(const float *xrow, int sw, const rs_f4
 // The chunk loop of one wave (work: the wave sums at all; gate: it sums the
 // gate; every wave stages and passes the same barriers).  Per chunk c: take
 // the weights loaded during chunk c - 1, issue the direct-to-LDS batch of
-// chunk c + 3 and the weights of chunk c + 1, sum chunk c, then wait for
-// batch c + 1 and pass a barrier.  Waiting for batch c + 1 leaves in flight
-// what was issued after it: the weights of chunks c - 1 .. c + 1 (2 NE + 2
-// loads each) and batches c + 2 and c + 3 (RS_XI each).
+// chunk c + RS_NB - 1 and the weights of chunk c + 1, sum chunk c, then wait
+// for batch c + 1 and pass a barrier.  Waiting for batch c + 1 leaves in
+// flight what was issued after it: with four buffers the weights of chunks
+// c - 1 .. c + 1 (2 NE + 2 loads each) and batches c + 2 and c + 3 (RS_XI
+// each); with two, the weights of chunk c + 1.
 template <int NE>
 __device__ __forceinline__ void rs_run(RsSmem &S, const float *__restrict__ x, const float *w0,
                                        const uint16_t *__restrict__ g, int t0, int T, int H, bool work, bool gate,
@@ -245,15 +246,20 @@ __device__ __forceinline__ void rs_run(RsSmem &S, const float *__restrict__ x, c
     bar();
     for (int c = 0; c < nc; c++) {
         rs_take<NE>(wc, wn, gn, gate);
-        // buffer (c + 3) % 4 was last read in chunk c - 1, before the
-        // barrier that ended it
+        // buffer (c + RS_NB - 1) % RS_NB was last read in chunk c - 1,
+        // before the barrier that ended it
         if (c + RS_NB - 1 < nc)
             rs_stage(S, (c + RS_NB - 1) % RS_NB, x, w0, t0, T, H, c + RS_NB - 1, wv, lane);
         if (c + 1 < nc) rs_load_w<NE>(wn, gn, w0, g, H, c + 1, lane);
         if (work) chunk_dot<NE>(S.x[c % RS_NB][lane], lane & 15, wc, acc);
         if (c + 1 < nc) {
-            if (c + 3 < nc) wait_vm<AFTER>();
-            else wait_vm<0>();
+            if constexpr (RS_NB == 4) {
+                if (c + 3 < nc) wait_vm<AFTER>();
+                else wait_vm<0>();
+            } else {
+                static_assert(RS_NB == 2, "chunk buffers");
+                wait_vm<2 * NE + 2>();  // chunk c + 1's weights were issued after its batch
+            }
             bar();
         }
     }
