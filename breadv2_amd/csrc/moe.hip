@@ -522,12 +522,14 @@ extern "C" int bread_route_layer_f16(bread_moe_ctx_t *c, const bread_moe_layer_t
     return bread_route_layer(c, L, c->x32, expert_indices, expert_weights, gsh_logit, stream);
 }
 
-// Up to this many tokens one decode-stack launch per token (509 us per
-// 40-layer stack on MI355X) beats 40 small-batch layers (28 us per layer at
-// 2 tokens, 35 at 4, 48 at 8), measured.
+// Up to this many tokens one decode-stack launch per token beats 40
+// small-batch layers, measured on MI355X over 40 resident layers: 1597 /
+// 2126 / 2680 us for 3 / 4 / 5 tokens one stack launch each, against
+// 2271 / 2508 / 2610 us on the small-batch path (its exact router and
+// selection cost ~27 us a layer).
 extern "C" int bread_stack_loop_tokens(void)
 {
-    return 2;
+    return 4;
 }
 
 extern "C" int bread_moe_forward(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, float *hidden,

@@ -93,8 +93,9 @@ def test_specialised_paths_refuse_other_layouts(typed_layer, path):
 def test_mixed_stack_matches_oracle():
     """Layers 0 and 2 have the decode kernel's types, 1 and 3 not: one
     bread_moe_decode_layers call runs layer 0, layer 1 (per-token), layer 2,
-    layer 3 (per-token) on one token; then 3 tokens through
-    bread_moe_stack_forward."""
+    layer 3 (per-token) on one token; then 3 tokens (one stack launch each)
+    and bread_stack_loop_tokens() + 1 tokens (batched calls per layer)
+    through bread_moe_stack_forward."""
     s = api.shape()
     L = 4
     types = [api.STANDARD_TYPES, LAYOUTS["q4_down"], api.STANDARD_TYPES, LAYOUTS["mixed"]]
@@ -123,7 +124,8 @@ def test_mixed_stack_matches_oracle():
             ridx.append(np.asarray(ri).reshape(h.shape[0], -1))
         return h, np.stack(ridx)
 
-    ctx = B.MoeContext(s, max_tokens=3)
+    TB = B.lib.bread_stack_loop_tokens() + 1
+    ctx = B.MoeContext(s, max_tokens=TB)
     h0 = xs(1, s.hidden, 18)
     hd = dev(h0)
     idx, _, _ = ctx.decode_layers(descs, hd, want_routing=True)
@@ -132,13 +134,14 @@ def test_mixed_stack_matches_oracle():
     assert np.array_equal(idx.cpu().numpy(), ridx[:, 0])
     assert_moe_close(hd.cpu().numpy(), href, base=h0)
 
-    h3 = xs(3, s.hidden, 19)
-    hd3 = dev(h3)
-    idx3, _, _ = ctx.stack_forward(descs, hd3, 3, want_routing=True)
-    torch.cuda.synchronize()
-    href3, ridx3 = oracle_stack(h3)
-    assert np.array_equal(idx3.cpu().numpy().reshape(ridx3.shape), ridx3)
-    assert_moe_close(hd3.cpu().numpy(), href3, base=h3)
+    for T in (3, TB):
+        h3 = xs(T, s.hidden, 19 + T)
+        hd3 = dev(h3)
+        idx3, _, _ = ctx.stack_forward(descs, hd3, T, want_routing=True)
+        torch.cuda.synchronize()
+        href3, ridx3 = oracle_stack(h3)
+        assert np.array_equal(idx3.cpu().numpy().reshape(ridx3.shape), ridx3), T
+        assert_moe_close(hd3.cpu().numpy(), href3, base=h3)
     assert ctx.check_device() == 0
     arena.close()
 
