@@ -109,10 +109,13 @@ def test_grouped_prefill_chunk(full_layer, zipf_layer, zipf):
         assert counts.max() > 4 * 16
 
 
-def test_grouped_all_tokens_same_experts(full_layer):
-    """Identical tokens: K experts take every token (T/16 tiles each)."""
+@pytest.mark.parametrize("T", [80, 300])
+def test_grouped_all_tokens_same_experts(full_layer, T):
+    """Identical tokens: K experts take every token (T/32 tiles each; at 300
+    tokens ten tiles, split into segments of four tiles on different XCDs'
+    work lists)."""
     s, t, hl = full_layer
-    x = np.repeat(tokens(1, s.hidden, 11, zipf=False), 80, axis=0)
+    x = np.repeat(tokens(1, s.hidden, 11, zipf=False), T, axis=0)
     hidden = np.zeros_like(x)
     got = run(s, t, x, hidden)
     assert distinct_experts(got[1]) == s.top_k
