@@ -85,8 +85,8 @@ def distinct_experts(idx) -> int:
 @pytest.mark.parametrize("T", [8, 16, 64, 128, 129])
 def test_grouped_batched_decode_zipf(zipf_layer, T):
     """Config 4: B tokens, Zipf-skewed routing (expert reuse across tokens).
-    128 and 129 tokens sit either side of the router's split (K over four
-    workgroups per tile, summed in k_topk_sum, up to 128 tokens)."""
+    64 and 128 tokens fill one and two 64-token router tiles; 129 starts a
+    third."""
     s, t, hl = zipf_layer
     x = tokens(T, s.hidden, 100 + T, zipf=True)
     hidden = np.zeros_like(x)
