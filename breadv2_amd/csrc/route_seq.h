@@ -237,7 +237,7 @@ __device__ __forceinline__ void rs_run(RsSmem &S, const float *__restrict__ x, c
     const int lane = lane_id(), wv = wave_id();
     const int nc = H / RS_CJ;
     constexpr int AFTER = 2 * RS_XI + 3 * (2 * NE + 2);
-    static_assert(AFTER < 64, "vmcnt range");
+    static_assert(RS_NB != 4 || AFTER < 64, "vmcnt range");
     rs_f4 wn[NE][2], wc[NE][2];
     uint2 gn[2];
     for (int c = 0; c < RS_NB - 1 && c < nc; c++) rs_stage(S, c, x, w0, t0, T, H, c, wv, lane);
