@@ -496,6 +496,7 @@ def main() -> int:
         arena.close()
         return 0
     h = torch.randn(1, s.hidden, device="cuda:0", generator=torch.Generator("cuda:0").manual_seed(1))
+    ctx.route_stats(reset=True)
 
     # one MoE layer of one decode token: x = RMSNorm(h); h += MoE_l(x), one
     # launch; the ctypes arguments are built once, so the host enqueues a step
@@ -553,6 +554,7 @@ def main() -> int:
             log(f"stack: {args.stack_tokens} tokens x {L} layers, {stack_us:.1f} us/token")
     if ctx.check_device():
         raise RuntimeError("decode kernel flagged a device error")
+    rstat = ctx.route_stats()
     if args.calib_copy:
         src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda:0")
         dst = torch.empty_like(src)
@@ -614,6 +616,15 @@ def main() -> int:
             "achieved_total_gbs": round(LAYER_TOTAL_BYTES / (launch_us * 1e-6) / 1e9, 1),
         },
         "cpu_baseline": None,
+    }
+    n_routed = sum(rstat[k] for k in ("decode_radius", "decode_per_expert", "decode_pair", "decode_exact"))
+    result["routing"] = {
+        "note": "outcome of the decode kernel's certified routing over every layer this run launched "
+                "(single-layer steps and stack tokens): ranks certified from the fast fp32 logits by one "
+                "radius or per-expert radii, or recomputed in the reference's sequential order",
+        "layers": n_routed,
+        **{k: rstat[k] for k in ("decode_radius", "decode_per_expert", "decode_pair", "decode_exact")},
+        "recomputed_frac": round((rstat["decode_pair"] + rstat["decode_exact"]) / max(n_routed, 1), 5),
     }
     if stack_us is not None:
         result["config"]["stack"] = {

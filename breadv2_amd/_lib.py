@@ -162,6 +162,7 @@ SIGNATURES = {
     "bread_moe_ctx_set_trace": (c_int, [c_void_p, c_void_p, ctypes.c_size_t, POINTER(c_int)]),
     "bread_moe_ctx_set_path": (c_int, [c_void_p, c_int]),
     "bread_moe_ctx_set_spin_limit": (c_int, [c_void_p, c_longlong]),
+    "bread_moe_ctx_route_stats": (c_int, [c_void_p, POINTER(c_uint64), c_int, c_int]),
     "bread_small_auto_tokens": (c_int, []),
     "bread_stack_loop_tokens": (c_int, []),
     "bread_rmsnorm_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_void_p]),

@@ -549,6 +549,18 @@ class MoeContext:
         self._trace = buf
         return g.value
 
+    ROUTE_STAT_NAMES = ("decode_radius", "decode_per_expert", "decode_pair", "decode_exact",
+                        "multi_certified", "multi_exact")
+
+    def route_stats(self, reset: bool = False) -> dict:
+        """bread_moe_ctx_route_stats: how often exact routing took each path
+        (decode layers by certificate outcome, multi-token tokens certified
+        or recomputed), since creation or the last reset."""
+        n = len(self.ROUTE_STAT_NAMES)
+        out = (ctypes.c_uint64 * n)()
+        check(lib.bread_moe_ctx_route_stats(self._h, out, n, 1 if reset else 0), "bread_moe_ctx_route_stats")
+        return dict(zip(self.ROUTE_STAT_NAMES, (int(v) for v in out)))
+
     def check_device(self) -> int:
         """bread_moe_ctx_check: 0, or BreadError carrying the kernels' error
         word in .device_error (the call clears it and resets the context)."""

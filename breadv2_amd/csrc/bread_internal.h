@@ -52,9 +52,21 @@ enum : uint32_t {
     BREAD_DEV_ERR_INDEX = 32u,  // expert block: a caller's expert index outside [0, n_experts)
 };
 
+// Routing outcomes counted on the device (bread_moe_ctx_route_stats).
+enum : int {
+    BREAD_RSTAT_RADIUS = 0,     // decode layers whose fast ranks one radius certified
+    BREAD_RSTAT_PER_EXPERT = 1, // decode layers certified by per-expert radii
+    BREAD_RSTAT_PAIR = 2,       // decode layers with two adjacent ranks recomputed in reference order
+    BREAD_RSTAT_EXACT = 3,      // decode layers with every logit recomputed in reference order
+    BREAD_RSTAT_N = 8,
+};
+
 // Device-side status of the persistent decode kernel.
 struct bread_decode_sync {
     bread_line error;  // non-zero: a bounded wait expired (sticky until checked)
+    struct alignas(128) {
+        uint32_t v[BREAD_RSTAT_N];
+    } rstat;           // routing outcomes, wrapping at 2^32
 };
 
 // Workspace of the grouped (multi-token) path, sized for max_tokens.
@@ -199,6 +211,9 @@ int bread_launch_decode_layers(bread_moe_ctx_t *ctx, const bread_moe_layer_t *la
 // decode kernel's types in one launch each, other layers on the per-token kernels.
 int bread_launch_decode_runs(bread_moe_ctx_t *ctx, const bread_moe_layer_t *layers, int n, float *hidden,
                              int32_t *idx, float *w, float *gsh, hipStream_t st, int rstride);
+// true if bread_launch_decode_layers takes this layer on this context (shape,
+// types, alignment, a grid that fits the device)
+bool bread_decode_accepts(const bread_moe_ctx_t *ctx, const bread_moe_layer_t *L);
 int bread_decode_max_blocks(int *out);
 int bread_decode_grid(const bread_moe_shape_t &s);
 int bread_decode_trace_points();

@@ -207,6 +207,18 @@ extern "C" int bread_moe_ctx_check(bread_moe_ctx_t *c, int *device_error)
     return BREAD_OK;
 }
 
+extern "C" int bread_moe_ctx_route_stats(bread_moe_ctx_t *c, uint64_t *counts, int n, int reset)
+{
+    BREAD_REQUIRE(c && (counts || n == 0), BREAD_ERR_ARG, "NULL context or counts");
+    BREAD_REQUIRE(n >= 0 && n <= BREAD_RSTAT_N, BREAD_ERR_ARG, "n outside [0, 8]");
+    BREAD_HIP(hipStreamSynchronize(c->last_stream));
+    uint32_t v[BREAD_RSTAT_N];
+    BREAD_HIP(hipMemcpy(v, c->dsync->rstat.v, sizeof(v), hipMemcpyDeviceToHost));
+    for (int i = 0; i < n; i++) counts[i] = v[i];
+    if (reset) BREAD_HIP(hipMemset(c->dsync->rstat.v, 0, sizeof(v)));
+    return BREAD_OK;
+}
+
 extern "C" int bread_moe_ctx_set_path(bread_moe_ctx_t *c, int path)
 {
     BREAD_REQUIRE(c, BREAD_ERR_ARG, "NULL context");
@@ -649,6 +661,8 @@ extern "C" int bread_moe_decode_layers(bread_moe_ctx_t *c, const bread_moe_layer
     c->last_stream = st;
     int rc = bread_launch_decode_runs(c, layers, n, hidden, idx, w, gsh, st, 1);
     if (rc == BREAD_ERR_SHAPE) return bread_fail(rc, "bread_moe_decode_layers", "shape not supported by the decode kernel");
+    if (rc == BREAD_ERR_CAPACITY)
+        return bread_fail(rc, "bread_moe_decode_layers", "a run of decode-kernel layers longer than the context's layer table");
     return rc;
 }
 

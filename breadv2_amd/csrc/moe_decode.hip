@@ -102,6 +102,17 @@ constexpr int N_HPOLL = W_PF;            // waves 0..11 poll the SwiGLU outputs
 constexpr int W_RAD = 4;                 // wave 4 publishes the logit's radius
 constexpr int W_CERT = NWV - 1;          // wave 15 certifies the routing (a down wave, idle until the ranks are in)
 constexpr uint32_t SPIN_DEFAULT = 1u << 18;  // sleeps a bounded wait allows after its first look
+// The layer's RMSNorm here sums the squares as a tree, the reference
+// (cpu_rms_norm_weighted, layer_ops.cu:203-212) sequentially, so the two
+// inv_rms differ by a factor c: the sequential sum of 2048 non-negative terms
+// is within (n-1)u of the exact one, the tree within 17u, so the sums differ
+// by at most 1.24e-4 relative, inv_rms (square root, one division, the eps
+// add) by at most 6.3e-5.  Every element of x then differs from c times the
+// reference's by at most 4u relative.  A common factor keeps the order of the
+// logits, so the certificate holds with each radius widened by 4u sum |w x|
+// and its tau and spread taken with this bound on |c - 1|; the recomputations
+// rebuild the reference's own x (ref_x).
+constexpr float CERT_KAPPA = 1.220703125e-4f;  // 2^-13 >= |c - 1|
 constexpr uint32_t BUF_WORD3 = 0x00020000u;  // raw buffer descriptor word 3 (gfx9)
 constexpr int AUX_COHERENT = 16;             // sc1: device-coherent access
 constexpr uint32_t SENTINEL = 0x7FA5A5A5u;   // signalling NaN: "not written yet"
@@ -120,6 +131,9 @@ static_assert(W_GU + MAXK == W_SH && W_SH + 2 <= NWV, "wave roles");
 static_assert(N_XQ * WAVE * 4 == DH && W_XQ >= NPOLL && W_XQ + N_XQ <= NWV,
               "fixed-point x: non-polling waves, four columns a thread");
 static_assert(G * ((MAXK + 2) / 2) <= 2 * N_HPOLL * WAVE, "h poll: at most two chunks a thread");
+static_assert(NSLOT * DI >= 2 * DH, "S.h holds h and its squares for the exact norm until the ranks are final");
+static_assert(BREAD_RSTAT_PER_EXPERT == 1 && BREAD_RSTAT_PAIR == 2 && BREAD_RSTAT_EXACT == 3,
+              "certify's return values index the routing counters");
 
 // Trace points recorded per (workgroup, layer) when a trace buffer is given.
 enum {
@@ -206,6 +220,7 @@ struct Smem {
     float sgsh;                        // sigmoid of the shared-gate logit
     float gsh;                         // the shared-gate logit
     int nready;                        // ranks published in idx
+    int wready;                        // key, w and smax of the ranks written (after the passes)
     int lgcnt;                         // polling waves done with the logits
     int rlcnt;                         // x-polling waves whose router partials are in S.rl
     int rbcnt;                         // x-polling waves whose radius terms are in S.rbw
@@ -457,6 +472,19 @@ __device__ __forceinline__ bool poll_word(bread_decode_sync *s, const uint64_t *
 struct Sel {
     uint32_t k0, k1, k2, k3;  // packed keys, descending
 };
+
+// Selection key of a fast logit: its bits mapped so that unsigned order is
+// numeric order, dropped to 30 bits (2 or more; NaN 1).  The passes order
+// the fast logits themselves, not their probabilities: a softmax is
+// monotone, and the certificate only vouches for ranks whose logits are far
+// more than the 4 ulps this drops apart, so the probabilities the reference
+// computes order them the same way.
+__device__ __forceinline__ uint32_t logit_key(float l)
+{
+    if (l != l) return 1u;
+    const uint32_t u = __builtin_bit_cast(uint32_t, l);
+    return ((u & 0x80000000u) ? ~u : (u | 0x80000000u)) >> 2;
+}
 
 __device__ __forceinline__ void cswap(uint32_t &a, uint32_t &b)
 {
@@ -869,6 +897,21 @@ __device__ float4 cert_prepare(const DecArgs &a, Smem &S, int E, uint32_t tag32,
     return make_float4(rm, am, sane ? 1.f : 0.f, 1.f);
 }
 
+// The softmax rounding margin tau = 12 u (1 + max|l| + R) of the reference's
+// logits (route_dev.h), taken from the fast logits' maximum magnitude am and
+// largest radius rm with the norm's factor (CERT_KAPPA) on both sides.
+__device__ __forceinline__ float cert_tau(float am, float rm)
+{
+    return 12.f * CERT_U * (1.f + CERT_KAPPA) * (1.f + (am + 2.f * rm) * (1.f + 2.f * CERT_KAPPA));
+}
+
+// The reference's spread limit (CERT_SPREAD) on the fast logits of ranks 0
+// and K-1, radii and the norm's factor included.
+__device__ __forceinline__ bool cert_spread_ok(float l0, float lk1, float rm)
+{
+    return l0 - lk1 + 2.f * rm <= CERT_SPREAD * (1.f - CERT_KAPPA);
+}
+
 // Wave W_CERT's one-radius certificate on wave 0's ranks as they arrive:
 // each new rank's logit against the previous rank's (gap > T = 2 R_max +
 // tau), and once rank K-1 is in, no expert outside the top K within T of it
@@ -879,10 +922,10 @@ __device__ float4 cert_prepare(const DecArgs &a, Smem &S, int E, uint32_t tag32,
 __device__ int cert_fast(Smem &S, int E, int K, float4 cm, const float (&lv)[4])
 {
     const int lane = opaque(lane_id());
-    const float T = 2.f * cm.x + 12.f * CERT_U * (1.f + cm.y + cm.x);
+    const float T = 2.f * cm.x + cert_tau(cm.y, cm.x);
     bool good = cm.z != 0.f;
     int have = 0;
-    float prev = 0.f;
+    float prev = 0.f, first = 0.f;
     const uint32_t lim = S.spin;
     for (uint32_t it = 0;; it++) {
         const int n = lds_get(&S.nready);
@@ -890,6 +933,7 @@ __device__ int cert_fast(Smem &S, int E, int K, float4 cm, const float (&lv)[4])
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             for (int k = have; k < n; k++) {
                 const float lk = S.lg[S.idx[k < MAXK ? k : 0]];
+                if (k == 0) first = lk;
                 if (k > 0 && !(prev - lk > T)) good = false;
                 prev = lk;
             }
@@ -903,7 +947,8 @@ __device__ int cert_fast(Smem &S, int E, int K, float4 cm, const float (&lv)[4])
         }
         __builtin_amdgcn_s_sleep(1);
     }
-    if (!good) return 0;
+    // the selected probabilities are normal floats (CERT_SPREAD)
+    if (!good || !cert_spread_ok(first, prev, cm.x)) return 0;
     if (K >= E) return 1;
     const float lo = prev - T;
     int cnt = 0;
@@ -988,6 +1033,29 @@ __device__ __forceinline__ uint32_t key_of(const Smem &S, float m)
     return prob_key(expf(m - ms.x) / ms.y);
 }
 
+// The reference's normalised input (cpu_rms_norm_weighted, layer_ops.cu:
+// 203-212) into S.x, by wave W_CERT before a recomputation in the reference's
+// order: the sequential fp32 sum of the rounded squares, inv_rms =
+// 1/sqrt(sum/H + eps), x = (h inv_rms) w.  P1 left the squares in S.h[0, DH)
+// and h in S.h[DH, 2 DH); nothing else writes S.h before the ranks are final.
+__device__ void ref_x(Smem &S, float eps, bool has_nw, int lane)
+{
+#pragma clang fp contract(off)
+    const float ss = seq_sum_lds(S.h, DH);
+    const float inv = 1.0f / sqrtf(ss / (float)DH + eps);
+#pragma unroll
+    for (int i = 0; i < DH / (4 * WAVE); i++) {
+        const int o = 4 * (WAVE * i + lane);
+        const float4 h = *reinterpret_cast<const float4 *>(&S.h[DH + o]);
+        const float4 w = has_nw ? *reinterpret_cast<const float4 *>(&S.nw[o]) : make_float4(1.f, 1.f, 1.f, 1.f);
+        *reinterpret_cast<float4 *>(&S.x[o]) =
+            make_float4((h.x * inv) * w.x, (h.y * inv) * w.y, (h.z * inv) * w.z, (h.w * inv) * w.w);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_wave_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Run by wave W_CERT once the K + 1 selection passes are published: the
 // fast logits order the top K + 1 as the reference's sums would (route_dev.h
 // gives each logit a radius around the reference's sequential sum).
@@ -1006,25 +1074,30 @@ __device__ __forceinline__ uint32_t key_of(const Smem &S, float m)
 //      equal logits tie (the lower index first, as cpu_topk's strict '>'
 //      takes it), logits more than tau apart order strictly.
 //   4. Otherwise exact_routing (every logit in the reference's order).
-// Returns 1 (certified), 2 (ranks settled anew) or 0 (a wait failed).
+// Steps 1-3 need rank K-1's logit within CERT_SPREAD of rank 0's (radii
+// included); otherwise step 4.  Returns 1 (certified), 2 (a pair
+// recomputed), 3 (every logit recomputed) or 0 (a wait failed).
 __device__ int certify(const DecArgs &a, const DecLayer &Ly, Smem &S, int g, int E, int K, uint32_t tag32, int l,
-                       float4 cm, int wk, float lk)
+                       float4 cm, int wk, float lk, bool normed)
 {
 #pragma clang fp contract(off)
     const int lane = opaque(lane_id());  // not hoisted out of the layer loop
     const int np = K < E ? K + 1 : K;
     const float rm = cm.x, am = cm.y;
-    const bool sane = cm.z != 0.f;
-    const float tau = 12.f * CERT_U * (1.f + am + rm);
+    const float tau = cert_tau(am, rm);
+    // steps 3 and 4 read (and step 4 rewrites) the ranks' keys, which wave 0
+    // writes after its passes
+    if (!lds_wait(S, &S.wready, 1)) return 0;
     // lane k < np holds rank k's expert and logit (cert_gather; rank K is
     // the first expert not selected)
+    const bool sane = cm.z != 0.f && cert_spread_ok(lane_f(lk, 0), lane_f(lk, K - 1), rm);
     const bool rk = lane < np;
     // 1: consecutive gaps against one radius (lane k: ranks k-1, k)
     const float prev = dpp_or<0x111>(__builtin_inff(), lk);
     const bool gk = lane == 0 || !rk || prev - lk > 2.f * rm + tau;
     if (sane && __builtin_amdgcn_ballot_w64(!gk) == 0) return 1;
     const float rr = rk ? S.lr[wk] : 0.f;
-    bool clobbered = false;
+    int j = -1;  // >= 0: only ranks j, j+1 are in doubt (step 3)
     if (sane && np > K) {
         // 2: per-expert radii.  um: the largest hi of the experts not selected
         int ws[MAXK + 1];
@@ -1059,41 +1132,46 @@ __device__ int certify(const DecArgs &a, const DecLayer &Ly, Smem &S, int g, int
         const uint64_t sep = __builtin_amdgcn_ballot_w64(sepk);
         const uint64_t doubt = ~sep & ((1ull << K) - 1ull);
         if (doubt == 0) return 1;
-        const int j = (int)__builtin_ctzll(doubt);
-        if ((doubt & (doubt - 1)) == 0 && ((sep >> (j + 1)) & 1ull)) {
-            // 3: the two logits of ranks j, j+1 in the reference's order
-            const int ea = __builtin_amdgcn_readlane(wk, j);
-            const int eb = __builtin_amdgcn_readlane(wk, j + 1);
-            clobbered = true;
+        const int jd = (int)__builtin_ctzll(doubt);
+        if ((doubt & (doubt - 1)) == 0 && ((sep >> (jd + 1)) & 1ull)) j = jd;
+    }
+    // steps 3 and 4 sum in the reference's order, on the reference's x
+    // (built before step 3 reuses S.nw)
+    if (normed) ref_x(S, a.eps, Ly.norm_w != nullptr, lane);
+    bool clobbered = false;
+    if (j >= 0) {
+        // 3: the two logits of ranks j, j+1 in the reference's order
+        const int ea = __builtin_amdgcn_readlane(wk, j);
+        const int eb = __builtin_amdgcn_readlane(wk, j + 1);
+        clobbered = true;
 #pragma unroll
-            for (int i = 0; i < DH / (4 * WAVE); i++) {
-                lds_load16(Ly.router + (size_t)ea * DH + 4 * (WAVE * i + lane), &S.wrow[4 * WAVE * i]);
-                lds_load16(Ly.router + (size_t)eb * DH + 4 * (WAVE * i + lane), &S.nw[4 * WAVE * i]);
-            }
-            __builtin_amdgcn_s_waitcnt(0);
-            products_in_place(S.wrow, S.x, lane);
-            products_in_place(S.nw, S.x, lane);
-            const float acc = seq_sum_lds(lane == 1 ? S.nw : S.wrow, DH);
-            const float la = lane_f(acc, 0), lb = lane_f(acc, 1);
-            trace_point_lane0(a, l, TP_XDOT);
-            if (__builtin_isfinite(la) && __builtin_isfinite(lb) && (la == lb || fabsf(la - lb) > tau)) {
-                const bool swap = la == lb ? eb < ea : lb > la;
-                const float lK = lane_f(lk, K);
-                if (swap && lane == 0) {
-                    const uint32_t kb = j + 1 < K ? S.key[j + 1] : key_of(S, lK);
-                    if (j + 1 < K) {
-                        S.idx[j + 1] = ea;
-                        S.key[j + 1] = S.key[j];
-                    }
-                    S.idx[j] = eb;
-                    S.key[j] = kb;
+        for (int i = 0; i < DH / (4 * WAVE); i++) {
+            lds_load16(Ly.router + (size_t)ea * DH + 4 * (WAVE * i + lane), &S.wrow[4 * WAVE * i]);
+            lds_load16(Ly.router + (size_t)eb * DH + 4 * (WAVE * i + lane), &S.nw[4 * WAVE * i]);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        products_in_place(S.wrow, S.x, lane);
+        products_in_place(S.nw, S.x, lane);
+        const float acc = seq_sum_lds(lane == 1 ? S.nw : S.wrow, DH);
+        const float la = lane_f(acc, 0), lb = lane_f(acc, 1);
+        trace_point_lane0(a, l, TP_XDOT);
+        if (__builtin_isfinite(la) && __builtin_isfinite(lb) && (la == lb || fabsf(la - lb) > tau)) {
+            const bool swap = la == lb ? eb < ea : lb > la;
+            const float lK = lane_f(lk, K);
+            if (swap && lane == 0) {
+                const uint32_t kb = j + 1 < K ? S.key[j + 1] : key_of(S, lK);
+                if (j + 1 < K) {
+                    S.idx[j + 1] = ea;
+                    S.key[j + 1] = S.key[j];
                 }
-                return 2;
+                S.idx[j] = eb;
+                S.key[j] = kb;
             }
+            return 2;
         }
     }
     // 4: every logit in the reference's order
-    return exact_routing(a, Ly, S, g, E, K, tag32, lane, l, clobbered) ? 2 : 0;
+    return exact_routing(a, Ly, S, g, E, K, tag32, lane, l, clobbered) ? 3 : 0;
 }
 
 // ---------------------------------------------------------------- logit radius
@@ -1106,14 +1184,15 @@ __device__ int certify(const DecArgs &a, const DecLayer &Ly, Smem &S, int g, int
 // with A_t = sum |w_k x_k| of the thread.  The logit itself carries at most
 // 17 u A of rounding (4 in a thread's fma chain, 6 in the wave tree, 7 across
 // the waves), which the radius absorbs: per unit of A, 4 + c_H + 17 with 2 to
-// spare for the fp32 rounding of the prefixes used here.  wave_terms gives
+// spare for the fp32 rounding of the prefixes used here, and 4 more for the
+// norm's per-element rounding against the reference's x (CERT_KAPPA).  wave_terms gives
 // wave w's sum of the thread terms; the workgroup's radius adds
 // u (sum_w 256 |W_w| + |logit|) to their sum, times (1 + 2^-9) for the fp32
 // rounding of these sums, plus 1e-37 for underflow.
 __device__ __forceinline__ float wave_terms(float r, float ra)
 {
     const float incl = wave_scan_incl_f32(r);
-    return wave_sum(4.f * fabsf(incl - r) + (23.f + cert_c_h(DH)) * ra);
+    return wave_sum(4.f * fabsf(incl - r) + (27.f + cert_c_h(DH)) * ra);
 }
 
 // ---------------------------------------------------------------- kernel
@@ -1162,6 +1241,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             if (lane <= K) cstore2(hnext + XREC * g + GR * lane, sent, sent);
             if (tid == 0) {
                 S.nready = 0;
+                S.wready = 0;
                 S.xqcnt = 0;
                 S.gudone = 0;
                 S.lgcnt = 0;
@@ -1188,6 +1268,13 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                 ok = poll4(sy, r, 4u * (uint32_t)(XREC * (tid >> 1) + 4 * (tid & 1)), hv, S.spin);
             }
             if (own && !(l == 0 && a.x0)) *reinterpret_cast<float4 *>(&S.hown[4 * (tid & 1)]) = hv;
+            if (!(l == 0 && a.x0)) {
+                // h and its rounded squares for the certificate's exact
+                // norm (ref_x), in S.h: free until the ranks are final
+                *reinterpret_cast<float4 *>(&S.h[4 * tid]) =
+                    make_float4(__fmul_rn(hv.x, hv.x), __fmul_rn(hv.y, hv.y), __fmul_rn(hv.z, hv.z), __fmul_rn(hv.w, hv.w));
+                *reinterpret_cast<float4 *>(&S.h[DH + 4 * tid]) = hv;
+            }
             const float ss = wave_sum(fmaf(hv.x, hv.x, fmaf(hv.y, hv.y, fmaf(hv.z, hv.z, hv.w * hv.w))));
             if (lane == 0) S.red[wid] = ss;
             if (!ok) S.abort = 1;
@@ -1295,9 +1382,10 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
 #pragma unroll
                         for (int vv = 0; vv < 4; vv++) p[vv] = S.lg[lane + WAVE * vv];
                         uint32_t key[4];
-                        const float2 ms = softmax_keys<4>(p, E, key);
-                        if (lane == 0) S.smax = ms;  // for the certificate's key of rank K
+#pragma unroll
+                        for (int vv = 0; vv < 4; vv++) key[vv] = lane + WAVE * vv < E ? logit_key(p[vv]) : 0u;
                         Sel sel = sel_init(key);
+                        int wsel = 0;  // lane k: rank k's expert
 #pragma unroll
                         for (int k = 0; k < MAXK; k++) {
                             if (k >= K) break;
@@ -1305,22 +1393,37 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                             const int win = sel_pass(sel, lane, M);
                             if (lane == 0) {
                                 S.idx[k] = win < E ? win : 0;
-                                S.key[k] = M;
                                 lds_put(&S.nready, k + 1);
                             }
+                            if (lane == k) wsel = win < E ? win : 0;
                             if (k == 0) trace_point(a, l, TP_RANK1);
                         }
                         trace_point(a, l, TP_PASSES);
-                        // the weights from these ranks (P7 redoes them if the
+                        // the softmax, off the ranks' path: the ranks'
+                        // probability keys and weights (P7 redoes them if the
                         // certificate settled the ranks anew)
-                        const float wk = renorm_weight(lane < K ? S.key[lane] : 0u, K);
+                        uint32_t pk[4];
+                        const float2 ms = softmax_keys<4>(p, E, pk);
+                        uint32_t mk = 0u;
+#pragma unroll
+                        for (int vv = 0; vv < 4; vv++) {
+                            const uint32_t q = (uint32_t)__shfl((int)pk[vv], wsel & (WAVE - 1));
+                            if ((wsel >> 6) == vv) mk = q;
+                        }
+                        if (lane >= K) mk = 0u;
+                        const float wk = renorm_weight(mk, K);
                         float gsh = 0.f;
 #pragma unroll
                         for (int w = 0; w < N_XPOLL; w++) gsh += S.gl[w];
-                        if (lane < K) S.w[lane] = wk;
+                        if (lane < K) {
+                            S.key[lane] = mk;
+                            S.w[lane] = wk;
+                        }
                         if (lane == 0) {
+                            S.smax = ms;  // for the certificate's key of rank K
                             S.sgsh = sigmoidf_ref(gsh);
                             S.gsh = gsh;
+                            lds_put(&S.wready, 1);
                         }
                         trace_point(a, l, TP_ROUTED);
                     } else if (lane == 0) {
@@ -1382,6 +1485,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
             // loads go out once every rank is known, behind the gate/up
             // loads, and again if the exact recomputation replaced the ranks
             // (wave W_CERT certifies the ranks first: its loads wait for it)
+            int kind = -1;  // the certificate's outcome (BREAD_RSTAT_*), wave W_CERT
             if (wid == W_CERT) {
                 // as urgent as wave 0's passes (another SIMD)
                 __builtin_amdgcn_s_setprio(3);
@@ -1390,12 +1494,17 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                 trace_point_lane0(a, l, TP_PREP);
                 int st = cm.w != 0.f ? cert_fast(S, E, K, cm, lv) : -1;
                 trace_point_lane0(a, l, TP_READY);
+                kind = BREAD_RSTAT_RADIUS;
                 if (st == 0) {
                     int wk;
                     float lk;
-                    st = cert_gather(S, E, K, wk, lk) ? certify(a, Ly, S, g, E, K, tag32, l, cm, wk, lk) : 0;
+                    st = cert_gather(S, E, K, wk, lk)
+                             ? certify(a, Ly, S, g, E, K, tag32, l, cm, wk, lk, !(l == 0 && a.x0))
+                             : 0;
+                    kind = st;  // BREAD_RSTAT_PER_EXPERT, _PAIR or _EXACT
                 }
-                if (lane == 0) lds_put(st > 0 ? &S.cert : &S.abort, st > 0 ? st : 1);
+                if (st <= 0) kind = -1;
+                if (lane == 0) lds_put(st > 0 ? &S.cert : &S.abort, st > 1 ? 2 : 1);  // cert 2: ranks settled anew
                 __builtin_amdgcn_s_setprio(0);
                 trace_point_lane0(a, l, TP_CERT);
             }
@@ -1416,6 +1525,10 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                 ok = lds_wait(S, &S.cert, 1) && lds_get(&S.cert) == 2 && round == 0;
             }
             if (lane == 0) lds_add(&S.dncnt, 1);
+            // workgroup 0 counts the layer's routing outcome: after the wave's
+            // last wait of the layer, so that no wait covers the atomic
+            if (g == 0 && kind >= 0 && lane == 0)
+                __hip_atomic_fetch_add(&sy->rstat.v[kind], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             // the next layer's routing-independent weights, now that this
             // layer's are consumed (the shared gate/up was used before waves
             // 9 and 10 loaded their bands)
@@ -1478,6 +1591,11 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                 if (!has_error(sy)) flag_error(sy, BREAD_DEV_ERR_HWAIT);
                 ok = false;
             }
+            // S.h holds the exact norm's operands until the ranks are final
+            // (the shared slot's values can arrive before then); a wave
+            // past the pre-decode gate has seen every routed gate/up done,
+            // which follows the final ranks
+            if (!pre && !lds_wait(S, &S.cert, 1)) ok = false;
             // columns 2w, 2w+1 stay adjacent in the hpos layout
             if (c0 < G * NQ) {
                 const int o = hpos(GR * wa);
@@ -1638,6 +1756,11 @@ int bread_decode_max_blocks(int *out)
     BREAD_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_decode, NT, 0));
     *out = cus * per_cu;
     return BREAD_OK;
+}
+
+bool bread_decode_accepts(const bread_moe_ctx_t *c, const bread_moe_layer_t *L)
+{
+    return c->decode_max_blocks >= G && decode_shape_ok(c->shape) && layer_ok(*L);
 }
 
 int bread_launch_moe_decode(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, float *hidden,

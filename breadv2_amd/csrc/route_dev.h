@@ -115,7 +115,14 @@ __device__ __forceinline__ float wave_scan_incl_f32(float v)
 // R); so when every consecutive pair of the top K+1 (in the order selected
 // here) is more than 2 R_max + tau apart in the fast logits, the reference
 // selects the same experts in the same order.
+// The tau argument bounds relative errors, so it needs the probabilities it
+// compares to be normal floats: the selected ranks' logits lie within
+// CERT_SPREAD of the largest (then p >= e^-80 / 256 > 2^-126); an expert
+// further below has a smaller probability in any case (subnormal or zero
+// when below 2^-126, otherwise ordered by tau).  Wider spreads are left to
+// the reference-order recomputation.
 constexpr float CERT_U = 5.9604645e-8f;  // 2^-24
+constexpr float CERT_SPREAD = 80.f;
 
 __device__ __forceinline__ float cert_c_h(int n)
 {

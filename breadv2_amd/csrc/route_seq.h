@@ -65,6 +65,20 @@ __device__ __forceinline__ void wait_vm()
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// Keeps the vector memory operations issued before it ahead of those issued
+// after it.  The partial vmcnt waits of rs_run count on that order (gfx9
+// completes a wave's vector memory operations in issue order), and nothing
+// else pins it: the weight and gate loads read __restrict__ read-only
+// arguments, so the optimiser could hoist them above the direct-to-LDS
+// batch, and a wait meant for the batch would then leave part of it in
+// flight across the barrier.  The empty asm with a memory clobber stops the
+// optimiser, the scheduling barrier the machine scheduler.
+__device__ __forceinline__ void issue_order()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 // A workgroup barrier without a memory fence: the direct-to-LDS data a
 // barrier publishes is waited for explicitly by its issuing wave, so the
 // loads running further ahead stay in flight.  The signal fences keep the
@@ -241,6 +255,7 @@ __device__ __forceinline__ void rs_run(RsSmem &S, const float *__restrict__ x, c
     rs_f4 wn[NE][2], wc[NE][2];
     uint2 gn[2];
     for (int c = 0; c < RS_NB - 1 && c < nc; c++) rs_stage(S, c, x, w0, t0, T, H, c, wv, lane);
+    issue_order();
     rs_load_w<NE>(wn, gn, w0, g, H, 0, lane);
     wait_vm<0>();
     bar();
@@ -250,7 +265,9 @@ __device__ __forceinline__ void rs_run(RsSmem &S, const float *__restrict__ x, c
         // before the barrier that ended it
         if (c + RS_NB - 1 < nc)
             rs_stage(S, (c + RS_NB - 1) % RS_NB, x, w0, t0, T, H, c + RS_NB - 1, wv, lane);
+        issue_order();
         if (c + 1 < nc) rs_load_w<NE>(wn, gn, w0, g, H, c + 1, lane);
+        issue_order();
         if (work) chunk_dot<NE>(S.x[c % RS_NB][lane], lane & 15, wc, acc);
         if (c + 1 < nc) {
             if constexpr (RS_NB == 4) {

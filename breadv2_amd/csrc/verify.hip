@@ -107,6 +107,18 @@ int bread_launch_decode_runs(bread_moe_ctx_t *c, const bread_moe_layer_t *layers
                              int32_t *idx, float *w, float *gsh, hipStream_t st, int rstride)
 {
     const int H = c->shape.hidden, K = c->shape.top_k;
+    // Decide before launching anything: a run refused after earlier layers
+    // had run would leave hidden part-way through the stack, and a caller
+    // that falls back to another path on BREAD_ERR_SHAPE would apply those
+    // layers twice.
+    for (int l = 0, run = 0; l < n; l++) {
+        if (!bread_standard_qtypes(&layers[l])) {
+            run = 0;
+            continue;
+        }
+        if (!bread_decode_accepts(c, &layers[l])) return BREAD_ERR_SHAPE;
+        if (++run > c->max_layers) return BREAD_ERR_CAPACITY;
+    }
     for (int l = 0; l < n;) {
         const size_t r = (size_t)l * rstride;
         if (bread_standard_qtypes(&layers[l])) {

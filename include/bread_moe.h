@@ -198,6 +198,18 @@ int bread_stack_loop_tokens(void);
  * again. */
 int bread_moe_ctx_check(bread_moe_ctx_t *ctx, int *device_error);
 
+/* Routing outcomes counted on the device since the context was created (or
+ * last reset), after synchronising its last stream: counts[0..n) (n <= 8)
+ * receives, per decode-kernel layer, 0 = ranks certified by one radius,
+ * 1 = by per-expert radii, 2 = two adjacent ranks recomputed in the
+ * reference's order, 3 = every logit recomputed in the reference's order;
+ * 4 = multi-token tokens whose fast logits were certified, 5 = multi-token
+ * tokens recomputed in the reference's order; 6-7 unused.  Counters wrap at
+ * 2^32.  reset != 0 clears them; bread_moe_ctx_check clears them after a
+ * flagged error.  No reference counterpart: it reports how often exact
+ * routing needed the slow path. */
+int bread_moe_ctx_route_stats(bread_moe_ctx_t *ctx, uint64_t *counts, int n, int reset);
+
 /* Routing for n_tokens tokens on the device: router GEMV (fp32), softmax,
  * top-k with ties to the lower index, renormalised weights, and the raw
  * shared-gate logit (before the sigmoid).  d_x is fp32 [n_tokens][H];

@@ -2,7 +2,8 @@
 // library's expf: every float input from `first` to `last` (bit patterns,
 // inclusive) taken `stride` apart.  Prints the number of inputs and of
 // mismatches (NaN results compare equal regardless of payload); exit status
-// 0 only with no mismatch.  Built by the Makefile beside the library.
+// 0 only with no mismatch.  Built by tests/test_expf.py against the library's
+// header (breadv2_amd/csrc on the include path).
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>

@@ -2,8 +2,8 @@
 equal the C library's expf bit for bit: cpu_softmax (layer_ops.cu:222-229)
 calls the C library's, and the oracle is that same function.
 
-The restatement compiled for the host (breadv2_amd/csrc/expf_check, built by
-the library's Makefile from the same header the kernels include) is compared
+The restatement compiled for the host (tests/expf_check.hip, built here
+against the same header the kernels include) is compared
 with the C library over every float in [-104, -1] and [-2^-20, 0) and a
 stride through all 2^32 bit patterns (NaNs, infinities, subnormals and the
 overflow and underflow edges included).  The whole 2^32 range was checked
@@ -22,7 +22,8 @@ from oracle import oracle as O
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "breadv2_amd", "csrc")
-TOOL = os.path.join(CSRC, "_build", "expf_check")
+TOOL_SRC = os.path.join(os.path.dirname(os.path.abspath(__file__)), "expf_check.hip")
+HIPCC = "/opt/rocm/bin/hipcc"
 
 RANGES = [
     ("bf800000", "c2d00000", 1),     # [-104, -1]: every float
@@ -32,11 +33,16 @@ RANGES = [
 ]
 
 
+def build_tool(src, inc, exe):
+    r = subprocess.run([HIPCC, "--offload-arch=gfx950", "-O2", "-std=c++17", "-I", str(inc), str(src), "-o", str(exe)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-400:]
+    return str(exe)
+
+
 @pytest.fixture(scope="module")
-def tool():
-    if not os.path.exists(TOOL):
-        subprocess.run(["make", "-C", CSRC, "_build/expf_check"], check=True, capture_output=True)
-    return TOOL
+def tool(tmp_path_factory):
+    return build_tool(TOOL_SRC, CSRC, tmp_path_factory.mktemp("expf") / "expf_check")
 
 
 def run(tool, first, last, stride):
@@ -73,11 +79,9 @@ def test_check_catches_planted_errors(tmp_path, old, new):
     src = open(os.path.join(CSRC, "bread_expf.h")).read()
     assert old in src
     (tmp_path / "bread_expf.h").write_text(src.replace(old, new))
-    (tmp_path / "expf_check.hip").write_text(open(os.path.join(CSRC, "expf_check.hip")).read())
-    exe = tmp_path / "expf_check"
-    r = subprocess.run(["/opt/rocm/bin/hipcc", "--offload-arch=gfx950", "-O2", "-std=c++17",
-                        str(tmp_path / "expf_check.hip"), "-o", str(exe)], capture_output=True, text=True)
-    assert r.returncode == 0, r.stderr[-400:]
+    (tmp_path / "expf_check.hip").write_text(open(TOOL_SRC).read())
+    # the copy's own directory comes first for a quoted include: the planted header
+    exe = build_tool(tmp_path / "expf_check.hip", tmp_path, tmp_path / "expf_check")
     total = 0
     for first, last, stride in RANGES[:2]:
         rc, n, nbad, _ = run(str(exe), first, last, stride)

@@ -90,15 +90,13 @@ def test_specialised_paths_refuse_other_layouts(typed_layer, path):
     assert e.value.status == api._lib.ERR_QTYPE
 
 
-def test_mixed_stack_matches_oracle():
-    """Layers 0 and 2 have the decode kernel's types, 1 and 3 not: one
-    bread_moe_decode_layers call runs layer 0, layer 1 (per-token), layer 2,
-    layer 3 (per-token) on one token; then 3 tokens (one stack launch each)
-    and bread_stack_loop_tokens() + 1 tokens (batched calls per layer)
-    through bread_moe_stack_forward."""
-    s = api.shape()
-    L = 4
-    types = [api.STANDARD_TYPES, LAYOUTS["q4_down"], api.STANDARD_TYPES, LAYOUTS["mixed"]]
+def mixed_stack(s, types):
+    """Arena layers of the given types with seeded weights and non-unit norm
+    weights; returns the arena, the descriptors, oracle_stack(h0), which runs
+    the stack on the host (RMSNorm, then the layer) for every row, and the
+    device norm weights the descriptors point at (the caller keeps them
+    alive while it uses the descriptors)."""
+    L = len(types)
     arena = B.Arena(s, L)
     for l in range(L):
         arena.set_layer_types(l, types[l])
@@ -124,6 +122,18 @@ def test_mixed_stack_matches_oracle():
             ridx.append(np.asarray(ri).reshape(h.shape[0], -1))
         return h, np.stack(ridx)
 
+    return arena, descs, oracle_stack, nwd
+
+
+def test_mixed_stack_matches_oracle():
+    """Layers 0 and 2 have the decode kernel's types, 1 and 3 not: one
+    bread_moe_decode_layers call runs layer 0, layer 1 (per-token), layer 2,
+    layer 3 (per-token) on one token; then 3 tokens (one stack launch each)
+    and bread_stack_loop_tokens() + 1 tokens (batched calls per layer)
+    through bread_moe_stack_forward."""
+    s = api.shape()
+    types = [api.STANDARD_TYPES, LAYOUTS["q4_down"], api.STANDARD_TYPES, LAYOUTS["mixed"]]
+    arena, descs, oracle_stack, nwd = mixed_stack(s, types)
     TB = B.lib.bread_stack_loop_tokens() + 1
     ctx = B.MoeContext(s, max_tokens=TB)
     h0 = xs(1, s.hidden, 18)
@@ -144,6 +154,38 @@ def test_mixed_stack_matches_oracle():
         assert_moe_close(hd3.cpu().numpy(), href3, base=h3)
     assert ctx.check_device() == 0
     arena.close()
+    del nwd
+
+
+def test_mixed_stack_other_shape_applies_each_layer_once():
+    """A stack the decode kernel does not take (hidden 1024) whose first
+    layer has other weight types.  The decode-run launcher refuses the whole
+    stack before running any layer, so bread_moe_stack_forward's fallback
+    (one batched call per layer) starts from the caller's hidden and applies
+    every layer once; bread_moe_decode_layers returns BREAD_ERR_SHAPE with
+    hidden untouched."""
+    s = api.shape(hidden=1024)
+    types = [LAYOUTS["q4_down"], api.STANDARD_TYPES, LAYOUTS["mixed"], api.STANDARD_TYPES]
+    arena, descs, oracle_stack, nwd = mixed_stack(s, types)
+    ctx = B.MoeContext(s, max_tokens=3)
+    for T in (1, 3):
+        h0 = xs(T, s.hidden, 40 + T)
+        hd = dev(h0)
+        idx, _, _ = ctx.stack_forward(descs, hd, T, want_routing=True)
+        torch.cuda.synchronize()
+        href, ridx = oracle_stack(h0)
+        assert np.array_equal(idx.cpu().numpy().reshape(ridx.shape), ridx), T
+        assert_moe_close(hd.cpu().numpy(), href, base=h0)
+    h1 = xs(1, s.hidden, 45)
+    hd1 = dev(h1)
+    with pytest.raises(B.BreadError) as e:
+        ctx.decode_layers(descs, hd1)
+    assert e.value.status == api._lib.ERR_SHAPE
+    torch.cuda.synchronize()
+    assert np.array_equal(hd1.cpu().numpy(), h1)
+    assert ctx.check_device() == 0
+    arena.close()
+    del nwd
 
 
 def test_gguf_mixed_types_load_and_match(tmp_path):

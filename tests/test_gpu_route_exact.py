@@ -209,3 +209,68 @@ def test_bulk_paths_route_bit_exact(base, path, T, chunks):
     assert int(np.sum(np.any(gi != ri, axis=1))) == 0
     assert int(np.sum(np.any(gw.view(np.uint32) != rw.view(np.uint32), axis=1))) == 0
     assert ctx.check_device() == 0
+
+
+@pytest.mark.parametrize("router_std", [0.02, 1.0 / np.sqrt(2048)])
+def test_bulk_decode_route_bit_exact(base, router_std):
+    """4,096 tokens, each through a single-layer launch of the decode kernel
+    (fast logits, certified ranks, reference-order recomputation when the
+    certificate fails): indices bit-identical to the oracle's for every
+    token, and the certificate's outcomes counted once per launch."""
+    s, _ = base
+    lt = bulk_layer(base, router_std, 21)
+    hl = host_layer(lt)
+    T = 4096
+    x = np.random.default_rng(22).standard_normal((T, s.hidden)).astype(np.float32)
+    xd = dev(x)
+    ctx = B.MoeContext(s, max_tokens=1)
+    ctx.set_path(api.PATH_DECODE)
+    ctx.route_stats(reset=True)
+    hid = torch.zeros(1, s.hidden, device=DEV)
+    gis = []
+    for t in range(T):
+        idx, _, _ = ctx.forward(lt.desc(), xd[t:t + 1], hid, 1, want_routing=True)
+        gis.append(idx)
+    torch.cuda.synchronize()
+    gi = torch.cat(gis).cpu().numpy()
+    ri, _, _ = O.route_batch(hl, x, nthreads=16)
+    bad = int(np.sum(np.any(gi != ri, axis=1)))
+    st = ctx.route_stats()
+    print(f"router std {router_std:.4f}: {st}", flush=True)
+    assert bad == 0, f"{bad} of {T} tokens routed differently"
+    assert st["decode_radius"] + st["decode_per_expert"] + st["decode_pair"] + st["decode_exact"] == T
+    assert ctx.check_device() == 0
+
+
+def test_decode_wide_logit_spread_routes_exactly(base):
+    """One logit at 60 and the others between -55 and -46, not in index
+    order.  The reference's probabilities below the first underflow to 0 and
+    tie, so cpu_topk takes the lowest indices; the fast logits order them
+    otherwise.  The certificate must not vouch for ranks whose probabilities
+    are not normal floats: the decode kernel recomputes every logit in the
+    reference's order and selects what the reference selects."""
+    s, t = base
+    E, H, K = s.n_experts, s.hidden, s.top_k
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal(H).astype(np.float32)
+    xx = np.float32(np.dot(x.astype(np.float64), x.astype(np.float64)))
+    target = (-46.0 - 9.0 * rng.random(E)).astype(np.float32)   # expf(l - 60) underflows to 0
+    top = 100
+    target[top] = 60.0
+    router = (target[:, None] * (x / xx)[None, :]).astype(np.float32)
+    lt = layer_with_router(t, s, router)
+    hl = host_layer(lt)
+    ri, _, _, lg = O.route(hl, x, want_logits=True)
+    rest = [e for e in range(E) if e != top]
+    assert ri[0] == top and list(ri[1:]) == rest[:K - 1], "reference ties the underflowed probabilities"
+    by_logit = np.lexsort((np.arange(E), -lg.astype(np.float64)))[:K]
+    assert not np.array_equal(by_logit, ri), "the logit order must differ from the reference's choice"
+    assert lg.max() - np.sort(lg)[-K] > 104.0
+    ctx = B.MoeContext(s, max_tokens=1)
+    ctx.set_path(api.PATH_DECODE)
+    hid = torch.zeros(1, H, device=DEV)
+    idx, _, _ = ctx.forward(lt.desc(), dev(x[None]), hid, 1, want_routing=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(idx.cpu().numpy()[0], ri), f"{idx.cpu().numpy()[0]} vs oracle {ri}"
+    assert ctx.route_stats()["decode_exact"] == 1
+    assert ctx.check_device() == 0

@@ -11,6 +11,9 @@ Checked:
     weights, shared-gate logit) and the final hidden state.  The stack
     launch's 40-entry layer table and its epoch-tagged exchange state (5,120
     layer epochs on one context here) must not change a single bit;
+  - every token's routing on all 40 layers (5,120 layer-tokens through the
+    decode kernel's certified routing) against the route-only oracle, indices
+    bit-exact, with the certificate's outcomes counted once per layer-token;
   - every 16th token against the oracle on all 40 layers: routed indices
     bit-exact, each layer's output within the north-star tolerance.  Routed
     experts are copied back from the arena only when a token selects them.
@@ -85,6 +88,8 @@ def test_stack40_128_tokens(stack40):
                              np.zeros(E * b["down_expert"], np.uint8))
     rng = np.random.default_rng(128)
     distinct = set()
+    all_in, all_idx = [], []
+    ctx_stack.route_stats(reset=True)
     for t in range(TOKENS):
         h0 = rng.standard_normal((1, H)).astype(np.float32)
         ha = torch.from_numpy(h0).to(DEV)
@@ -107,9 +112,11 @@ def test_stack40_128_tokens(stack40):
         assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32)), f"token {t}: shared-gate logits differ"
         assert torch.equal(ha, hb), f"token {t}: stack and chained hidden differ"
         distinct.update(ia.reshape(-1).tolist())
+        hin = torch.cat(ins).cpu().numpy()
+        all_in.append(hin)
+        all_idx.append(ia)
         if t % SAMPLE_EVERY:
             continue
-        hin = torch.cat(ins).cpu().numpy()
         hout = np.concatenate([hin[1:], hb.cpu().numpy()])
         for l in range(L):
             xr = O.rms_norm_weighted(hin[l], nws[l], s.rms_eps)
@@ -119,6 +126,17 @@ def test_stack40_128_tokens(stack40):
             assert np.array_equal(ri[0], ia[l]), f"token {t} layer {l}: {ia[l]} vs oracle {ri[0]}"
             np.testing.assert_allclose(wa[l], rw[0], rtol=2e-5, atol=1e-7)
             assert_moe_close(hout[l], ref[0], base=hin[l])
+    # every layer-token's routing against the route-only oracle
+    st = ctx_stack.route_stats()
+    print(f"stack routing outcomes: {st}", flush=True)
+    assert sum(st.values()) == TOKENS * L
+    hins, idxs = np.stack(all_in), np.stack(all_idx)    # [TOKENS][L][H], [TOKENS][L][K]
+    bad = 0
+    for l in range(L):
+        xr = np.stack([O.rms_norm_weighted(hins[t, l], nws[l], s.rms_eps) for t in range(TOKENS)])
+        ri, _, _ = O.route_batch(sparse.load(descs[l], []), xr, nthreads=16)
+        bad += int(np.sum(np.any(ri != idxs[:, l], axis=1)))
+    assert bad == 0, f"{bad} of {TOKENS * L} layer-tokens routed differently"
     assert ctx_stack.check_device() == 0 and ctx_chain.check_device() == 0
     # routing varies over layers and tokens (logits ~ N(0, 1))
     assert len(distinct) > E // 2
