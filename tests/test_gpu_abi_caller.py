@@ -11,8 +11,9 @@ its own that links libbread_moe.so directly.
 - the MoE block at the decode kernel's shape (H 2048, I 512, 32 experts,
   top 8, unit-scale superblocks): normed input within one fp16 ulp of the
   oracle's RMSNorm, routing bit-exact against the oracle on that input, and
-  the fp16 residual within one fp16 ulp of the oracle's fp32 block rounded
-  to fp16.
+  the block's contribution to the fp16 residual within the north-star
+  tolerance (1e-3 relative L2, 1e-2 max-abs of its RMS) of the oracle's fp32
+  block, plus the one rounding of the result to fp16.
 """
 import os
 import subprocess
@@ -89,7 +90,13 @@ def test_caller_moe_block_f16(tmp_path):
     ref = h16.astype(np.float32)[None].copy()
     ri, _, _ = O.moe_forward(hl, x, ref, 1, nthreads=16)
     assert np.array_equal(gi, np.asarray(ri).reshape(-1)), f"{gi} vs oracle {ri}"
-    contrib = float(np.sqrt(np.mean((ref[0] - h16.astype(np.float32)).astype(np.float64) ** 2)))
-    assert 0.1 < contrib < 1e3
-    d = np.abs(got_h.astype(np.float64) - ref[0].astype(np.float16).astype(np.float64))
-    assert np.all(d <= ulp16(ref[0])), float(np.max(d / ulp16(ref[0])))
+    # the block's contribution within the north-star tolerance of the
+    # oracle's fp32 block, plus the one rounding of the result to fp16
+    base = h16.astype(np.float64)
+    got_c, ref_c = got_h.astype(np.float64) - base, ref[0].astype(np.float64) - base
+    rms = float(np.sqrt(np.mean(ref_c ** 2)))
+    assert 0.1 < rms < 1e3
+    half_ulp = 0.5 * ulp16(ref[0])
+    rel = float(np.linalg.norm(got_c - ref_c) / np.linalg.norm(ref_c))
+    assert rel < 1e-3 + float(np.linalg.norm(half_ulp) / np.linalg.norm(ref_c)), rel
+    assert np.all(np.abs(got_c - ref_c) <= 1e-2 * rms + half_ulp)
