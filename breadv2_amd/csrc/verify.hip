@@ -15,6 +15,8 @@
 //   bread_spec_accept        the acceptance rule of :477-497 on the host.
 #include <math.h>
 
+#include <algorithm>
+
 #include "bread_device.h"
 #include "bread_internal.h"
 
@@ -94,6 +96,317 @@ __global__ __launch_bounds__(AM_THREADS) void k_argmax_f16(const uint16_t *__res
         for (int wv = 1; wv < AM_THREADS / WAVE; wv++) am_merge(bv, bi, sv[wv], si[wv]);
         out[blockIdx.x] = (bi < 0 || isnan(h2f(lt[0]))) ? 0 : bi;
     }
+}
+
+// ---------------------------------------------------------------------------
+// Batched greedy head: the lm_head for T <= 32 tokens in one pass over its
+// Q4_K weights (main.cu:297-319 runs one bread_matvec per token; a verify
+// round of main_speculative.cu:477-497 runs B of them), with the argmax of
+// each token's logits (greedy_sample, main.cu:326-335) folded in.
+//
+// A Q4_K weight is d sc_j q - dmin m_j in sub-block j (32 elements), so a
+// superblock's dot product with x is d D - dmin M, D = sum sc_j q x and
+// M = sum_j m_j X_j, X_j the sum of x over sub-block j.  D runs on
+// v_mfma_f32_16x16x32_f16 with tokens as the M side and 16 weight rows as
+// the N side: the B operand is sc q (exact in fp16, <= 945, from the nibble
+// by a byte permutation and one packed fp16 fma), the A operand the fp16 x
+// (exact), the products exact and the sums fp32.  M runs on two
+// v_mfma_f32_16x16x4_f32 (X_j fp32, m_j exact).
+//
+// Lanes: lane l holds token / weight row c = l % 16 and quarter g = l / 16.
+// From weight row c it reads the superblock's 16-byte head and qs bytes
+// [32 g, 32 g + 32): the low nibbles are elements 64 g + e of the
+// superblock (sub-block 2 g), the high nibbles 64 g + 32 + e (sub-block
+// 2 g + 1).  Eight MFMAs take 8 of these elements each, so MFMA i covers
+// elements 64 g + 8 i .. + 7 in quarter g; the x fragments follow the same
+// order (a relabelling of K that A and B share), and so the lane also holds
+// x over sub-blocks 2 g and 2 g + 1 of its token, whose sums are its X_j.
+// The D layout puts tokens 4 g + i of row c in lane l, where the row's d
+// and dmin are.
+//
+// Workgroup: HD_MAXSB compute waves, wave w owning superblock w (a K slice)
+// of every row with its x fragments in registers for the whole launch, and
+// HD_NRED reducing waves.  Workgroups take 16-row tiles in turn, one barrier
+// a tile.  A compute wave keeps DEPTH tiles of its superblock column in a
+// register ring, loading tile k + DEPTH - 1 while it computes tile k (the
+// compiler's own vmcnt waits); its partial sums go to LDS, double-buffered.
+// The reducing waves sum the partials, round to fp16, store the logits and
+// keep a running argmax per token while the compute waves work on the next
+// tile.  (Staging tiles in LDS with direct-to-LDS loads gave stale data now
+// and then: a slot read right after the issuing wave's vmcnt drained and a
+// barrier did not always hold the loaded bytes yet.)
+// ---------------------------------------------------------------------------
+typedef _Float16 hd_half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 hd_half2 __attribute__((ext_vector_type(2)));
+typedef float hd_f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int HD_MAXSB = 8;           // superblocks a row (H <= 2048): one compute wave each
+constexpr int HD_MAXT = 32;           // tokens a launch (two 16-token tiles)
+constexpr int HD_NRED = 4;            // reducing waves: one thread per (token, row) of a 16 x 16 tile
+constexpr int HD_THREADS = 64 * (HD_MAXSB + HD_NRED);
+// register ring slots a compute wave (tiles in flight + 1), for one and two
+// 16-token tiles (two hold twice the x fragments)
+constexpr int HD_DEPTH1 = 4, HD_DEPTH2 = 3;
+constexpr int HD_GRID = 256;          // workgroups: one a CU (12 waves of up to 168 VGPRs)
+constexpr uint32_t HD_MAGIC = 0x64646464u;  // fp16 0x64xx = 1024 + xx
+
+// Four nibbles (bytes of v, each < 16) as two packed fp16 pairs of sc * q.
+__device__ __forceinline__ void hd_scq(uint32_t v, hd_half2 sc, hd_half2 nsc, uint32_t &p0, uint32_t &p1)
+{
+    const hd_half2 a = __builtin_bit_cast(hd_half2, __builtin_amdgcn_perm(HD_MAGIC, v, 0x07010700u));
+    const hd_half2 b = __builtin_bit_cast(hd_half2, __builtin_amdgcn_perm(HD_MAGIC, v, 0x07030702u));
+    p0 = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(a, sc, nsc));  // (1024 + q) sc - 1024 sc
+    p1 = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(b, sc, nsc));
+}
+
+// Eight consecutive elements' sc * q: the low (hi = 0) or high nibbles of
+// the bytes in (a, b).
+__device__ __forceinline__ hd_half8 hd_b8(uint32_t a, uint32_t b, int hi, hd_half2 sc, hd_half2 nsc)
+{
+    uint4 r;
+    hd_scq((a >> (4 * hi)) & 0x0F0F0F0Fu, sc, nsc, r.x, r.y);
+    hd_scq((b >> (4 * hi)) & 0x0F0F0F0Fu, sc, nsc, r.z, r.w);
+    return __builtin_bit_cast(hd_half8, r);
+}
+
+// A workgroup barrier that publishes the waves' LDS writes but leaves their
+// global loads in flight (__syncthreads would wait for every outstanding
+// load, the ring's tiles ahead included).  The asm memory clobber and the
+// scheduling barrier keep LDS accesses and the ring's loads on their side.
+__device__ __forceinline__ void hd_bar()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maxima
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// A lane's head and qs quarters of one superblock (row c, quarter g).
+struct HdRaw {
+    uint4 head;  // d, dmin, scales
+    uint4 q0;    // qs bytes [32 g, 32 g + 16)
+    uint4 q1;    // qs bytes [32 g + 16, 32 g + 32)
+};
+
+__device__ __forceinline__ void hd_load(HdRaw &r, const uint8_t *sb, int g)
+{
+    r.head = *reinterpret_cast<const uint4 *>(sb);
+    r.q0 = *reinterpret_cast<const uint4 *>(sb + 16 + 32 * g);
+    r.q1 = *reinterpret_cast<const uint4 *>(sb + 32 + 32 * g);
+}
+
+template <int NTT, int DEPTH>
+__global__ __launch_bounds__(HD_THREADS) void k_head_q4k(const uint8_t *__restrict__ w,
+                                                         const uint16_t *__restrict__ x16,
+                                                         uint16_t *__restrict__ logits, float *__restrict__ part_v,
+                                                         int32_t *__restrict__ part_i, int vocab, int H, int T)
+{
+    __shared__ float part[2][HD_MAXSB][NTT * 16][17];  // [buffer][superblock][tt, token][row]
+    const int NSB = H / 256;
+    const int wv = wave_id(), l = lane_id();
+    const size_t row_bytes = (size_t)NSB * Q4K_BYTES;
+    const int ntile = vocab / 16;
+    const int G = gridDim.x;
+    const int niter = ((int)blockIdx.x < ntile) ? (ntile - 1 - (int)blockIdx.x) / G + 1 : 0;
+    if (wv < HD_MAXSB) {
+        if (wv >= NSB) {  // no superblock: keep the barrier count
+            for (int it = 0; it < niter; it++) hd_bar();
+            return;
+        }
+        const int g = l >> 4, c = l & 15;
+        // x fragments of token 16 tt + c (zero beyond T): MFMA i takes
+        // elements 256 wv + 64 g + 8 i .. + 7; xm = the sums over sub-blocks
+        // 2 g and 2 g + 1
+        uint4 xf[NTT][8];
+        float xm[NTT][2];
+#pragma unroll
+        for (int tt = 0; tt < NTT; tt++) {
+            const int t = 16 * tt + c;
+            xm[tt][0] = xm[tt][1] = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                xf[tt][i] = t < T ? *reinterpret_cast<const uint4 *>(x16 + (size_t)t * H + 256 * wv + 64 * g + 8 * i)
+                                  : make_uint4(0u, 0u, 0u, 0u);
+                const uint32_t v[4] = {xf[tt][i].x, xf[tt][i].y, xf[tt][i].z, xf[tt][i].w};
+#pragma unroll
+                for (int k = 0; k < 4; k++) xm[tt][i >> 2] += h2f(v[k] & 0xFFFFu) + h2f(v[k] >> 16);
+            }
+        }
+        // tile it's column; past the workgroup's last tile that one again
+        // (an L2 hit): loads without a condition keep the compiler's vmcnt
+        // waits counted rather than draining
+        const uint8_t *wcol = w + (size_t)c * row_bytes + (size_t)wv * Q4K_BYTES;  // row c of tile 0
+        auto load = [&](HdRaw &r, int it) {
+            const int ti = (int)blockIdx.x + std::min(it, niter - 1) * G;
+            hd_load(r, wcol + (size_t)16 * ti * row_bytes, g);
+        };
+        HdRaw ring[DEPTH];
+#pragma unroll
+        for (int k = 0; k < DEPTH - 1; k++) load(ring[k], k);
+        for (int it0 = 0; it0 < niter; it0 += DEPTH) {
+#pragma unroll
+            for (int k = 0; k < DEPTH; k++) {
+                const int it = it0 + k;
+                if (it >= niter) break;
+                load(ring[(k + DEPTH - 1) % DEPTH], it + DEPTH - 1);
+                const HdRaw &b = ring[k];
+                const float d = h2f(b.head.x & 0xFFFFu), dmin = h2f(b.head.x >> 16);
+                uint32_t sc0, m0, sc1, m1;
+                scale_min_k4(2 * g, b.head.y, b.head.z, b.head.w, sc0, m0);
+                scale_min_k4(2 * g + 1, b.head.y, b.head.z, b.head.w, sc1, m1);
+                const _Float16 s0 = (_Float16)(float)sc0, s1 = (_Float16)(float)sc1;
+                const _Float16 n0 = (_Float16)(-1024.f * (float)sc0), n1 = (_Float16)(-1024.f * (float)sc1);
+                const hd_half2 S0{s0, s0}, N0{n0, n0}, S1{s1, s1}, N1{n1, n1};
+                const hd_half8 bq[8] = {hd_b8(b.q0.x, b.q0.y, 0, S0, N0), hd_b8(b.q0.z, b.q0.w, 0, S0, N0),
+                                        hd_b8(b.q1.x, b.q1.y, 0, S0, N0), hd_b8(b.q1.z, b.q1.w, 0, S0, N0),
+                                        hd_b8(b.q0.x, b.q0.y, 1, S1, N1), hd_b8(b.q0.z, b.q0.w, 1, S1, N1),
+                                        hd_b8(b.q1.x, b.q1.y, 1, S1, N1), hd_b8(b.q1.z, b.q1.w, 1, S1, N1)};
+#pragma unroll
+                for (int tt = 0; tt < NTT; tt++) {
+                    hd_f32x4 acc = {0.f, 0.f, 0.f, 0.f}, accm = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int i = 0; i < 8; i++)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(hd_half8, xf[tt][i]), bq[i],
+                                                                     acc, 0, 0, 0);
+                    accm = __builtin_amdgcn_mfma_f32_16x16x4f32(xm[tt][0], (float)m0, accm, 0, 0, 0);
+                    accm = __builtin_amdgcn_mfma_f32_16x16x4f32(xm[tt][1], (float)m1, accm, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        part[it & 1][wv][16 * tt + 4 * g + i][c] = d * acc[i] - dmin * accm[i];
+                }
+                hd_bar();
+            }
+        }
+        return;
+    }
+    // reducing waves: thread r sums output (tt, token, row) = (r / 256 + k,
+    // (r / 16) % 16, r % 16) for k = 0 .. NTT - 1
+    const int r = (int)threadIdx.x - 64 * HD_MAXSB, row = r & 15, tok = r >> 4;
+    float best[NTT];
+    int besti[NTT];
+#pragma unroll
+    for (int tt = 0; tt < NTT; tt++) {
+        best[tt] = 0.f;
+        besti[tt] = -1;
+    }
+    // the barrier after tile it's partials are in part[it & 1]; reduced
+    // while the compute waves work on tile it + 1
+    for (int it = 0; it < niter; it++) {
+        hd_bar();
+        const int ti = (int)blockIdx.x + it * G;
+#pragma unroll
+        for (int tt = 0; tt < NTT; tt++) {
+            const int t = 16 * tt + tok;
+            if (t >= T) continue;  // uniform over each 16-lane row group
+            float v = 0.f;
+            for (int sbi = 0; sbi < NSB; sbi++) v += part[it & 1][sbi][16 * tt + tok][row];
+            const uint16_t h = f2h(v);
+            logits[(size_t)t * vocab + 16 * ti + row] = h;
+            // greedy_sample's order: the largest non-NaN value, the lowest
+            // index among equals
+            const float vf = h2f(h);
+            float bv = vf;
+            int bi = vf == vf ? 16 * ti + row : -1;
+#pragma unroll
+            for (int off = 8; off > 0; off >>= 1) {
+                const float ov = __shfl_xor(bv, off, 16);
+                const int oi = __shfl_xor(bi, off, 16);
+                if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+                    bv = ov;
+                    bi = oi;
+                }
+            }
+            if (bi >= 0 && (besti[tt] < 0 || bv > best[tt])) {
+                best[tt] = bv;
+                besti[tt] = bi;
+            }
+        }
+    }
+#pragma unroll
+    for (int tt = 0; tt < NTT; tt++) {
+        const int t = 16 * tt + tok;
+        if (row == 0 && t < T) {
+            part_v[(size_t)t * G + blockIdx.x] = best[tt];
+            part_i[(size_t)t * G + blockIdx.x] = besti[tt];
+        }
+    }
+}
+
+// Token t's argmax from the workgroups' partials: the largest value, the
+// lowest index among equals; 0 when logits[t][0] is NaN (greedy_sample keeps
+// index 0 then) or no value is a number.
+__global__ __launch_bounds__(256) void k_head_argmax_merge(const float *__restrict__ part_v,
+                                                           const int32_t *__restrict__ part_i, int nparts,
+                                                           const uint16_t *__restrict__ logits, int vocab,
+                                                           int32_t *__restrict__ out)
+{
+    __shared__ float sv[256 / WAVE];
+    __shared__ int si[256 / WAVE];
+    const int t = blockIdx.x;
+    float bv = 0.f;
+    int bi = -1;
+    for (int p = threadIdx.x; p < nparts; p += 256) {
+        const float v = part_v[(size_t)t * nparts + p];
+        const int i = part_i[(size_t)t * nparts + p];
+        if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) {
+            bv = v;
+            bi = i;
+        }
+    }
+    for (int off = WAVE / 2; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (lane_id() == 0) {
+        sv[threadIdx.x / WAVE] = bv;
+        si[threadIdx.x / WAVE] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 256 / WAVE; k++)
+            if (si[k] >= 0 && (bi < 0 || sv[k] > bv || (sv[k] == bv && si[k] < bi))) {
+                bv = sv[k];
+                bi = si[k];
+            }
+        out[t] = (bi < 0 || isnan(h2f(logits[(size_t)t * vocab]))) ? 0 : bi;
+    }
+}
+
+// The batched head over tokens [0, T) in chunks of HD_MAXT, each chunk one
+// pass over the weights.  The workgroups' argmax partials live in the
+// context's SwiGLU buffer (free between MoE calls on the stream).
+int launch_head_q4k(bread_moe_ctx_t *c, const uint8_t *w, const uint16_t *x16, int vocab, int T, uint16_t *logits,
+                    int32_t *tokens, hipStream_t st)
+{
+    const int H = c->shape.hidden;
+    const int Imax = c->shape.expert_inter > c->shape.shared_inter ? c->shape.expert_inter : c->shape.shared_inter;
+    const size_t h_floats = (size_t)c->max_tokens * (c->shape.top_k + 1) * Imax;
+    const int tmax = std::min(T, HD_MAXT);
+    const int grid = (int)std::min<size_t>((size_t)std::min(vocab / 16, HD_GRID), h_floats / (2 * (size_t)tmax));
+    if (grid < 1) return bread_fail(BREAD_ERR_CAPACITY, "bread_moe_greedy_head", "no room for the argmax partials");
+    for (int t0 = 0; t0 < T; t0 += HD_MAXT) {
+        const int tn = std::min(HD_MAXT, T - t0);
+        float *pv = c->h;
+        int32_t *pi = reinterpret_cast<int32_t *>(c->h + (size_t)tn * grid);
+        bread_clear_stale_error();
+        if (tn > 16)
+            hipLaunchKernelGGL((k_head_q4k<2, HD_DEPTH2>), dim3(grid), dim3(HD_THREADS), 0, st, w, x16 + (size_t)t0 * H,
+                               logits + (size_t)t0 * vocab, pv, pi, vocab, H, tn);
+        else
+            hipLaunchKernelGGL((k_head_q4k<1, HD_DEPTH1>), dim3(grid), dim3(HD_THREADS), 0, st, w, x16 + (size_t)t0 * H,
+                               logits + (size_t)t0 * vocab, pv, pi, vocab, H, tn);
+        BREAD_HIP(hipGetLastError());
+        hipLaunchKernelGGL(k_head_argmax_merge, dim3(tn), dim3(256), 0, st, pv, pi, grid,
+                           logits + (size_t)t0 * vocab, vocab, tokens + t0);
+        BREAD_HIP(hipGetLastError());
+    }
+    return BREAD_OK;
 }
 
 }  // namespace
@@ -207,6 +520,9 @@ extern "C" int bread_moe_greedy_head(bread_moe_ctx_t *c, const float *hidden, co
     bread_clear_stale_error();
     hipLaunchKernelGGL(k_norm_rows<uint16_t>, dim3(T), dim3(256), 0, st, hidden, norm_w, x16, H, c->shape.rms_eps);
     BREAD_HIP(hipGetLastError());
+    if (qtype == BREAD_QTYPE_Q4_K && H % 256 == 0 && H / 256 <= HD_MAXSB && vocab % 16 == 0 &&
+        ((uintptr_t)w_out & 15) == 0)
+        return launch_head_q4k(c, static_cast<const uint8_t *>(w_out), x16, vocab, T, logits, tokens, st);
     for (int t = 0; t < T; t++) {
         const int rc = bread_matvec(w_out, x16 + (size_t)t * H, logits + (size_t)t * vocab, vocab, H, qtype, stream);
         if (rc) return rc;

@@ -12,7 +12,11 @@
   fp16-weight rounding, ~4e-4 relative L2 per layer against ~2e-6 for the
   fp32 paths, so near-tied ranks may swap there);
 - bread_moe_greedy_head: fp16 logits within the bread_matvec bound of the
-  oracle's, tokens the argmax of those logits;
+  oracle's, tokens the argmax of those logits; the batched Q4_K head (one
+  pass over the weights for up to 32 tokens) on inputs whose fp16
+  normalisation is exact: every token's logits within one fp16 ulp plus the
+  fp32 order bound of the oracle's matvec on the same input, each token's
+  logits and token bit-equal to a one-token call's;
 - a verification round: the batched predictions equal the token-by-token
   ones (main_speculative.cu:477-497 runs bread_step per token), and
   bread_spec_accept accepts exactly the drafts that match them.
@@ -27,6 +31,7 @@ from breadv2_amd import api, synth
 from oracle import oracle as O
 
 from helpers import arena_host_layer, assert_moe_close
+from test_gpu_quant import abs_bound
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -197,6 +202,57 @@ def test_greedy_head(qtype, vocab):
         srt = np.sort(r[t])
         if srt[-1] - srt[-2] > 4 * float(np.max(np.abs(g[t] - r[t]))):
             assert tok[t] == O.greedy_f16(ref[t])
+
+
+@pytest.mark.parametrize("T", [1, 5, 16, 17, 32, 35])
+def test_greedy_head_batched_q4k(T):
+    s = api.shape()
+    H, vocab = s.hidden, 4096 + 16 * T
+    rng = np.random.default_rng(600 + T)
+    # h = +-1 and fp16-exact norm weights: x = h inv_rms w rounds to +-w in
+    # fp16 on any summation order (inv_rms = 1/sqrt(1 + eps) is within 5e-7
+    # of 1), so device and oracle start from the same x16
+    h = rng.choice([-1.0, 1.0], size=(T, H)).astype(np.float32)
+    nw = rng.choice([0.5, 0.75, 1.0, 1.25, 1.5], size=H).astype(np.float32)
+    w = head_weights(Q4K, vocab, H, seed=900 + T)
+    x16 = (h * nw[None]).astype(np.float16)
+    ctx = B.MoeContext(s, max_tokens=T)
+    wd, nwd = dev(w), dev(nw)
+    print(f"batched head T={T} vocab={vocab}", flush=True)
+    tok, lg = ctx.greedy_head(dev(h), nwd, wd, Q4K, vocab, T)
+    torch.cuda.synchronize()
+    tok, lg = tok.cpu().numpy(), lg.cpu().numpy()
+    assert ctx.check_device() == 0
+    for t in range(T):
+        ref = O.matvec_f16io(w, Q4K, x16[t].view(np.uint16), vocab, H).view(np.float16).astype(np.float64)
+        order = 2 * H * 2.0 ** -24 * abs_bound(w, Q4K, x16[t].astype(np.float32), vocab, H)
+        err = np.abs(lg[t].astype(np.float64) - ref)
+        assert np.all(err <= np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) + order + 1e-6), \
+            f"token {t}: max excess {float(np.max(err - order))}"
+        assert tok[t] == O.greedy_f16(lg[t])
+    # tokens are independent: the one-token call gives the same row and token
+    for t in sorted({0, T // 2, T - 1}):
+        t1, l1 = ctx.greedy_head(dev(h[t:t + 1]), nwd, wd, Q4K, vocab, 1)
+        assert np.array_equal(l1.cpu().numpy()[0].view(np.uint16), lg[t].view(np.uint16))
+        assert int(t1.cpu().numpy()[0]) == tok[t]
+
+
+def test_greedy_head_batched_nan_row():
+    """greedy_sample keeps index 0 when logits[0] is NaN: a NaN input token
+    gives an all-NaN row and token 0; the other tokens are unaffected."""
+    s = api.shape()
+    H, vocab, T = s.hidden, 2048, 3
+    rng = np.random.default_rng(77)
+    h = rng.standard_normal((T, H)).astype(np.float32)
+    h[1, 5] = np.nan
+    w = head_weights(Q4K, vocab, H, seed=78)
+    ctx = B.MoeContext(s, max_tokens=T)
+    tok, lg = ctx.greedy_head(dev(h), None, dev(w), Q4K, vocab, T)
+    torch.cuda.synchronize()
+    tok, lg = tok.cpu().numpy(), lg.cpu().numpy()
+    assert np.all(np.isnan(lg[1].astype(np.float32))) and tok[1] == 0
+    for t in (0, 2):
+        assert tok[t] == O.greedy_f16(lg[t]) and not np.any(np.isnan(lg[t].astype(np.float32)))
 
 
 def test_verify_round_matches_token_by_token(stack):
