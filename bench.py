@@ -379,6 +379,49 @@ def expert_block(arena, s, steps: int, stream, run_cpu: bool):
 
 
 VERIFY_B = (5, 9, 17)
+HEAD_T = (1, 5, 9, 16, 17, 32)
+
+
+def greedy_head(steps: int):
+    """bread_moe_greedy_head with the Q4_K lm_head (248,320 x 2048): output
+    RMSNorm, one pass over the weights for up to 32 tokens (k_head_q4k) and
+    the greedy argmax, for the token counts of verify rounds.  Two weight
+    copies alternated so reads come from HBM."""
+    import torch
+
+    import breadv2_amd as B
+    from breadv2_amd import api
+
+    s = api.shape()
+    H, V = s.hidden, 248_320
+    nb = V * H // 256 * 144
+    ws = [torch.empty(nb, dtype=torch.uint8, device="cuda:0") for _ in range(2)]
+    for i, w in enumerate(ws):
+        api.synth_q4k(w, V * H // 256, 77 + i)
+    nw = torch.ones(H, device="cuda:0")
+    ctx = B.MoeContext(s, max_tokens=max(HEAD_T))
+    out = []
+    for T in HEAD_T:
+        h = torch.randn(T, H, device="cuda:0", generator=torch.Generator("cuda:0").manual_seed(T))
+        for i in range(3):
+            ctx.greedy_head(h, nw, ws[i % 2], api.QTYPE_Q4_K, V, T)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            ctx.greedy_head(h, nw, ws[i % 2], api.QTYPE_Q4_K, V, T)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / steps
+        out.append({"tokens": T, "us_per_call": round(us, 1), "weight_bytes": nb,
+                    "weight_gbs": round(nb / us / 1e3, 1), "us_per_token": round(us / T, 2)})
+        log(f"greedy head T={T}: {us:.1f} us per call")
+    if ctx.check_device():
+        raise RuntimeError("greedy head flagged a device error")
+    ctx.close()
+    del ws
+    return out
 
 
 def verify(arena, s, rounds: int, stream):
@@ -457,6 +500,8 @@ def main() -> int:
                     help="config 1: timed cold 512 x 2048 Q4_K matvec launches (0 skips it)")
     ap.add_argument("--only-mt", action="store_true",
                     help="profiling aid: run only the configs 4/5 cases and print their JSON")
+    ap.add_argument("--only-head", action="store_true",
+                    help="profiling aid: run only the batched greedy head timings and print their JSON")
     ap.add_argument("--only-verify", action="store_true",
                     help="profiling aid: run only the speculative-verify rounds and print their JSON")
     ap.add_argument("--calib-copy", action="store_true",
@@ -475,6 +520,9 @@ def main() -> int:
     from breadv2_amd import api
 
     torch.cuda.set_device(0)
+    if args.only_head:
+        print(json.dumps({"greedy_head": greedy_head(20)}), flush=True)
+        return 0
     s = api.shape()
     L = args.layers
     log(f"allocating {L} resident layers")
@@ -650,6 +698,10 @@ def main() -> int:
         result["config1"] = config1(args.cfg1_steps, stream, run_cpu=not args.no_cpu)
     if args.mt_steps > 0:
         result["lm_head"] = {"entry": "bread_matvec (fp16 x/y)", "cases": lm_head(20)}
+        result["greedy_head"] = {
+            "entry": "bread_moe_greedy_head, Q4_K lm_head: norm + one weight pass for up to 32 tokens + argmax",
+            "cases": greedy_head(20),
+        }
         result["expert_block"] = expert_block(arena, s, 200, stream, not args.no_cpu)
     if args.mt_steps > 0 and L >= 40:
         result["verify"] = {
