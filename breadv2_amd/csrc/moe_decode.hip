@@ -473,19 +473,6 @@ struct Sel {
     uint32_t k0, k1, k2, k3;  // packed keys, descending
 };
 
-// Selection key of a fast logit: its bits mapped so that unsigned order is
-// numeric order, dropped to 30 bits (2 or more; NaN 1).  The passes order
-// the fast logits themselves, not their probabilities: a softmax is
-// monotone, and the certificate only vouches for ranks whose logits are far
-// more than the 4 ulps this drops apart, so the probabilities the reference
-// computes order them the same way.
-__device__ __forceinline__ uint32_t logit_key(float l)
-{
-    if (l != l) return 1u;
-    const uint32_t u = __builtin_bit_cast(uint32_t, l);
-    return ((u & 0x80000000u) ? ~u : (u | 0x80000000u)) >> 2;
-}
-
 __device__ __forceinline__ void cswap(uint32_t &a, uint32_t &b)
 {
     const uint32_t hi = umax32(a, b), lo = a ^ b ^ hi;

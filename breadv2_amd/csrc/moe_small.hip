@@ -86,33 +86,20 @@ __device__ __forceinline__ void load_row4(const float *p, int lane, int nm, floa
         v[m] = m < nm ? *reinterpret_cast<const float4 *>(p + 4 * lane + 256 * m) : make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
-// Softmax / top-k per token (the host's arithmetic, topk_wave_exact), then the
-// experts chosen by any token numbered into slots in expert order (slot 0 is
-// the shared expert with every token), each slot with its (token, rank)
-// pairs in token order, from per-expert token bitmasks.  One workgroup of
-// 1024 threads.
-template <int MAXV>
-__device__ void sb_select(const float *__restrict__ logits, int E, int K, int T, int32_t *__restrict__ idx,
-                          float *__restrict__ w, int32_t *__restrict__ slot_expert, int32_t *__restrict__ slot_cnt,
-                          int32_t *__restrict__ slot_pair, int32_t *__restrict__ n_slots)
+// The experts chosen by any token numbered into slots in expert order (the
+// shared expert's slots first, with every token), each slot with its
+// (token, rank) pairs in token order, from per-expert token bitmasks.
+// sidx[t K + k] (LDS): rank k's expert of token t, complete before the call.
+// One workgroup of RT_THREADS.
+__device__ void sb_number_slots(const int *sidx, int E, int K, int T, int32_t *__restrict__ slot_expert,
+                         int32_t *__restrict__ slot_cnt, int32_t *__restrict__ slot_pair,
+                         int32_t *__restrict__ n_slots)
 {
-    __shared__ int sidx[SB_MAX_T * MAX_K];
-    __shared__ __attribute__((aligned(16))) float s_e[RT_WAVES][WAVE * MAXV];  // softmax scratch of each wave
     __shared__ uint32_t mask[MAX_E];  // tokens that chose expert e
     __shared__ int slot_of[MAX_E];
     __shared__ int wave_tot[RT_WAVES];
     const int tid = (int)threadIdx.x, wv = tid / WAVE, lane = lane_id();
     for (int e = tid; e < E; e += RT_THREADS) mask[e] = 0u;
-    for (int t = wv; t < T; t += RT_WAVES) {
-        int ik;
-        float wk;
-        topk_wave_exact<MAXV>(logits + (size_t)t * E, E, K, s_e[wv], ik, wk);
-        if (lane < K) {
-            idx[(size_t)t * K + lane] = ik;
-            w[(size_t)t * K + lane] = wk;
-            sidx[t * K + lane] = ik;
-        }
-    }
     __syncthreads();
     const int P = T * K;
     for (int i = tid; i < P; i += RT_THREADS) {
@@ -162,6 +149,8 @@ __device__ void sb_select(const float *__restrict__ logits, int E, int K, int T,
     for (int t = tid; t < T; t += RT_THREADS) slot_pair[t] = t * (K + 1);  // slot t / SB_CH, place t % SB_CH
 }
 
+// Softmax / top-k per token with the host's arithmetic (topk_wave_exact) on
+// the reference-order logits, then the slots.  One workgroup.
 template <int MAXV>
 __global__ __launch_bounds__(RT_THREADS) void k_sb_select(const float *__restrict__ logits, int E, int K, int T,
                                                           int32_t *__restrict__ idx, float *__restrict__ w,
@@ -170,7 +159,112 @@ __global__ __launch_bounds__(RT_THREADS) void k_sb_select(const float *__restric
                                                           int32_t *__restrict__ slot_pair,
                                                           int32_t *__restrict__ n_slots)
 {
-    sb_select<MAXV>(logits, E, K, T, idx, w, slot_expert, slot_cnt, slot_pair, n_slots);
+    __shared__ int sidx[SB_MAX_T * MAX_K];
+    __shared__ __attribute__((aligned(16))) float s_e[RT_WAVES][WAVE * MAXV];  // softmax scratch of each wave
+    const int wv = (int)threadIdx.x / WAVE, lane = lane_id();
+    for (int t = wv; t < T; t += RT_WAVES) {
+        int ik;
+        float wk;
+        topk_wave_exact<MAXV>(logits + (size_t)t * E, E, K, s_e[wv], ik, wk);
+        if (lane < K) {
+            idx[(size_t)t * K + lane] = ik;
+            w[(size_t)t * K + lane] = wk;
+            sidx[t * K + lane] = ik;
+        }
+    }
+    __syncthreads();
+    sb_number_slots(sidx, E, K, T, slot_expert, slot_cnt, slot_pair, n_slots);
+}
+
+// Certified selection from the fast logits and radii (k_route_fast): wave v
+// takes tokens v, v + 16, ...; a token the certificate vouches for
+// (cert_select_wave) gets its experts and weights here, the others join the
+// list that k_route_seq_list sums again in the reference's order and
+// k_sb_select_list then selects.  With every token certified the slots are
+// numbered here as well.  Counts both outcomes in stats.  One workgroup.
+template <int MAXV>
+__global__ __launch_bounds__(RT_THREADS) void k_sb_select_cert(const float *__restrict__ logits,
+                                                               const float *__restrict__ radii, int E, int K, int T,
+                                                               int32_t *__restrict__ idx, float *__restrict__ w,
+                                                               int32_t *__restrict__ slot_expert,
+                                                               int32_t *__restrict__ slot_cnt,
+                                                               int32_t *__restrict__ slot_pair,
+                                                               int32_t *__restrict__ n_slots, int *__restrict__ list,
+                                                               int *__restrict__ list_n,
+                                                               uint32_t *__restrict__ stats)
+{
+    __shared__ int sidx[SB_MAX_T * MAX_K];
+    __shared__ int s_list[SB_MAX_T];
+    __shared__ int s_n;
+    const int tid = (int)threadIdx.x, wv = tid / WAVE, lane = lane_id();
+    if (tid == 0) s_n = 0;
+    __syncthreads();
+    for (int t = wv; t < T; t += RT_WAVES) {
+        int ik = 0;
+        float wk = 0.f;
+        if (cert_select_wave<MAXV>(logits + (size_t)t * E, radii + (size_t)t * E, E, K, ik, wk)) {
+            if (lane < K) {
+                idx[(size_t)t * K + lane] = ik;
+                w[(size_t)t * K + lane] = wk;
+                sidx[t * K + lane] = ik;
+            }
+        } else if (lane == 0) {
+            s_list[atomicAdd(&s_n, 1)] = t;
+        }
+    }
+    __syncthreads();
+    const int n = s_n;
+    if (tid < n) list[tid] = s_list[tid];
+    if (tid == 0) {
+        *list_n = n;
+        atomicAdd(&stats[BREAD_RSTAT_MT_CERT], (uint32_t)(T - n));
+        atomicAdd(&stats[BREAD_RSTAT_MT_EXACT], (uint32_t)n);
+    }
+    if (n == 0) sb_number_slots(sidx, E, K, T, slot_expert, slot_cnt, slot_pair, n_slots);
+}
+
+// After k_route_seq_list: the listed tokens selected with the host's
+// arithmetic on their reference-order logits, then the slots of every token
+// (the certified ones' experts as k_sb_select_cert wrote them).  Returns at
+// once when the list is empty.  One workgroup.
+template <int MAXV>
+__global__ __launch_bounds__(RT_THREADS) void k_sb_select_list(const float *__restrict__ logits, int E, int K,
+                                                               int T, int32_t *__restrict__ idx,
+                                                               float *__restrict__ w,
+                                                               int32_t *__restrict__ slot_expert,
+                                                               int32_t *__restrict__ slot_cnt,
+                                                               int32_t *__restrict__ slot_pair,
+                                                               int32_t *__restrict__ n_slots,
+                                                               const int *__restrict__ list,
+                                                               const int *__restrict__ list_n)
+{
+    __shared__ int sidx[SB_MAX_T * MAX_K];
+    __shared__ int listed[SB_MAX_T];
+    __shared__ __attribute__((aligned(16))) float s_e[RT_WAVES][WAVE * MAXV];
+    const int n_raw = __builtin_amdgcn_readfirstlane(*list_n);
+    if (n_raw <= 0) return;
+    const int n = n_raw < T ? n_raw : T;
+    const int tid = (int)threadIdx.x, wv = tid / WAVE, lane = lane_id();
+    if (tid < SB_MAX_T) listed[tid] = 0;
+    __syncthreads();
+    for (int i = wv; i < n; i += RT_WAVES) {
+        const int t = __builtin_amdgcn_readfirstlane(list[i]);
+        if (t < 0 || t >= T) continue;
+        int ik;
+        float wk;
+        topk_wave_exact<MAXV>(logits + (size_t)t * E, E, K, s_e[wv], ik, wk);
+        if (lane < K) {
+            idx[(size_t)t * K + lane] = ik;
+            w[(size_t)t * K + lane] = wk;
+            sidx[t * K + lane] = ik;
+        }
+        if (lane == 0) listed[t] = 1;
+    }
+    __syncthreads();
+    for (int i = tid; i < T * K; i += RT_THREADS)
+        if (!listed[i / K]) sidx[i] = idx[i];
+    __syncthreads();
+    sb_number_slots(sidx, E, K, T, slot_expert, slot_cnt, slot_pair, n_slots);
 }
 
 // ---- gate / up + SwiGLU ---------------------------------------------------------
@@ -1044,15 +1138,45 @@ int bread_launch_moe_small(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const
                      L->gate_expert_bytes, L->up_expert_bytes, L->down_expert_bytes};
     const SbSlots ss{g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots};
     bread_clear_stale_error();
-    // routing logits and shared-gate scores in the reference's order (route.hip)
-    int rc = bread_launch_route_logits(L->router, L->shexp_gate, x, c->logits, c->gsh, H, E, T, true, st);
-    if (rc) return rc;
-    if (E <= 4 * WAVE)
-        hipLaunchKernelGGL(k_sb_select<4>, dim3(1), dim3(RT_THREADS), 0, st, c->logits, E, K, T, c->idx, c->w,
-                           g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots);
-    else
-        hipLaunchKernelGGL(k_sb_select<16>, dim3(1), dim3(RT_THREADS), 0, st, c->logits, E, K, T, c->idx, c->w,
-                           g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots);
+    // routing (route.hip): fast logits with radii, the certificate and the
+    // selection of the tokens it vouches for, the reference's order and the
+    // host's selection for the rest (the last two return at once when no
+    // token is left); beyond the certified path's limits, the reference's
+    // order for every token
+    const bool mv4 = E <= 4 * WAVE;
+    if (bread_route_certified_ok(c, T)) {
+        const bread_route_cert_ws cw = bread_route_cert_buffers(c, T);
+        int rc = bread_launch_route_fast(c, L, x, T, c->gsh, cw.radii, st);
+        if (rc) return rc;
+        if (mv4)
+            hipLaunchKernelGGL(k_sb_select_cert<4>, dim3(1), dim3(RT_THREADS), 0, st, c->logits, cw.radii, E, K, T,
+                               c->idx, c->w, g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots, cw.list, cw.list_n,
+                               c->dsync->rstat.v);
+        else
+            hipLaunchKernelGGL(k_sb_select_cert<16>, dim3(1), dim3(RT_THREADS), 0, st, c->logits, cw.radii, E, K,
+                               T, c->idx, c->w, g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots, cw.list,
+                               cw.list_n, c->dsync->rstat.v);
+        BREAD_HIP(hipGetLastError());
+        rc = bread_launch_route_exact_list(c, L, x, T, c->gsh, cw.list, cw.list_n, st);
+        if (rc) return rc;
+        if (mv4)
+            hipLaunchKernelGGL(k_sb_select_list<4>, dim3(1), dim3(RT_THREADS), 0, st, c->logits, E, K, T, c->idx,
+                               c->w, g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots, cw.list, cw.list_n);
+        else
+            hipLaunchKernelGGL(k_sb_select_list<16>, dim3(1), dim3(RT_THREADS), 0, st, c->logits, E, K, T, c->idx,
+                               c->w, g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots, cw.list, cw.list_n);
+    } else {
+        const int rc =
+            bread_launch_route_logits(L->router, L->shexp_gate, x, c->logits, c->gsh, H, E, T, true, st);
+        if (rc) return rc;
+        if (mv4)
+            hipLaunchKernelGGL(k_sb_select<4>, dim3(1), dim3(RT_THREADS), 0, st, c->logits, E, K, T, c->idx, c->w,
+                               g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots);
+        else
+            hipLaunchKernelGGL(k_sb_select<16>, dim3(1), dim3(RT_THREADS), 0, st, c->logits, E, K, T, c->idx,
+                               c->w, g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots);
+    }
+    BREAD_HIP(hipGetLastError());
     if (H == SW_H && I == SW_I && Ish == SW_I && K <= SW_K && T <= SW_MAX_T) {
         // the decode shape: every workgroup owns a slice of every slot
         hipLaunchKernelGGL(k_sw_gateup, dim3(SW_G), dim3(SW_NT), 0, st, sl, x, ss, c->h, E, K, T, S);

@@ -64,6 +64,173 @@ __global__ __launch_bounds__(RS_WAVES * WAVE) void k_route_seq(const float *__re
     route_seq_block<NE>(S, (int)blockIdx.x, (int)blockIdx.y, router, shg, x, logits, gsh, H, E, T, shg_row != 0);
 }
 
+// The exact logits of the tokens list[0 .. *list_n) (the rest of the grid
+// returns at once): k_route_seq through a token list.
+template <int NE>
+__global__ __launch_bounds__(RS_WAVES * WAVE) void k_route_seq_list(const float *__restrict__ router,
+                                                                   const uint16_t *__restrict__ shg,
+                                                                   const float *__restrict__ x,
+                                                                   float *__restrict__ logits,
+                                                                   float *__restrict__ gsh, int H, int E, int T,
+                                                                   const int *__restrict__ list,
+                                                                   const int *__restrict__ list_n)
+{
+    __shared__ RsSmem S;
+    route_seq_block<NE>(S, (int)blockIdx.x, (int)blockIdx.y, router, shg, x, logits, gsh, H, E, T, true, list, list_n);
+}
+
+// ---------------------------------------------------------------------------
+// Certified fast routing for a few tokens.  The reference's sequential sums
+// (one_layer.cu:969-971) are a 2048-step dependent chain per logit; for a
+// few tokens the chain, not the data, sets the time of k_route_seq.  Here
+// every logit is first summed in parallel with a rigorous radius R >=
+// |fast - sequential|; a token whose top K, so widened, is strictly
+// separated (cert_select_wave, route_dev.h) keeps its fast logits, which
+// select the reference's experts in the reference's order; the other tokens
+// are summed again in the reference's order (k_route_seq_list) and selected
+// with the host's arithmetic.  Indices are exact either way; the weights of
+// certified tokens come from the fast logits (within the layer tolerance).
+//
+// k_route_fast: grid (E + 1, ceil(T / TT)); workgroup (r, g) takes router
+// row r (r = E: the fp16 shared gate, widened; its fast sums are the
+// shared-gate scores) for tokens TT g .. TT g + TT - 1, thread i the L = H / 256
+// consecutive columns [L i, L i + L) of every token: a fused multiply-add
+// chain gives the chunk sum p and a = sum |w x|; an inclusive scan of p over
+// the threads (in column order) gives every chunk's exact prefix P_i to
+// within gamma_{L+10} A, and the last prefix is the fast logit F.
+//
+// Radius.  With q_k = fl(w_k x_k), s*_k the reference's partial sums and S_k
+// the exact ones (A = sum |w_k x_k|, n = H):
+//   |s*_n - sum q| <= u sum |s*_k|,  |sum q - S_n| <= u A (+ n 2^-150),
+//   sum |s*_k| <= sum |S_k| + n gamma_n A,
+//   sum over chunk i of |S_k| <= L (|S_{Li}| + A_i),
+//   |S_{Li}| <= |P_i| + gamma_{L+10} A,  |F - S_n| <= gamma_{L+10} A,
+// so R = u (L SP + c A) with SP = sum_i |P_i| (exclusive prefixes) and
+// c = 2 L + 12 + n^2 u (the gamma terms for n <= 4096, L <= 16), widened by
+// 2^-10 for the fp32 evaluation and by 1e-37 for underflow.
+constexpr int CF_TT = 16;        // tokens per workgroup at most (TT)
+constexpr int CF_THREADS = 256;  // threads per router row
+constexpr int CF_WAVES = CF_THREADS / WAVE;
+constexpr int CF_MAX_T = 32;     // tokens per call (the small-batch path's limit)
+constexpr int CF_MAX_K = 16;
+
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float cf_dpp(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xF,
+                                                                 true));
+}
+
+// Inclusive prefix sum over the wave in lane order: row_shr 1, 2, 4, 8
+// inside the 16-lane rows (lanes without a source add 0), then each row's
+// total into the rows after it (row_bcast 15 and 31).
+__device__ __forceinline__ float cf_wave_scan(float v)
+{
+    v += cf_dpp<0x111, 0xF>(v);
+    v += cf_dpp<0x112, 0xF>(v);
+    v += cf_dpp<0x114, 0xF>(v);
+    v += cf_dpp<0x118, 0xF>(v);
+    v += cf_dpp<0x142, 0xA>(v);
+    v += cf_dpp<0x143, 0xC>(v);
+    return v;
+}
+
+template <int L, int TT>
+__global__ __launch_bounds__(CF_THREADS, 2) void k_route_fast(const float *__restrict__ router,
+                                                             const uint16_t *__restrict__ shg, int has_shg,
+                                                             const float *__restrict__ x, float *__restrict__ logits,
+                                                             float *__restrict__ radii, float *__restrict__ gsh,
+                                                             int H, int E, int T, float coef_a)
+{
+    static_assert(L % 4 == 0 && L <= 16 && TT <= CF_TT, "columns and tokens per thread");
+    __shared__ float s_tot[TT][CF_WAVES], s_sp[TT][CF_WAVES], s_a[TT][CF_WAVES];
+    const int tid = (int)threadIdx.x, wv = tid / WAVE, lane = lane_id();
+    const int r = (int)blockIdx.x, t0 = (int)blockIdx.y * TT;
+    const int nt = T - t0 < TT ? T - t0 : TT;
+    const bool gate = r == E;
+    const int c0 = L * tid;
+    // both the router row (row 0 for the gate workgroup) and the gate's
+    // columns are read (shg points at readable memory of H halves either
+    // way), so no load waits on a branch
+    float4 rv[L / 4];
+    uint2 hv[L / 4];
+#pragma unroll
+    for (int j = 0; j < L / 4; j++) {
+        rv[j] = reinterpret_cast<const float4 *>(router + (size_t)(gate ? 0 : r) * H + c0)[j];
+        hv[j] = reinterpret_cast<const uint2 *>(shg + c0)[j];
+    }
+    // every token's columns requested at once (positions past the last
+    // token read the last token again and are not stored)
+    float4 xv[TT][L / 4];
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+        const float *xt = x + (size_t)(t0 + (t < nt ? t : nt - 1)) * H + c0;
+#pragma unroll
+        for (int j = 0; j < L / 4; j++) xv[t][j] = reinterpret_cast<const float4 *>(xt)[j];
+    }
+    float w[L];
+#pragma unroll
+    for (int j = 0; j < L / 4; j++) {
+        const bool hz = gate && !has_shg;
+        w[4 * j] = gate ? (hz ? 0.f : h2f(hv[j].x)) : rv[j].x;
+        w[4 * j + 1] = gate ? (hz ? 0.f : h2f(hv[j].x >> 16)) : rv[j].y;
+        w[4 * j + 2] = gate ? (hz ? 0.f : h2f(hv[j].y)) : rv[j].z;
+        w[4 * j + 3] = gate ? (hz ? 0.f : h2f(hv[j].y >> 16)) : rv[j].w;
+    }
+    float inc[TT], a[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+        float p = 0.f, aa = 0.f;
+#pragma unroll
+        for (int j = 0; j < L / 4; j++) {
+            p = fmaf(w[4 * j], xv[t][j].x, p);
+            p = fmaf(w[4 * j + 1], xv[t][j].y, p);
+            p = fmaf(w[4 * j + 2], xv[t][j].z, p);
+            p = fmaf(w[4 * j + 3], xv[t][j].w, p);
+            aa = fmaf(fabsf(w[4 * j]), fabsf(xv[t][j].x), aa);
+            aa = fmaf(fabsf(w[4 * j + 1]), fabsf(xv[t][j].y), aa);
+            aa = fmaf(fabsf(w[4 * j + 2]), fabsf(xv[t][j].z), aa);
+            aa = fmaf(fabsf(w[4 * j + 3]), fabsf(xv[t][j].w), aa);
+        }
+        inc[t] = cf_wave_scan(p);  // inclusive prefix of p in the wave
+        a[t] = aa;
+        if (lane == WAVE - 1) s_tot[t][wv] = inc[t];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+        float off = 0.f;  // the earlier waves' totals, in order
+#pragma unroll
+        for (int u = 0; u < CF_WAVES - 1; u++)
+            if (u < wv) off += s_tot[t][u];
+        // exclusive prefix P_i of this thread's chunk: the previous lane's
+        // inclusive prefix (wave_shr 1; lane 0 reads 0) after the waves before
+        const float excl = off + cf_dpp<0x138, 0xF>(inc[t]);
+        const float sp = wave_sum(fabsf(excl)), aa = wave_sum(a[t]);
+        if (lane == 0) {
+            s_sp[t][wv] = sp;
+            s_a[t][wv] = aa;
+        }
+    }
+    __syncthreads();
+    if (tid < nt) {
+        const int t = tid;
+        float f = 0.f, sp = 0.f, aa = 0.f;
+#pragma unroll
+        for (int u = 0; u < CF_WAVES; u++) {
+            f += s_tot[t][u];
+            sp += s_sp[t][u];
+            aa += s_a[t][u];
+        }
+        if (gate) {
+            gsh[t0 + t] = has_shg ? f : 0.f;
+        } else {
+            logits[(size_t)(t0 + t) * E + r] = f;
+            radii[(size_t)(t0 + t) * E + r] = (1.0f + 1.0f / 1024) * CERT_U * ((float)L * sp + coef_a * aa) + 1e-37f;
+        }
+    }
+}
+
 // One wave per token: softmax / top-k / renormalisation with the host's
 // arithmetic on the logits of k_route_seq.
 template <int MAXV>
@@ -105,6 +272,83 @@ int bread_launch_route_logits(const float *router, const uint16_t *shg, const fl
     else
         hipLaunchKernelGGL(k_route_seq<2>, grid, dim3(RS_WAVES * WAVE), 0, st, router, shg, x, logits, gsh, H, E, T,
                            shg_row ? 1 : 0);
+    BREAD_HIP(hipGetLastError());
+    return BREAD_OK;
+}
+
+// Certified fast routing of T <= CF_MAX_T tokens (see k_route_fast); false
+// if the shape does not allow it (the caller then runs
+// bread_launch_route_logits).  The radii, the token list and its count live
+// in c->h, which the layer's gate/up kernels only write afterwards.
+bool bread_route_certified_ok(const bread_moe_ctx_t *c, int T)
+{
+    const bread_moe_shape_t &s = c->shape;
+    const int H = s.hidden, E = s.n_experts, K = s.top_k;
+    const int Imax = s.expert_inter > s.shared_inter ? s.expert_inter : s.shared_inter;
+    const size_t hcap = (size_t)c->max_tokens * (K + 1) * Imax;
+    return T >= 1 && T <= CF_MAX_T && H % (4 * CF_THREADS) == 0 && H <= 4096 && E <= 16 * WAVE && K >= 1 &&
+           K <= CF_MAX_K && K <= E && (size_t)T * E + T + 1 <= hcap;
+}
+
+bread_route_cert_ws bread_route_cert_buffers(bread_moe_ctx_t *c, int T)
+{
+    bread_route_cert_ws b;
+    b.radii = c->h;
+    b.list = reinterpret_cast<int *>(c->h + (size_t)T * c->shape.n_experts);
+    b.list_n = b.list + T;
+    return b;
+}
+
+int bread_launch_route_fast(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, int T, float *gsh,
+                            float *radii, hipStream_t st)
+{
+    const bread_moe_shape_t &s = c->shape;
+    const int H = s.hidden, E = s.n_experts;
+    const double u = 5.9604644775390625e-8, n = (double)H;
+    const float coef_a = (float)(2.0 * (H / CF_THREADS) + 12.0 + n * n * u * 1.01);
+    // the gate workgroup reads H halves at shg; without a gate it reads the
+    // router's first row instead (and stores zeros)
+    const uint16_t *g = L->shexp_gate ? L->shexp_gate : reinterpret_cast<const uint16_t *>(L->router);
+    const int has_g = L->shexp_gate ? 1 : 0;
+    // tokens per workgroup: the fewest of 4, 8, 16 that hold T (8 at most
+    // for L > 8, where 16 tokens' columns would not fit the registers)
+    const int tt = T <= 4 ? 4 : (T <= 8 || H / CF_THREADS > 8 ? 8 : 16);
+    const dim3 grid(E + 1, (T + tt - 1) / tt), block(CF_THREADS);
+#define BREAD_ROUTE_FAST(LL, TTT)                                                                              \
+    hipLaunchKernelGGL((k_route_fast<LL, TTT>), grid, block, 0, st, L->router, g, has_g, x, c->logits, radii, gsh, \
+                       H, E, T, coef_a)
+    switch (H / CF_THREADS * 100 + tt) {
+    case 404: BREAD_ROUTE_FAST(4, 4); break;
+    case 408: BREAD_ROUTE_FAST(4, 8); break;
+    case 416: BREAD_ROUTE_FAST(4, 16); break;
+    case 804: BREAD_ROUTE_FAST(8, 4); break;
+    case 808: BREAD_ROUTE_FAST(8, 8); break;
+    case 816: BREAD_ROUTE_FAST(8, 16); break;
+    case 1204: BREAD_ROUTE_FAST(12, 4); break;
+    case 1208: BREAD_ROUTE_FAST(12, 8); break;
+    case 1604: BREAD_ROUTE_FAST(16, 4); break;
+    case 1608: BREAD_ROUTE_FAST(16, 8); break;
+    default:
+        return bread_fail(BREAD_ERR_SHAPE, "bread_launch_route_fast", "hidden must be 1024, 2048, 3072 or 4096");
+    }
+#undef BREAD_ROUTE_FAST
+    BREAD_HIP(hipGetLastError());
+    return BREAD_OK;
+}
+
+int bread_launch_route_exact_list(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, int T,
+                                  float *gsh, const int *list, const int *list_n, hipStream_t st)
+{
+    const bread_moe_shape_t &s = c->shape;
+    const int H = s.hidden, E = s.n_experts;
+    const int ne = bread_route_rows_per_wave(T, E);
+    const dim3 grid((E + RS_WAVES * ne - 1) / (RS_WAVES * ne) + 1, (T + RS_TT - 1) / RS_TT);
+    if (ne == 1)
+        hipLaunchKernelGGL(k_route_seq_list<1>, grid, dim3(RS_WAVES * WAVE), 0, st, L->router, L->shexp_gate, x,
+                           c->logits, gsh, H, E, T, list, list_n);
+    else
+        hipLaunchKernelGGL(k_route_seq_list<2>, grid, dim3(RS_WAVES * WAVE), 0, st, L->router, L->shexp_gate, x,
+                           c->logits, gsh, H, E, T, list, list_n);
     BREAD_HIP(hipGetLastError());
     return BREAD_OK;
 }
