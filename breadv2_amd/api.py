@@ -550,7 +550,7 @@ class MoeContext:
         return g.value
 
     ROUTE_STAT_NAMES = ("decode_radius", "decode_per_expert", "decode_pair", "decode_exact",
-                        "multi_certified", "multi_exact")
+                        "multi_certified", "multi_candidates", "multi_exact")
 
     def route_stats(self, reset: bool = False) -> dict:
         """bread_moe_ctx_route_stats: how often exact routing took each path

@@ -32,9 +32,10 @@ __host__ __device__ inline uint32_t fresh_u32(uint32_t v)
     return v;
 }
 
-__host__ __device__ inline float libm_expf(float x)
+// The 32 table entries (used through libm_expf_t; a caller may copy them
+// to LDS once and pass that copy, so the lookup does not wait on memory).
+__host__ __device__ inline uint64_t libm_expf_tab(int i)
 {
-#pragma clang fp contract(off)
     constexpr uint64_t tab[32] = {
         0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
         0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
@@ -45,6 +46,14 @@ __host__ __device__ inline float libm_expf(float x)
         0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
         0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
     };
+    return tab[i & 31];
+}
+
+// The computation, with entry i of the table from tab(i).
+template <class Tab>
+__host__ __device__ inline float libm_expf_g(float x, Tab tab)
+{
+#pragma clang fp contract(off)
     constexpr double inv_ln2_n = 0x1.71547652b82fep+0 * 32;
     constexpr double shift = 0x1.8p+52;
     constexpr double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
@@ -63,11 +72,32 @@ __host__ __device__ inline float libm_expf(float x)
     const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
     kd -= shift;
     const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    const double s = __builtin_bit_cast(double, tab[ki % 32] + (ki << 47));
+    const double s = __builtin_bit_cast(double, tab((int)(ki % 32)) + (ki << 47));
     const double c1 = __builtin_bit_cast(double, ((uint64_t)fresh_u32(0x3f2ebfceu) << 32) | fresh_u32(0x50fac4f3u));
     const double z = __builtin_fma(c0, r, c1);
     const double r2 = r * r;
     double y = __builtin_fma(c2, r, 1.0);
     y = __builtin_fma(z, r2, y);
     return (float)(y * s);
+}
+
+struct LibmExpfConstTab {
+    __host__ __device__ uint64_t operator()(int i) const { return libm_expf_tab(i); }
+};
+
+struct LibmExpfPtrTab {
+    const uint64_t *t;
+    __host__ __device__ uint64_t operator()(int i) const { return t[i]; }
+};
+
+__host__ __device__ inline float libm_expf(float x)
+{
+    return libm_expf_g(x, LibmExpfConstTab{});
+}
+
+// libm_expf with a copy of the table at tab (libm_expf_tab's 32 entries,
+// e.g. in LDS).
+__host__ __device__ inline float libm_expf_t(float x, const uint64_t *tab)
+{
+    return libm_expf_g(x, LibmExpfPtrTab{tab});
 }

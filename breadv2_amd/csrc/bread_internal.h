@@ -58,8 +58,9 @@ enum : int {
     BREAD_RSTAT_PER_EXPERT = 1, // decode layers certified by per-expert radii
     BREAD_RSTAT_PAIR = 2,       // decode layers with two adjacent ranks recomputed in reference order
     BREAD_RSTAT_EXACT = 3,      // decode layers with every logit recomputed in reference order
-    BREAD_RSTAT_MT_CERT = 4,    // small-batch tokens whose fast ranks the certificate vouched for
-    BREAD_RSTAT_MT_EXACT = 5,   // small-batch tokens summed again in reference order
+    BREAD_RSTAT_MT_CERT = 4,    // multi-token tokens whose fast ranks the certificate vouched for
+    BREAD_RSTAT_MT_CAND = 5,    // ... ranked by the reference-order sums of their candidate rows
+    BREAD_RSTAT_MT_EXACT = 6,   // ... with every row summed in reference order
     BREAD_RSTAT_N = 8,
 };
 
@@ -192,21 +193,12 @@ int bread_route_rows_per_wave(int T, int E);
 int bread_launch_route_logits(const float *router, const uint16_t *shg, const float *x, float *logits, float *gsh,
                               int H, int E, int T, bool shg_row, hipStream_t st);
 // Certified fast routing for a few tokens (route.hip): fast logits with
-// radii for every token (bread_launch_route_fast), a certificate per token
-// on the device (cert_select_wave, route_dev.h) that lists the tokens it
-// cannot vouch for, and the reference's order for the listed ones
-// (bread_launch_route_exact_list).  Buffers in c->h.
-struct bread_route_cert_ws {
-    float *radii;  // [T][E]
-    int *list;     // [T]: tokens to sum again in the reference's order
-    int *list_n;   // their number
-};
+// radii for every token into c->logits and radii (T x E floats in c->h);
+// the certificate and the exact sums it asks for run in the caller's
+// selection kernel (route_cert.h).
 bool bread_route_certified_ok(const bread_moe_ctx_t *c, int T);
-bread_route_cert_ws bread_route_cert_buffers(bread_moe_ctx_t *c, int T);
 int bread_launch_route_fast(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, int T, float *gsh,
                             float *radii, hipStream_t st);
-int bread_launch_route_exact_list(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, int T,
-                                  float *gsh, const int *list, const int *list_n, hipStream_t st);
 int bread_grouped_alloc(bread_moe_ctx_t *ctx);
 void bread_grouped_free(bread_moe_ctx_t *ctx);
 bool bread_grouped_supported(const bread_moe_shape_t &s, const bread_moe_layer_t *L);

@@ -13,16 +13,19 @@
 // vector ALUs.
 //
 // Kernels per layer, stream-ordered:
-//   k_route_seq   router logits and shared-gate scores in the reference's
-//                 sequential order (route.hip).
-//   k_sb_select   one workgroup: softmax / top-k per token with the host's
-//                 arithmetic (routing bit-identical to the reference's), then
-//                 slots: an
-//                 expert's tokens in chunks of at most SB_CH (the shared
-//                 expert's chunks first, with every token, then the chosen
-//                 experts in expert order), each with its (token, rank) pairs
-//                 in token order.  Chunks spread a hot expert over more
-//                 workgroups.
+//   k_route_fast  router logits and shared-gate scores summed in parallel,
+//                 each logit with a rigorous radius around the reference's
+//                 sequential sum (route.hip).
+//   k_sb_route    one workgroup: per token, the certificate and selection
+//                 from the fast logits, or the reference-order sums of the
+//                 candidate rows (route_cert.h; indices bit-identical to the
+//                 reference's), then slots: an expert's tokens in chunks of
+//                 at most SB_CH (the shared expert's chunks first, with every
+//                 token, then the chosen experts in expert order), each with
+//                 its (token, rank) pairs in token order.  Chunks spread a
+//                 hot expert over more workgroups.  Shapes beyond the fast
+//                 sums' limits take k_route_seq (the reference's order) and
+//                 k_sb_select (the host's selection) instead.
 //   k_sb_gateup   grid (slot, 32-row chunk): 8 lanes per gate/up row pair,
 //                 one Q4_K superblock a lane, dotted with the slot's tokens
 //                 (staged in LDS), then SwiGLU.
@@ -38,6 +41,7 @@
 // before it.  Every sum has a fixed order: repeated calls are bit-identical.
 #include "bread_internal.h"
 #include "quant_dot.h"
+#include "route_cert.h"
 #include "route_dev.h"
 
 namespace {
@@ -176,94 +180,76 @@ __global__ __launch_bounds__(RT_THREADS) void k_sb_select(const float *__restric
     sb_number_slots(sidx, E, K, T, slot_expert, slot_cnt, slot_pair, n_slots);
 }
 
-// Certified selection from the fast logits and radii (k_route_fast): wave v
-// takes tokens v, v + 16, ...; a token the certificate vouches for
-// (cert_select_wave) gets its experts and weights here, the others join the
-// list that k_route_seq_list sums again in the reference's order and
-// k_sb_select_list then selects.  With every token certified the slots are
-// numbered here as well.  Counts both outcomes in stats.  One workgroup.
+// Certified routing from the fast logits and radii (k_route_fast), then the
+// slots.  Wave v takes tokens v, v + 16, ...: a token the certificate
+// vouches for (cert_select_wave) gets its experts and weights at once; the
+// others are then routed one after another by the whole workgroup from the
+// reference-order sums of their candidate rows (route_token_exact).  Counts
+// the three outcomes in stats.  One workgroup.
 template <int MAXV>
-__global__ __launch_bounds__(RT_THREADS) void k_sb_select_cert(const float *__restrict__ logits,
-                                                               const float *__restrict__ radii, int E, int K, int T,
-                                                               int32_t *__restrict__ idx, float *__restrict__ w,
-                                                               int32_t *__restrict__ slot_expert,
-                                                               int32_t *__restrict__ slot_cnt,
-                                                               int32_t *__restrict__ slot_pair,
-                                                               int32_t *__restrict__ n_slots, int *__restrict__ list,
-                                                               int *__restrict__ list_n,
-                                                               uint32_t *__restrict__ stats)
+__global__ __launch_bounds__(RT_THREADS) void k_sb_route(const float *__restrict__ router,
+                                                         const float *__restrict__ x, const float *__restrict__ logits,
+                                                         const float *__restrict__ radii, int H, int E, int K, int T,
+                                                         int32_t *__restrict__ idx, float *__restrict__ w,
+                                                         int32_t *__restrict__ slot_expert,
+                                                         int32_t *__restrict__ slot_cnt,
+                                                         int32_t *__restrict__ slot_pair,
+                                                         int32_t *__restrict__ n_slots, uint32_t *__restrict__ stats)
 {
+    __shared__ RxSmem S;
     __shared__ int sidx[SB_MAX_T * MAX_K];
+    __shared__ int s_cand[SB_MAX_T][RX_CAND];
+    __shared__ int s_ncand[SB_MAX_T];
     __shared__ int s_list[SB_MAX_T];
     __shared__ int s_n;
+    __shared__ uint64_t s_tab[32];
+    static_assert(RT_WAVES * 2 * RX_MAX_E <= RX_CH * RX_ROW, "certificate scratch in S.prod");
     const int tid = (int)threadIdx.x, wv = tid / WAVE, lane = lane_id();
     if (tid == 0) s_n = 0;
     __syncthreads();
+    // expf's table for the exact selection, requested now and stored after
+    // the certificates (its wait then costs nothing)
+    const uint64_t tabv = libm_expf_tab(tid);
     for (int t = wv; t < T; t += RT_WAVES) {
-        int ik = 0;
+        int ik = 0, nc = 0;
         float wk = 0.f;
-        if (cert_select_wave<MAXV>(logits + (size_t)t * E, radii + (size_t)t * E, E, K, ik, wk)) {
+        // scratch: S.prod, free until the reference-order sums below
+        const int r = cert_select_wave<MAXV>(logits + (size_t)t * E, radii + (size_t)t * E, E, K, ik, wk,
+                                             s_cand[t], nc, &S.prod[0][0] + wv * 2 * RX_MAX_E);
+        if (r == 1) {
             if (lane < K) {
                 idx[(size_t)t * K + lane] = ik;
                 w[(size_t)t * K + lane] = wk;
                 sidx[t * K + lane] = ik;
             }
         } else if (lane == 0) {
+            s_ncand[t] = r == 0 ? nc : -1;
             s_list[atomicAdd(&s_n, 1)] = t;
         }
     }
+    if (tid < 32) s_tab[tid] = tabv;
     __syncthreads();
     const int n = s_n;
-    if (tid < n) list[tid] = s_list[tid];
-    if (tid == 0) {
-        *list_n = n;
-        atomicAdd(&stats[BREAD_RSTAT_MT_CERT], (uint32_t)(T - n));
-        atomicAdd(&stats[BREAD_RSTAT_MT_EXACT], (uint32_t)n);
-    }
-    if (n == 0) sb_number_slots(sidx, E, K, T, slot_expert, slot_cnt, slot_pair, n_slots);
-}
-
-// After k_route_seq_list: the listed tokens selected with the host's
-// arithmetic on their reference-order logits, then the slots of every token
-// (the certified ones' experts as k_sb_select_cert wrote them).  Returns at
-// once when the list is empty.  One workgroup.
-template <int MAXV>
-__global__ __launch_bounds__(RT_THREADS) void k_sb_select_list(const float *__restrict__ logits, int E, int K,
-                                                               int T, int32_t *__restrict__ idx,
-                                                               float *__restrict__ w,
-                                                               int32_t *__restrict__ slot_expert,
-                                                               int32_t *__restrict__ slot_cnt,
-                                                               int32_t *__restrict__ slot_pair,
-                                                               int32_t *__restrict__ n_slots,
-                                                               const int *__restrict__ list,
-                                                               const int *__restrict__ list_n)
-{
-    __shared__ int sidx[SB_MAX_T * MAX_K];
-    __shared__ int listed[SB_MAX_T];
-    __shared__ __attribute__((aligned(16))) float s_e[RT_WAVES][WAVE * MAXV];
-    const int n_raw = __builtin_amdgcn_readfirstlane(*list_n);
-    if (n_raw <= 0) return;
-    const int n = n_raw < T ? n_raw : T;
-    const int tid = (int)threadIdx.x, wv = tid / WAVE, lane = lane_id();
-    if (tid < SB_MAX_T) listed[tid] = 0;
-    __syncthreads();
-    for (int i = wv; i < n; i += RT_WAVES) {
-        const int t = __builtin_amdgcn_readfirstlane(list[i]);
-        if (t < 0 || t >= T) continue;
-        int ik;
-        float wk;
-        topk_wave_exact<MAXV>(logits + (size_t)t * E, E, K, s_e[wv], ik, wk);
-        if (lane < K) {
-            idx[(size_t)t * K + lane] = ik;
-            w[(size_t)t * K + lane] = wk;
-            sidx[t * K + lane] = ik;
+    int nfull = 0;
+    for (int i = 0; i < n; i++) {
+        const int t = s_list[i];
+        int ik = 0;
+        float wk = 0.f;
+        const int how = route_token_exact<MAXV, RT_THREADS>(S, router, x + (size_t)t * H, s_cand[t], s_ncand[t], H,
+                                                            E, K, s_tab, ik, wk);
+        if (tid < K) {
+            idx[(size_t)t * K + tid] = ik;
+            w[(size_t)t * K + tid] = wk;
+            sidx[t * K + tid] = ik;
         }
-        if (lane == 0) listed[t] = 1;
+        nfull += how == 2 ? 1 : 0;
     }
     __syncthreads();
-    for (int i = tid; i < T * K; i += RT_THREADS)
-        if (!listed[i / K]) sidx[i] = idx[i];
-    __syncthreads();
+    if (tid == 0) {
+        if (n < T) atomicAdd(&stats[BREAD_RSTAT_MT_CERT], (uint32_t)(T - n));
+        if (n > nfull) atomicAdd(&stats[BREAD_RSTAT_MT_CAND], (uint32_t)(n - nfull));
+        if (nfull) atomicAdd(&stats[BREAD_RSTAT_MT_EXACT], (uint32_t)nfull);
+    }
     sb_number_slots(sidx, E, K, T, slot_expert, slot_cnt, slot_pair, n_slots);
 }
 
@@ -1138,33 +1124,23 @@ int bread_launch_moe_small(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const
                      L->gate_expert_bytes, L->up_expert_bytes, L->down_expert_bytes};
     const SbSlots ss{g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots};
     bread_clear_stale_error();
-    // routing (route.hip): fast logits with radii, the certificate and the
-    // selection of the tokens it vouches for, the reference's order and the
-    // host's selection for the rest (the last two return at once when no
-    // token is left); beyond the certified path's limits, the reference's
-    // order for every token
+    // routing: fast logits with radii (route.hip), then the certificate, the
+    // reference-order sums it asks for and the slots in one workgroup
+    // (k_sb_route); beyond the certified path's limits, the reference's
+    // order for every logit and the host's selection (k_sb_select)
     const bool mv4 = E <= 4 * WAVE;
     if (bread_route_certified_ok(c, T)) {
-        const bread_route_cert_ws cw = bread_route_cert_buffers(c, T);
-        int rc = bread_launch_route_fast(c, L, x, T, c->gsh, cw.radii, st);
+        float *radii = c->h;
+        const int rc = bread_launch_route_fast(c, L, x, T, c->gsh, radii, st);
         if (rc) return rc;
         if (mv4)
-            hipLaunchKernelGGL(k_sb_select_cert<4>, dim3(1), dim3(RT_THREADS), 0, st, c->logits, cw.radii, E, K, T,
-                               c->idx, c->w, g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots, cw.list, cw.list_n,
+            hipLaunchKernelGGL(k_sb_route<4>, dim3(1), dim3(RT_THREADS), 0, st, L->router, x, c->logits, radii, H, E,
+                               K, T, c->idx, c->w, g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots,
                                c->dsync->rstat.v);
         else
-            hipLaunchKernelGGL(k_sb_select_cert<16>, dim3(1), dim3(RT_THREADS), 0, st, c->logits, cw.radii, E, K,
-                               T, c->idx, c->w, g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots, cw.list,
-                               cw.list_n, c->dsync->rstat.v);
-        BREAD_HIP(hipGetLastError());
-        rc = bread_launch_route_exact_list(c, L, x, T, c->gsh, cw.list, cw.list_n, st);
-        if (rc) return rc;
-        if (mv4)
-            hipLaunchKernelGGL(k_sb_select_list<4>, dim3(1), dim3(RT_THREADS), 0, st, c->logits, E, K, T, c->idx,
-                               c->w, g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots, cw.list, cw.list_n);
-        else
-            hipLaunchKernelGGL(k_sb_select_list<16>, dim3(1), dim3(RT_THREADS), 0, st, c->logits, E, K, T, c->idx,
-                               c->w, g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots, cw.list, cw.list_n);
+            hipLaunchKernelGGL(k_sb_route<16>, dim3(1), dim3(RT_THREADS), 0, st, L->router, x, c->logits, radii, H,
+                               E, K, T, c->idx, c->w, g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots,
+                               c->dsync->rstat.v);
     } else {
         const int rc =
             bread_launch_route_logits(L->router, L->shexp_gate, x, c->logits, c->gsh, H, E, T, true, st);

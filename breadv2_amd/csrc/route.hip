@@ -64,32 +64,17 @@ __global__ __launch_bounds__(RS_WAVES * WAVE) void k_route_seq(const float *__re
     route_seq_block<NE>(S, (int)blockIdx.x, (int)blockIdx.y, router, shg, x, logits, gsh, H, E, T, shg_row != 0);
 }
 
-// The exact logits of the tokens list[0 .. *list_n) (the rest of the grid
-// returns at once): k_route_seq through a token list.
-template <int NE>
-__global__ __launch_bounds__(RS_WAVES * WAVE) void k_route_seq_list(const float *__restrict__ router,
-                                                                   const uint16_t *__restrict__ shg,
-                                                                   const float *__restrict__ x,
-                                                                   float *__restrict__ logits,
-                                                                   float *__restrict__ gsh, int H, int E, int T,
-                                                                   const int *__restrict__ list,
-                                                                   const int *__restrict__ list_n)
-{
-    __shared__ RsSmem S;
-    route_seq_block<NE>(S, (int)blockIdx.x, (int)blockIdx.y, router, shg, x, logits, gsh, H, E, T, true, list, list_n);
-}
-
 // ---------------------------------------------------------------------------
 // Certified fast routing for a few tokens.  The reference's sequential sums
 // (one_layer.cu:969-971) are a 2048-step dependent chain per logit; for a
 // few tokens the chain, not the data, sets the time of k_route_seq.  Here
 // every logit is first summed in parallel with a rigorous radius R >=
-// |fast - sequential|; a token whose top K, so widened, is strictly
-// separated (cert_select_wave, route_dev.h) keeps its fast logits, which
-// select the reference's experts in the reference's order; the other tokens
-// are summed again in the reference's order (k_route_seq_list) and selected
-// with the host's arithmetic.  Indices are exact either way; the weights of
-// certified tokens come from the fast logits (within the layer tolerance).
+// |fast - sequential|; the selection kernel then certifies each token from
+// these (route_cert.h): a token whose top K, so widened, is strictly
+// separated keeps its fast logits, which select the reference's experts in
+// the reference's order; for the others only the rows that could reach the
+// top K are summed again in the reference's order.  Indices are exact either
+// way; the weights come from the fast logits (within the layer tolerance).
 //
 // k_route_fast: grid (E + 1, ceil(T / TT)); workgroup (r, g) takes router
 // row r (r = E: the fp16 shared gate, widened; its fast sums are the
@@ -278,8 +263,8 @@ int bread_launch_route_logits(const float *router, const uint16_t *shg, const fl
 
 // Certified fast routing of T <= CF_MAX_T tokens (see k_route_fast); false
 // if the shape does not allow it (the caller then runs
-// bread_launch_route_logits).  The radii, the token list and its count live
-// in c->h, which the layer's gate/up kernels only write afterwards.
+// bread_launch_route_logits).  The radii live in c->h, which the layer's
+// gate/up kernels only write afterwards.
 bool bread_route_certified_ok(const bread_moe_ctx_t *c, int T)
 {
     const bread_moe_shape_t &s = c->shape;
@@ -287,16 +272,7 @@ bool bread_route_certified_ok(const bread_moe_ctx_t *c, int T)
     const int Imax = s.expert_inter > s.shared_inter ? s.expert_inter : s.shared_inter;
     const size_t hcap = (size_t)c->max_tokens * (K + 1) * Imax;
     return T >= 1 && T <= CF_MAX_T && H % (4 * CF_THREADS) == 0 && H <= 4096 && E <= 16 * WAVE && K >= 1 &&
-           K <= CF_MAX_K && K <= E && (size_t)T * E + T + 1 <= hcap;
-}
-
-bread_route_cert_ws bread_route_cert_buffers(bread_moe_ctx_t *c, int T)
-{
-    bread_route_cert_ws b;
-    b.radii = c->h;
-    b.list = reinterpret_cast<int *>(c->h + (size_t)T * c->shape.n_experts);
-    b.list_n = b.list + T;
-    return b;
+           K <= CF_MAX_K && K <= E && (size_t)T * E <= hcap;
 }
 
 int bread_launch_route_fast(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, int T, float *gsh,
@@ -332,23 +308,6 @@ int bread_launch_route_fast(bread_moe_ctx_t *c, const bread_moe_layer_t *L, cons
         return bread_fail(BREAD_ERR_SHAPE, "bread_launch_route_fast", "hidden must be 1024, 2048, 3072 or 4096");
     }
 #undef BREAD_ROUTE_FAST
-    BREAD_HIP(hipGetLastError());
-    return BREAD_OK;
-}
-
-int bread_launch_route_exact_list(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, int T,
-                                  float *gsh, const int *list, const int *list_n, hipStream_t st)
-{
-    const bread_moe_shape_t &s = c->shape;
-    const int H = s.hidden, E = s.n_experts;
-    const int ne = bread_route_rows_per_wave(T, E);
-    const dim3 grid((E + RS_WAVES * ne - 1) / (RS_WAVES * ne) + 1, (T + RS_TT - 1) / RS_TT);
-    if (ne == 1)
-        hipLaunchKernelGGL(k_route_seq_list<1>, grid, dim3(RS_WAVES * WAVE), 0, st, L->router, L->shexp_gate, x,
-                           c->logits, gsh, H, E, T, list, list_n);
-    else
-        hipLaunchKernelGGL(k_route_seq_list<2>, grid, dim3(RS_WAVES * WAVE), 0, st, L->router, L->shexp_gate, x,
-                           c->logits, gsh, H, E, T, list, list_n);
     BREAD_HIP(hipGetLastError());
     return BREAD_OK;
 }

@@ -193,9 +193,10 @@ __device__ __forceinline__ float seq_dot_lds(const float *w, const float *x, int
     return acc;
 }
 
-// The reference's sequential fp32 sum ((0 + p_0) + p_1) + ... of n values in
-// LDS (n % 16 == 0; each lane may read its own array).  Reads run two blocks
-// of 8 ahead of the dependent adds.
+// The reference's sequential fp32 sum ((acc + p_0) + p_1) + ... of n values
+// in LDS (acc 0 unless a previous part's sum continues; n % 16 == 0; each
+// lane may read its own array).  Reads run two blocks of 8 ahead of the
+// dependent adds.
 __device__ __forceinline__ void lds_read8(const float *p, int o, float (&v)[8])
 {
 #pragma unroll
@@ -205,12 +206,11 @@ __device__ __forceinline__ void lds_read8(const float *p, int o, float (&v)[8])
     }
 }
 
-__device__ __forceinline__ float seq_sum_lds(const float *p, int n)
+__device__ __forceinline__ float seq_sum_lds(const float *p, int n, float acc = 0.f)
 {
 #pragma clang fp contract(off)
     const int nb = n / 8;
     float va[8], vb[8];
-    float acc = 0.f;
     lds_read8(p, 0, va);
     for (int b = 0; b < nb; b += 2) {
         lds_read8(p, 8 * min(b + 1, nb - 1), vb);
@@ -347,95 +347,6 @@ __device__ __forceinline__ float renorm_weight(uint32_t my_key, int K)
         w_sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_w), k));
     if (w_sum > 0.f) my_w = my_w / w_sum;
     return my_w;
-}
-
-// Certified selection of one token from fast logits lg[e] with radii rd[e]
-// (one wave; entry e = lane + 64 v).  The certificate: every logit and
-// radius finite, |l| <= 64, the top K by fast logit (larger first, the lower
-// index among equal keys) spread at most CERT_SPREAD (widened by 2 max R),
-// every consecutive pair of the top K and the last of them and the largest
-// l + r below it more than their radii plus tau apart (tau = 12 u (1 +
-// max|l| + 2 max R)).  When it holds, the reference's selection on its own
-// sums picks the same experts in the same order; lane k < K then returns
-// rank k's expert and its weight (softmax of the fast logits, the rank-order
-// renormalisation of layer_ops.cu:244-249) and the result is true.  Otherwise
-// false and nothing is returned.  E >= K.
-template <int MAXV>
-__device__ __forceinline__ bool cert_select_wave(const float *lg, const float *rd, int E, int K, int &idx_k,
-                                                 float &w_k)
-{
-    const int lane = lane_id();
-    float l[MAXV], rr[MAXV];
-#pragma unroll
-    for (int v = 0; v < MAXV; v++) {
-        const int e = lane + WAVE * v, ec = e < E ? e : E - 1;
-        l[v] = lg[ec];
-        rr[v] = rd[ec];
-    }
-    bool fin = true;
-    float am = 0.f, rm = 0.f;
-#pragma unroll
-    for (int v = 0; v < MAXV; v++) {
-        fin = fin && __builtin_isfinite(l[v]) && __builtin_isfinite(rr[v]);
-        am = fmaxf(am, fabsf(l[v]));
-        rm = fmaxf(rm, rr[v]);
-    }
-    am = wave_max(am);
-    rm = wave_max(rm);
-    if (__builtin_amdgcn_ballot_w64(!fin) != 0 || !(am <= 64.f)) return false;
-    const float tau = 12.f * CERT_U * (1.f + am + 2.f * rm);
-    uint32_t key[MAXV];
-#pragma unroll
-    for (int v = 0; v < MAXV; v++) key[v] = lane + WAVE * v < E ? logit_key(l[v]) : 0u;
-    bool ok = true;
-    float top = 0.f, prev_l = 0.f, prev_r = 0.f, my_l = 0.f;
-    int my_idx = 0;
-    for (int k = 0; k < K; k++) {
-        uint32_t M;
-        const int win = select_round<MAXV>(key, M);  // wave-uniform; its key is now 0
-        float wl = l[0], wr = rr[0];
-#pragma unroll
-        for (int v = 1; v < MAXV; v++)
-            if (win / WAVE == v) {
-                wl = l[v];
-                wr = rr[v];
-            }
-        wl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), win % WAVE));
-        wr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wr), win % WAVE));
-        if (k == 0)
-            top = wl;
-        else
-            ok = ok && prev_l - wl > prev_r + wr + tau;
-        prev_l = wl;
-        prev_r = wr;
-        if (lane == k) {
-            my_idx = win;
-            my_l = wl;
-        }
-    }
-    // the largest l + r among the experts not selected
-    float rest = -__builtin_inff();
-#pragma unroll
-    for (int v = 0; v < MAXV; v++)
-        if (key[v] != 0u) rest = fmaxf(rest, l[v] + rr[v]);
-    rest = wave_max(rest);
-    ok = ok && top - prev_l + 2.f * rm <= CERT_SPREAD && prev_l - rest > prev_r + tau;
-    if (!ok) return false;
-    // weights: expf(l - max) / sum, the sum over every expert, then the
-    // rank-order renormalisation
-    float s = 0.f;
-#pragma unroll
-    for (int v = 0; v < MAXV; v++)
-        if (lane + WAVE * v < E) s += libm_expf(l[v] - top);
-    s = wave_sum(s);
-    float p = lane < K ? libm_expf(my_l - top) / s : 0.f;
-    float w_sum = 0.f;
-    for (int k = 0; k < K; k++)
-        w_sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), k));
-    if (w_sum > 0.f) p = p / w_sum;
-    idx_k = my_idx;
-    w_k = p;
-    return true;
 }
 
 // One wave: softmax over E logits, K selection passes, renormalisation.

@@ -92,16 +92,16 @@ __device__ __forceinline__ void bar()
 
 // Chunk c into buffer b: RS_XI direct-to-LDS loads a wave, two activation
 // rows an instruction (lanes 0-31 row 2i, 32-63 row 2i+1; lane l writes unit
-// l % 32 from unit (l % 32) ^ (row % 16) of the token's chunk).  Rows with
-// no token (rowtok -1) load the same units of fb instead.
-__device__ __forceinline__ void rs_stage(RsSmem &S, int b, const float *__restrict__ x, const float *fb,
-                                         const int (&rowtok)[RS_XI], int H, int c, int wv, int lane)
+// l % 32 from unit (l % 32) ^ (row % 16) of the token's chunk).  Rows past
+// T load the same units of fb instead.
+__device__ __forceinline__ void rs_stage(RsSmem &S, int b, const float *__restrict__ x, const float *fb, int t0,
+                                         int T, int H, int c, int wv, int lane)
 {
     const int half = lane >> 5, u = lane & 31;
 #pragma unroll
     for (int i = 0; i < RS_XI; i++) {
         const int row = 2 * (wv + RS_WAVES * i) + half;
-        const float *base = rowtok[i] >= 0 ? x + (size_t)rowtok[i] * H : fb;
+        const float *base = t0 + row < T ? x + (size_t)(t0 + row) * H : fb;
         lds_load16(base + c * RS_CJ + 4 * (u ^ (row & 15)), &S.x[b][row - half][0]);
     }
 }
@@ -245,8 +245,8 @@ __device__ __forceinline__ void chunk_dot(const float *xrow, int sw, const rs_f4
 // each); with two, the weights of chunk c + 1.
 template <int NE>
 __device__ __forceinline__ void rs_run(RsSmem &S, const float *__restrict__ x, const float *w0,
-                                       const uint16_t *__restrict__ g, const int (&rowtok)[RS_XI], int H, bool work,
-                                       bool gate, float (&acc)[NE])
+                                       const uint16_t *__restrict__ g, int t0, int T, int H, bool work, bool gate,
+                                       float (&acc)[NE])
 {
     const int lane = lane_id(), wv = wave_id();
     const int nc = H / RS_CJ;
@@ -254,7 +254,7 @@ __device__ __forceinline__ void rs_run(RsSmem &S, const float *__restrict__ x, c
     static_assert(RS_NB != 4 || AFTER < 64, "vmcnt range");
     rs_f4 wn[NE][2], wc[NE][2];
     uint2 gn[2];
-    for (int c = 0; c < RS_NB - 1 && c < nc; c++) rs_stage(S, c, x, w0, rowtok, H, c, wv, lane);
+    for (int c = 0; c < RS_NB - 1 && c < nc; c++) rs_stage(S, c, x, w0, t0, T, H, c, wv, lane);
     issue_order();
     rs_load_w<NE>(wn, gn, w0, g, H, 0, lane);
     wait_vm<0>();
@@ -264,7 +264,7 @@ __device__ __forceinline__ void rs_run(RsSmem &S, const float *__restrict__ x, c
         // buffer (c + RS_NB - 1) % RS_NB was last read in chunk c - 1,
         // before the barrier that ended it
         if (c + RS_NB - 1 < nc)
-            rs_stage(S, (c + RS_NB - 1) % RS_NB, x, w0, rowtok, H, c + RS_NB - 1, wv, lane);
+            rs_stage(S, (c + RS_NB - 1) % RS_NB, x, w0, t0, T, H, c + RS_NB - 1, wv, lane);
         issue_order();
         if (c + 1 < nc) rs_load_w<NE>(wn, gn, w0, g, H, c + 1, lane);
         issue_order();
@@ -286,15 +286,12 @@ __device__ __forceinline__ void rs_run(RsSmem &S, const float *__restrict__ x, c
 // threads, nbx = ceil(E / (4 NE)): router rows 4 NE bx .. + 4 NE - 1 (NE a
 // wave) for tokens 64 by .. (one a lane); with shg_row, workgroup bx = nbx
 // takes the fp16 shared gate (on wave 0; written to gsh, 0 when shg is NULL).
-// With a token list, position i stands for token list[i] and only the first
-// *list_n positions exist (read on the device; T bounds them).
 // H % 128 == 0 and E >= NE.
 template <int NE>
 __device__ __forceinline__ void route_seq_block(RsSmem &S, int bx, int by, const float *__restrict__ router,
                                                 const uint16_t *__restrict__ shg, const float *__restrict__ x,
                                                 float *__restrict__ logits, float *__restrict__ gsh, int H, int E,
-                                                int T, bool shg_row, const int *__restrict__ list = nullptr,
-                                                const int *__restrict__ list_n = nullptr)
+                                                int T, bool shg_row)
 {
     static_assert(NE == 1 || NE == 2, "weight registers");
     const int lane = lane_id(), wv = wave_id();
@@ -302,15 +299,6 @@ __device__ __forceinline__ void route_seq_block(RsSmem &S, int bx, int by, const
     const bool gate_wg = shg_row && bx == nbx;
     const bool gate_wave = gate_wg && wv == 0 && shg;  // sums the gate
     const int t0 = by * RS_TT;
-    const int Tn = list ? min(__builtin_amdgcn_readfirstlane(*list_n), T) : T;
-    if (t0 >= Tn) return;  // the whole workgroup: no position of its tile exists
-    // the token of each activation row this lane stages (-1: none)
-    int rowtok[RS_XI];
-#pragma unroll
-    for (int i = 0; i < RS_XI; i++) {
-        const int pos = t0 + 2 * (wv + RS_WAVES * i) + (lane >> 5);
-        rowtok[i] = pos < Tn ? (list ? list[pos] : pos) : -1;
-    }
     // the wave stands for rows eb .. eb + NE - 1 and sums the NE consecutive
     // rows from e0 (moved back from eb so that every row read exists; rows
     // past E are not stored); the gate workgroup's waves read row 0
@@ -321,10 +309,9 @@ __device__ __forceinline__ void route_seq_block(RsSmem &S, int bx, int by, const
 #pragma unroll
     for (int n = 0; n < NE; n++) acc[n] = 0.f;
     const uint16_t *g = shg ? shg : reinterpret_cast<const uint16_t *>(w0);
-    rs_run<NE>(S, x, w0, g, rowtok, H, !gate_wg || gate_wave, gate_wave, acc);
-    const int pos = t0 + lane;
-    if (pos >= Tn) return;
-    const int t = list ? list[pos] : pos;
+    rs_run<NE>(S, x, w0, g, t0, T, H, !gate_wg || gate_wave, gate_wave, acc);
+    const int t = t0 + lane;
+    if (t >= T) return;
     if (gate_wg) {
         if (wv == 0) gsh[t] = shg ? acc[0] : 0.f;
         return;

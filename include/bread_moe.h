@@ -203,8 +203,10 @@ int bread_moe_ctx_check(bread_moe_ctx_t *ctx, int *device_error);
  * receives, per decode-kernel layer, 0 = ranks certified by one radius,
  * 1 = by per-expert radii, 2 = two adjacent ranks recomputed in the
  * reference's order, 3 = every logit recomputed in the reference's order;
- * 4 = multi-token tokens whose fast logits were certified, 5 = multi-token
- * tokens recomputed in the reference's order; 6-7 unused.  Counters wrap at
+ * per multi-token token routed from fast logits (the small-batch path),
+ * 4 = ranks certified from the fast logits, 5 = ranked by the
+ * reference-order sums of the candidate rows, 6 = every logit recomputed in
+ * the reference's order; 7 unused.  Counters wrap at
  * 2^32.  reset != 0 clears them; bread_moe_ctx_check clears them after a
  * flagged error.  No reference counterpart: it reports how often exact
  * routing needed the slow path. */

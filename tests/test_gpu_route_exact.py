@@ -253,7 +253,7 @@ def test_small_path_certified_routing(base, router_std, T):
     assert np.all(np.abs(gw - rw) <= 1e-3 * np.abs(rw) + 1e-7), float(np.max(np.abs(gw - rw) / np.abs(rw)))
     rg = np.asarray(rg).reshape(-1)
     assert np.all(np.abs(gg - rg) <= 1e-3 * np.maximum(1.0, np.abs(rg)))
-    assert st["multi_certified"] + st["multi_exact"] == n * T
+    assert st["multi_certified"] + st["multi_candidates"] + st["multi_exact"] == n * T
     assert st["multi_certified"] > 0.5 * n * T
     assert ctx.check_device() == 0
 
@@ -321,3 +321,75 @@ def test_decode_wide_logit_spread_routes_exactly(base):
     assert np.array_equal(idx.cpu().numpy()[0], ri), f"{idx.cpu().numpy()[0]} vs oracle {ri}"
     assert ctx.route_stats()["decode_exact"] == 1
     assert ctx.check_device() == 0
+
+
+def small_route(s, lt, xs):
+    T = xs.shape[0]
+    ctx = B.MoeContext(s, max_tokens=T)
+    ctx.set_path(api.PATH_SMALL)
+    ctx.route_stats(reset=True)
+    hid = torch.zeros(T, s.hidden, device=DEV)
+    idx, w, _ = ctx.forward(lt.desc(), dev(xs), hid, T, want_routing=True)
+    torch.cuda.synchronize()
+    st = ctx.route_stats()
+    assert ctx.check_device() == 0
+    return idx.cpu().numpy(), w.cpu().numpy(), st
+
+
+def test_small_wide_logit_spread_routes_exactly(base):
+    """The decode kernel's wide-spread case on the small-batch path: the
+    fast certificate and the candidates' exact ranks must both refuse the
+    underflowed probabilities, so every logit is summed in the reference's
+    order and the host's selection picks the lowest indices, as cpu_topk
+    does; weights then bit-identical too."""
+    s, t = base
+    E, H, K = s.n_experts, s.hidden, s.top_k
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal(H).astype(np.float32)
+    xx = np.float32(np.dot(x.astype(np.float64), x.astype(np.float64)))
+    target = (-46.0 - 9.0 * rng.random(E)).astype(np.float32)
+    target[100] = 60.0
+    router = (target[:, None] * (x / xx)[None, :]).astype(np.float32)
+    lt = layer_with_router(t, s, router)
+    ri, rw, _ = O.route(host_layer(lt), x)
+    gi, gw, st = small_route(s, lt, np.repeat(x[None], 3, axis=0))
+    for tt in range(3):
+        assert np.array_equal(gi[tt], ri), f"{gi[tt]} vs oracle {ri}"
+        assert np.array_equal(gw[tt].view(np.uint32), np.asarray(rw, np.float32).view(np.uint32))
+    assert st["multi_exact"] == 3, st
+
+
+def test_small_tied_rows_route_by_index(base):
+    """24 identical router rows on top (identical reference sums, so the
+    reference takes them by index): the fast certificate cannot separate
+    them, the candidates (more than one batch of 16 rows) are summed in the
+    reference's order, tie exactly and are ranked by index."""
+    s, t = base
+    E, H = s.n_experts, s.hidden
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal((5, H)).astype(np.float32)
+    router = (rng.standard_normal((E, H)) * 0.004).astype(np.float32)
+    rows = np.sort(rng.choice(E, 24, replace=False))
+    router[rows] = (np.sign(x[0]) * 0.01).astype(np.float32)[None, :]
+    lt = layer_with_router(t, s, router)
+    ri, _, _ = O.route_batch(host_layer(lt), x, nthreads=8)
+    assert np.array_equal(ri[0], rows[:s.top_k]), "the oracle ranks the tied rows by index"
+    gi, _, st = small_route(s, lt, x)
+    assert np.array_equal(gi, ri), f"{gi} vs oracle {ri}"
+    assert st["multi_certified"] + st["multi_candidates"] + st["multi_exact"] == 5
+    assert st["multi_candidates"] >= 1, st
+
+
+def test_small_large_logits_route_exactly(base):
+    """Logits far beyond |64| (router std 2): the certificate does not apply,
+    every logit is summed in the reference's order and the host's selection
+    runs: indices and weights bit-identical to the oracle's."""
+    s, _ = base
+    lt = bulk_layer(base, 2.0, 51)
+    T = 7
+    x = np.random.default_rng(52).standard_normal((T, s.hidden)).astype(np.float32)
+    ri, rw, _ = O.route_batch(host_layer(lt), x, nthreads=8)
+    gi, gw, st = small_route(s, lt, x)
+    assert np.array_equal(gi, ri)
+    assert np.array_equal(gw.view(np.uint32), np.asarray(rw, np.float32).view(np.uint32))
+    assert st["multi_exact"] == T, st
