@@ -76,9 +76,10 @@ __global__ __launch_bounds__(RS_WAVES * WAVE) void k_route_seq(const float *__re
 // top K are summed again in the reference's order.  Indices are exact either
 // way; the weights come from the fast logits (within the layer tolerance).
 //
-// k_route_fast: grid (E + 1, ceil(T / TT)); workgroup (r, g) takes router
-// row r (r = E: the fp16 shared gate, widened; its fast sums are the
-// shared-gate scores) for tokens TT g .. TT g + TT - 1, thread i the L = H / 256
+// k_route_fast: grid (ceil((E + 1) / NR), ceil(T / TT)); workgroup (b, g)
+// takes router rows NR b .. NR b + NR - 1 (row E: the fp16 shared gate,
+// widened; its fast sums are the shared-gate scores) for tokens TT g ..
+// TT g + TT - 1, thread i the L = H / 256
 // consecutive columns [L i, L i + L) of every token: a fused multiply-add
 // chain gives the chunk sum p and a = sum |w x|; an inclusive scan of p over
 // the threads (in column order) gives every chunk's exact prefix P_i to
@@ -120,30 +121,32 @@ __device__ __forceinline__ float cf_wave_scan(float v)
     return v;
 }
 
-template <int L, int TT>
+template <int L, int TT, int NR>
 __global__ __launch_bounds__(CF_THREADS, 2) void k_route_fast(const float *__restrict__ router,
                                                              const uint16_t *__restrict__ shg, int has_shg,
                                                              const float *__restrict__ x, float *__restrict__ logits,
                                                              float *__restrict__ radii, float *__restrict__ gsh,
                                                              int H, int E, int T, float coef_a)
 {
-    static_assert(L % 4 == 0 && L <= 16 && TT <= CF_TT, "columns and tokens per thread");
-    __shared__ float s_tot[TT][CF_WAVES], s_sp[TT][CF_WAVES], s_a[TT][CF_WAVES];
+    static_assert(L % 4 == 0 && L <= 16 && TT <= CF_TT && NR * TT <= CF_THREADS, "columns, tokens, rows");
+    __shared__ float s_tot[NR][TT][CF_WAVES], s_sp[NR][TT][CF_WAVES], s_a[NR][TT][CF_WAVES];
     const int tid = (int)threadIdx.x, wv = tid / WAVE, lane = lane_id();
-    const int r = (int)blockIdx.x, t0 = (int)blockIdx.y * TT;
+    const int r0 = NR * (int)blockIdx.x, t0 = (int)blockIdx.y * TT;
     const int nt = T - t0 < TT ? T - t0 : TT;
-    const bool gate = r == E;
     const int c0 = L * tid;
-    // both the router row (row 0 for the gate workgroup) and the gate's
-    // columns are read (shg points at readable memory of H halves either
-    // way), so no load waits on a branch
-    float4 rv[L / 4];
+    // every row's columns and the gate's are read (rows past E read row 0;
+    // shg points at readable memory of H halves either way), so no load
+    // waits on a branch
+    float4 rv[NR][L / 4];
     uint2 hv[L / 4];
 #pragma unroll
-    for (int j = 0; j < L / 4; j++) {
-        rv[j] = reinterpret_cast<const float4 *>(router + (size_t)(gate ? 0 : r) * H + c0)[j];
-        hv[j] = reinterpret_cast<const uint2 *>(shg + c0)[j];
+    for (int n = 0; n < NR; n++) {
+        const int r = r0 + n < E ? r0 + n : 0;
+#pragma unroll
+        for (int j = 0; j < L / 4; j++) rv[n][j] = reinterpret_cast<const float4 *>(router + (size_t)r * H + c0)[j];
     }
+#pragma unroll
+    for (int j = 0; j < L / 4; j++) hv[j] = reinterpret_cast<const uint2 *>(shg + c0)[j];
     // every token's columns requested at once (positions past the last
     // token read the last token again and are not stored)
     float4 xv[TT][L / 4];
@@ -153,63 +156,70 @@ __global__ __launch_bounds__(CF_THREADS, 2) void k_route_fast(const float *__res
 #pragma unroll
         for (int j = 0; j < L / 4; j++) xv[t][j] = reinterpret_cast<const float4 *>(xt)[j];
     }
-    float w[L];
+    float inc[NR][TT], a[NR][TT];
 #pragma unroll
-    for (int j = 0; j < L / 4; j++) {
-        const bool hz = gate && !has_shg;
-        w[4 * j] = gate ? (hz ? 0.f : h2f(hv[j].x)) : rv[j].x;
-        w[4 * j + 1] = gate ? (hz ? 0.f : h2f(hv[j].x >> 16)) : rv[j].y;
-        w[4 * j + 2] = gate ? (hz ? 0.f : h2f(hv[j].y)) : rv[j].z;
-        w[4 * j + 3] = gate ? (hz ? 0.f : h2f(hv[j].y >> 16)) : rv[j].w;
-    }
-    float inc[TT], a[TT];
-#pragma unroll
-    for (int t = 0; t < TT; t++) {
-        float p = 0.f, aa = 0.f;
+    for (int n = 0; n < NR; n++) {
+        const bool gate = r0 + n == E, hz = gate && !has_shg;
+        float w[L];
 #pragma unroll
         for (int j = 0; j < L / 4; j++) {
-            p = fmaf(w[4 * j], xv[t][j].x, p);
-            p = fmaf(w[4 * j + 1], xv[t][j].y, p);
-            p = fmaf(w[4 * j + 2], xv[t][j].z, p);
-            p = fmaf(w[4 * j + 3], xv[t][j].w, p);
-            aa = fmaf(fabsf(w[4 * j]), fabsf(xv[t][j].x), aa);
-            aa = fmaf(fabsf(w[4 * j + 1]), fabsf(xv[t][j].y), aa);
-            aa = fmaf(fabsf(w[4 * j + 2]), fabsf(xv[t][j].z), aa);
-            aa = fmaf(fabsf(w[4 * j + 3]), fabsf(xv[t][j].w), aa);
+            w[4 * j] = gate ? (hz ? 0.f : h2f(hv[j].x)) : rv[n][j].x;
+            w[4 * j + 1] = gate ? (hz ? 0.f : h2f(hv[j].x >> 16)) : rv[n][j].y;
+            w[4 * j + 2] = gate ? (hz ? 0.f : h2f(hv[j].y)) : rv[n][j].z;
+            w[4 * j + 3] = gate ? (hz ? 0.f : h2f(hv[j].y >> 16)) : rv[n][j].w;
         }
-        inc[t] = cf_wave_scan(p);  // inclusive prefix of p in the wave
-        a[t] = aa;
-        if (lane == WAVE - 1) s_tot[t][wv] = inc[t];
-    }
-    __syncthreads();
 #pragma unroll
-    for (int t = 0; t < TT; t++) {
-        float off = 0.f;  // the earlier waves' totals, in order
+        for (int t = 0; t < TT; t++) {
+            float p = 0.f, aa = 0.f;
 #pragma unroll
-        for (int u = 0; u < CF_WAVES - 1; u++)
-            if (u < wv) off += s_tot[t][u];
-        // exclusive prefix P_i of this thread's chunk: the previous lane's
-        // inclusive prefix (wave_shr 1; lane 0 reads 0) after the waves before
-        const float excl = off + cf_dpp<0x138, 0xF>(inc[t]);
-        const float sp = wave_sum(fabsf(excl)), aa = wave_sum(a[t]);
-        if (lane == 0) {
-            s_sp[t][wv] = sp;
-            s_a[t][wv] = aa;
+            for (int j = 0; j < L / 4; j++) {
+                p = fmaf(w[4 * j], xv[t][j].x, p);
+                p = fmaf(w[4 * j + 1], xv[t][j].y, p);
+                p = fmaf(w[4 * j + 2], xv[t][j].z, p);
+                p = fmaf(w[4 * j + 3], xv[t][j].w, p);
+                aa = fmaf(fabsf(w[4 * j]), fabsf(xv[t][j].x), aa);
+                aa = fmaf(fabsf(w[4 * j + 1]), fabsf(xv[t][j].y), aa);
+                aa = fmaf(fabsf(w[4 * j + 2]), fabsf(xv[t][j].z), aa);
+                aa = fmaf(fabsf(w[4 * j + 3]), fabsf(xv[t][j].w), aa);
+            }
+            inc[n][t] = cf_wave_scan(p);  // inclusive prefix of p in the wave
+            a[n][t] = aa;
+            if (lane == WAVE - 1) s_tot[n][t][wv] = inc[n][t];
         }
     }
     __syncthreads();
-    if (tid < nt) {
-        const int t = tid;
+#pragma unroll
+    for (int n = 0; n < NR; n++) {
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            float off = 0.f;  // the earlier waves' totals, in order
+#pragma unroll
+            for (int u = 0; u < CF_WAVES - 1; u++)
+                if (u < wv) off += s_tot[n][t][u];
+            // exclusive prefix P_i of this thread's chunk: the previous
+            // lane's inclusive prefix (wave_shr 1; lane 0 reads 0) after the
+            // waves before
+            const float excl = off + cf_dpp<0x138, 0xF>(inc[n][t]);
+            const float sp = wave_sum(fabsf(excl)), sa = wave_sum(a[n][t]);
+            if (lane == 0) {
+                s_sp[n][t][wv] = sp;
+                s_a[n][t][wv] = sa;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < NR * TT) {
+        const int n = tid / TT, t = tid % TT, r = r0 + n;
         float f = 0.f, sp = 0.f, aa = 0.f;
 #pragma unroll
         for (int u = 0; u < CF_WAVES; u++) {
-            f += s_tot[t][u];
-            sp += s_sp[t][u];
-            aa += s_a[t][u];
+            f += s_tot[n][t][u];
+            sp += s_sp[n][t][u];
+            aa += s_a[n][t][u];
         }
-        if (gate) {
+        if (t < nt && r == E) {
             gsh[t0 + t] = has_shg ? f : 0.f;
-        } else {
+        } else if (t < nt && r < E) {
             logits[(size_t)(t0 + t) * E + r] = f;
             radii[(size_t)(t0 + t) * E + r] = (1.0f + 1.0f / 1024) * CERT_U * ((float)L * sp + coef_a * aa) + 1e-37f;
         }
@@ -287,23 +297,31 @@ int bread_launch_route_fast(bread_moe_ctx_t *c, const bread_moe_layer_t *L, cons
     const uint16_t *g = L->shexp_gate ? L->shexp_gate : reinterpret_cast<const uint16_t *>(L->router);
     const int has_g = L->shexp_gate ? 1 : 0;
     // tokens per workgroup: the fewest of 4, 8, 16 that hold T (8 at most
-    // for L > 8, where 16 tokens' columns would not fit the registers)
-    const int tt = T <= 4 ? 4 : (T <= 8 || H / CF_THREADS > 8 ? 8 : 16);
-    const dim3 grid(E + 1, (T + tt - 1) / tt), block(CF_THREADS);
-#define BREAD_ROUTE_FAST(LL, TTT)                                                                              \
-    hipLaunchKernelGGL((k_route_fast<LL, TTT>), grid, block, 0, st, L->router, g, has_g, x, c->logits, radii, gsh, \
-                       H, E, T, coef_a)
-    switch (H / CF_THREADS * 100 + tt) {
-    case 404: BREAD_ROUTE_FAST(4, 4); break;
-    case 408: BREAD_ROUTE_FAST(4, 8); break;
-    case 416: BREAD_ROUTE_FAST(4, 16); break;
-    case 804: BREAD_ROUTE_FAST(8, 4); break;
-    case 808: BREAD_ROUTE_FAST(8, 8); break;
-    case 816: BREAD_ROUTE_FAST(8, 16); break;
-    case 1204: BREAD_ROUTE_FAST(12, 4); break;
-    case 1208: BREAD_ROUTE_FAST(12, 8); break;
-    case 1604: BREAD_ROUTE_FAST(16, 4); break;
-    case 1608: BREAD_ROUTE_FAST(16, 8); break;
+    // for L > 8, where 16 tokens' columns would not fit the registers);
+    // beyond 16 tokens each workgroup takes 4 router rows (rows share every
+    // activation read: each row workgroup reads all of its tokens' columns)
+    const int L1 = H / CF_THREADS;
+    const int tt = T <= 4 ? 4 : (T <= 8 || L1 > 8 || T > 16 ? 8 : 16);
+    const int nr = T > 16 ? 4 : 1;
+    const dim3 grid((E + 1 + nr - 1) / nr, (T + tt - 1) / tt), block(CF_THREADS);
+#define BREAD_ROUTE_FAST(LL, TTT, NRR)                                                                       \
+    hipLaunchKernelGGL((k_route_fast<LL, TTT, NRR>), grid, block, 0, st, L->router, g, has_g, x, c->logits, radii, \
+                       gsh, H, E, T, coef_a)
+    switch (L1 * 1000 + tt * 10 + nr) {
+    case 4041: BREAD_ROUTE_FAST(4, 4, 1); break;
+    case 4081: BREAD_ROUTE_FAST(4, 8, 1); break;
+    case 4161: BREAD_ROUTE_FAST(4, 16, 1); break;
+    case 4084: BREAD_ROUTE_FAST(4, 8, 4); break;
+    case 8041: BREAD_ROUTE_FAST(8, 4, 1); break;
+    case 8081: BREAD_ROUTE_FAST(8, 8, 1); break;
+    case 8161: BREAD_ROUTE_FAST(8, 16, 1); break;
+    case 8084: BREAD_ROUTE_FAST(8, 8, 4); break;
+    case 12041: BREAD_ROUTE_FAST(12, 4, 1); break;
+    case 12081: BREAD_ROUTE_FAST(12, 8, 1); break;
+    case 12084: BREAD_ROUTE_FAST(12, 8, 4); break;
+    case 16041: BREAD_ROUTE_FAST(16, 4, 1); break;
+    case 16081: BREAD_ROUTE_FAST(16, 8, 1); break;
+    case 16084: BREAD_ROUTE_FAST(16, 8, 4); break;
     default:
         return bread_fail(BREAD_ERR_SHAPE, "bread_launch_route_fast", "hidden must be 1024, 2048, 3072 or 4096");
     }

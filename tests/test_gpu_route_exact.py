@@ -217,18 +217,20 @@ def test_bulk_paths_route_bit_exact(base, path, T, chunks):
 
 
 @pytest.mark.parametrize("router_std", [0.02, 1.0 / np.sqrt(2048)])
-@pytest.mark.parametrize("T", [1, 5, 16, 17, 32])
-def test_small_path_certified_routing(base, router_std, T):
-    """The small-batch path's certified fast routing over 2,048 tokens: indices
-    bit-identical to the oracle's for every token; weights and shared-gate
-    scores of certified tokens from the fast sums, within 1e-3 relative of the
-    oracle's (the radius bounds the logits' difference at ~1e-4); the outcome
-    counters account for every token, and some tokens take each path."""
+@pytest.mark.parametrize("path,T", [(api.PATH_SMALL, 1), (api.PATH_SMALL, 5), (api.PATH_SMALL, 16),
+                                    (api.PATH_SMALL, 17), (api.PATH_SMALL, 32)])
+def test_certified_routing_bulk(base, router_std, path, T):
+    """Certified fast routing (the small-batch path, 1 to 32 tokens a call)
+    over 2,048 tokens: indices bit-identical to the oracle's for every token;
+    weights and shared-gate scores of certified tokens from the fast sums,
+    within 1e-3 relative of the oracle's (the radius bounds the logits'
+    difference at ~1e-4); the outcome counters account for every token, and
+    most tokens are certified."""
     s, _ = base
     lt = bulk_layer(base, router_std, 30 + T)
     hl = host_layer(lt)
     ctx = B.MoeContext(s, max_tokens=T)
-    ctx.set_path(api.PATH_SMALL)
+    ctx.set_path(path)
     ctx.route_stats(reset=True)
     rng = np.random.default_rng(31 + T)
     n = 2048 // T
@@ -248,7 +250,7 @@ def test_small_path_certified_routing(base, router_std, T):
     gg = torch.cat(ggs).cpu().numpy().reshape(-1)
     ri, rw, rg = O.route_batch(hl, x, nthreads=16)
     st = ctx.route_stats()
-    print(f"T={T} router std {router_std:.4f}: {st}", flush=True)
+    print(f"path {path} T={T} router std {router_std:.4f}: {st}", flush=True)
     assert int(np.sum(np.any(gi != ri, axis=1))) == 0
     assert np.all(np.abs(gw - rw) <= 1e-3 * np.abs(rw) + 1e-7), float(np.max(np.abs(gw - rw) / np.abs(rw)))
     rg = np.asarray(rg).reshape(-1)
