@@ -93,6 +93,7 @@ struct bread_small_ws {
     int32_t *slot_pair = nullptr;    // pair ids of each slot in token order [slots][4]
     int32_t *n_slots = nullptr;
     float *eo = nullptr;             // expert outputs by pair [T (K+1)][H]
+    uint8_t *xq = nullptr;           // activations in fixed point for k_sw_gateup [16][XQ_TOKEN_BYTES]
 };
 
 struct bread_moe_ctx {
@@ -198,7 +199,7 @@ int bread_launch_route_logits(const float *router, const uint16_t *shg, const fl
 // selection kernel (route_cert.h).
 bool bread_route_certified_ok(const bread_moe_ctx_t *c, int T);
 int bread_launch_route_fast(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, int T, float *gsh,
-                            float *radii, hipStream_t st);
+                            float *radii, uint8_t *xq, hipStream_t st);
 int bread_grouped_alloc(bread_moe_ctx_t *ctx);
 void bread_grouped_free(bread_moe_ctx_t *ctx);
 bool bread_grouped_supported(const bread_moe_shape_t &s, const bread_moe_layer_t *L);

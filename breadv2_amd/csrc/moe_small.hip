@@ -607,7 +607,8 @@ __global__ __launch_bounds__(256) void k_sb_combine(float *__restrict__ hidden, 
 // 8g..8g+7.  Each CU then has loads of all its slots in flight at once,
 // where the per-slot workgroups of the general kernels form chains of small
 // dependent steps.  The gate/up dots use the decode kernel's integer form
-// (x in 16-bit block fixed point, q4k_chunk_dot_q16); the down dots are fp32
+// (x in 16-bit block fixed point, q4k_chunk_dot_q16; k_route_fast converts
+// each token once, xq16_store); the down dots are fp32
 // on pre-decoded weights; the combine runs in the down kernel.
 
 constexpr int SW_G = 256;                                         // workgroups
@@ -641,35 +642,6 @@ struct SwGuSmem {
     float red[SW_NW][16];                    // each wave's reduced dots
 };
 static_assert(sizeof(SwGuSmem) <= 160 * 1024, "LDS");
-
-// x_t of columns 4c..4c+3 to fixed point (the decode kernel's conversion:
-// per 32-column block s = max|x| / 32511, x ~= s (256 hi + lo)); eight
-// consecutive lanes hold one block.
-__device__ __forceinline__ void sw_quant(SwGuSmem &M, int t, int c, float4 v)
-{
-    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    m = fmaxf(m, dpp_f<0xB1>(m));
-    m = fmaxf(m, dpp_f<0x4E>(m));
-    m = fmaxf(m, dpp_f<0x141>(m));
-    const float inv = m > 0.f ? 32511.0f / m : 0.f;
-    const float xv[4] = {v.x, v.y, v.z, v.w};
-    uint32_t hw = 0, lw = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int q = __float2int_rn(xv[k] * inv);
-        const int hi = (q + 128) >> 8;
-        const int lo = q - 256 * hi;
-        hw |= ((uint32_t)hi & 0xFFu) << (8 * k);
-        lw |= ((uint32_t)lo & 0xFFu) << (8 * k);
-    }
-    M.xqh[t][c] = hw;
-    M.xql[t][c] = lw;
-    if ((c & 7) == 0) M.xqs[t][c >> 3] = m / 32511.0f;
-    float r = (v.x + v.y) + (v.z + v.w);
-    r += dpp_f<0xB1>(r);
-    r += dpp_f<0x4E>(r);
-    if ((c & 3) == 0) M.xsum[t][c >> 2] = r;
-}
 
 // The slot's gate/up rows of this workgroup into the wave's LDS staging.
 __device__ __forceinline__ void sw_gu_issue(SwGuSmem &M, const SbLayer &L, int e, int g, int wid, int lane)
@@ -739,22 +711,25 @@ __device__ __forceinline__ float reduce16(const float (&v)[16], int lane)
     return y;
 }
 
-__global__ __launch_bounds__(SW_NT, 1) void k_sw_gateup(SbLayer L, const float *__restrict__ x, SbSlots S,
+__global__ __launch_bounds__(SW_NT, 1) void k_sw_gateup(SbLayer L, const uint8_t *__restrict__ xq, SbSlots S,
                                                         float *__restrict__ h, int E, int K, int T, int max_slots)
 {
     __shared__ SwGuSmem M;
+    static_assert(XQ_H == SW_H, "fixed-point record layout");
     const int g = (int)blockIdx.x, tid = (int)threadIdx.x, wid = tid / WAVE, lane = lane_id();
     const int P = T * (K + 1);
     int ns = *S.n;
     ns = ns < max_slots ? (ns > 0 ? ns : 0) : max_slots;
-    // activations requested first (a wait for them must not include the
-    // weights), then the first slot's weights, then the conversion
-    constexpr int XI = SW_MAX_T * (SW_H / 4) / SW_NT;  // conversion items a thread (8)
-    float4 xv[XI];
+    // the activations' fixed-point records requested first (a wait for them
+    // must not include the weights), then the first slot's weights, then the
+    // records into LDS
+    constexpr int XU = XQ_TOKEN_BYTES / 16;                   // 16-byte units a token (304)
+    constexpr int XI = (SW_MAX_T * XU + SW_NT - 1) / SW_NT;   // units a thread (5)
+    uint4 xr[XI];
 #pragma unroll
     for (int i = 0; i < XI; i++) {
-        const int it = SW_NT * i + tid, t = it / (SW_H / 4), c = it % (SW_H / 4);
-        xv[i] = t < T ? *reinterpret_cast<const float4 *>(x + (size_t)t * SW_H + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int it = SW_NT * i + tid;
+        xr[i] = it < T * XU ? reinterpret_cast<const uint4 *>(xq)[it] : make_uint4(0u, 0u, 0u, 0u);
     }
     int e0 = -2;
     if (wid < ns) {
@@ -763,8 +738,14 @@ __global__ __launch_bounds__(SW_NT, 1) void k_sw_gateup(SbLayer L, const float *
     }
 #pragma unroll
     for (int i = 0; i < XI; i++) {
-        const int it = SW_NT * i + tid, t = it / (SW_H / 4), c = it % (SW_H / 4);
-        if (t < T) sw_quant(M, t, c, xv[i]);
+        const int it = SW_NT * i + tid, t = it / XU, u = it % XU;
+        if (it < T * XU) {
+            uint4 *dst = u < XQ_LO / 16   ? reinterpret_cast<uint4 *>(&M.xqh[t][0]) + u
+                         : u < XQ_SC / 16 ? reinterpret_cast<uint4 *>(&M.xql[t][0]) + (u - XQ_LO / 16)
+                         : u < XQ_SUM / 16 ? reinterpret_cast<uint4 *>(&M.xqs[t][0]) + (u - XQ_SC / 16)
+                                           : reinterpret_cast<uint4 *>(&M.xsum[t][0]) + (u - XQ_SUM / 16);
+            *dst = xr[i];
+        }
     }
     __syncthreads();
     const int base = (lane >> 3) * QK + 64 * ((lane & 7) >> 1) + 16 * (lane & 1);  // the lane's columns (gu_base)
@@ -817,6 +798,11 @@ __global__ __launch_bounds__(SW_NT, 1) void k_sw_gateup(SbLayer L, const float *
         float v[16];
 #pragma unroll
         for (int k = 0; k < SB_CH; k++) {
+            if (k >= cnt) {  // wave-uniform: a slot's missing tokens cost nothing
+#pragma unroll
+                for (int m = 0; m < 4; m++) v[4 * m + k] = 0.f;
+                continue;
+            }
             const int t = pr[k] >= 0 ? pr[k] / (K + 1) : 0;
             const uint4 lh = *reinterpret_cast<const uint4 *>(&M.xqh[t][base >> 2]);
             const uint4 ll = *reinterpret_cast<const uint4 *>(&M.xql[t][base >> 2]);
@@ -838,7 +824,7 @@ __global__ __launch_bounds__(SW_NT, 1) void k_sw_gateup(SbLayer L, const float *
                 }
                 const float al = (float)(a_lh * 256 + a_ll) * sc.x;
                 const float ah = (float)(a_hh * 256 + a_hl) * sc.y;
-                v[4 * m + k] = k < cnt ? dsc0[m] * al - dm0[m] * sxl + dsc1[m] * ah - dm1[m] * sxh : 0.f;
+                v[4 * m + k] = dsc0[m] * al - dm0[m] * sxl + dsc1[m] * ah - dm1[m] * sxh;
             }
         }
         const float tot = reduce16(v, lane);
@@ -1092,6 +1078,7 @@ int bread_small_alloc(bread_moe_ctx_t *c)
     if (e == hipSuccess) e = hipMalloc((void **)&g.slot_pair, S * SB_CH * sizeof(int32_t));
     if (e == hipSuccess) e = hipMalloc((void **)&g.n_slots, sizeof(int32_t));
     if (e == hipSuccess) e = hipMalloc((void **)&g.eo, T * (K + 1) * H * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&g.xq, (size_t)SW_MAX_T * XQ_TOKEN_BYTES);
     if (e == hipSuccess) e = hipMemset(g.n_slots, 0, sizeof(int32_t));
     if (e == hipSuccess) e = hipMemset(g.slot_expert, 0, S * sizeof(int32_t));
     if (e == hipSuccess) e = hipMemset(g.slot_cnt, 0, S * sizeof(int32_t));
@@ -1107,6 +1094,7 @@ void bread_small_free(bread_moe_ctx_t *c)
     (void)hipFree(g.slot_pair);
     (void)hipFree(g.n_slots);
     (void)hipFree(g.eo);
+    (void)hipFree(g.xq);
     g = bread_small_ws{};
 }
 
@@ -1129,9 +1117,14 @@ int bread_launch_moe_small(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const
     // (k_sb_route); beyond the certified path's limits, the reference's
     // order for every logit and the host's selection (k_sb_select)
     const bool mv4 = E <= 4 * WAVE;
-    if (bread_route_certified_ok(c, T)) {
+    // the decode shape: every workgroup owns a slice of every slot
+    // (k_sw_gateup / k_sw_down), on the activations in fixed point that
+    // k_route_fast writes
+    const bool cert = bread_route_certified_ok(c, T);
+    const bool sw = cert && H == SW_H && I == SW_I && Ish == SW_I && K <= SW_K && T <= SW_MAX_T;
+    if (cert) {
         float *radii = c->h;
-        const int rc = bread_launch_route_fast(c, L, x, T, c->gsh, radii, st);
+        const int rc = bread_launch_route_fast(c, L, x, T, c->gsh, radii, sw ? g.xq : nullptr, st);
         if (rc) return rc;
         if (mv4)
             hipLaunchKernelGGL(k_sb_route<4>, dim3(1), dim3(RT_THREADS), 0, st, L->router, x, c->logits, radii, H, E,
@@ -1153,9 +1146,8 @@ int bread_launch_moe_small(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const
                                c->w, g.slot_expert, g.slot_cnt, g.slot_pair, g.n_slots);
     }
     BREAD_HIP(hipGetLastError());
-    if (H == SW_H && I == SW_I && Ish == SW_I && K <= SW_K && T <= SW_MAX_T) {
-        // the decode shape: every workgroup owns a slice of every slot
-        hipLaunchKernelGGL(k_sw_gateup, dim3(SW_G), dim3(SW_NT), 0, st, sl, x, ss, c->h, E, K, T, S);
+    if (sw) {
+        hipLaunchKernelGGL(k_sw_gateup, dim3(SW_G), dim3(SW_NT), 0, st, sl, g.xq, ss, c->h, E, K, T, S);
         const uint32_t spin = c->spin_limit >= 0 ? (uint32_t)c->spin_limit : SW_SPIN_DEFAULT;
         hipLaunchKernelGGL(k_sw_down, dim3(SW_G), dim3(SW_NT), 0, st, sl, c->h, ss, hidden, c->w, c->gsh, E, K, T,
                            S, &c->dsync->error.v, spin);

@@ -280,3 +280,48 @@ __device__ __forceinline__ float q4k_chunk_dot_sx(uint4 hd, uint4 q, uint32_t j,
     return (d * (float)sc0) * al - (dmin * (float)m0) * sl + (d * (float)sc1) * ah -
            (dmin * (float)m1) * sh;
 }
+
+// Activations in 16-bit block fixed point for the small-batch gate/up
+// kernel (H = 2048): per 32-column block s = max|x| / 32511 and x ~= s (256
+// hi + lo) with hi, lo signed bytes, plus fp32 sums of 16-column runs (the
+// min term).  One token's record, XQ_TOKEN_BYTES bytes: hi bytes [H / 4]
+// words (4 columns a word), lo bytes [H / 4], block scales [H / 32], run sums
+// [H / 16].
+constexpr int XQ_H = 2048;
+constexpr int XQ_HI = 0, XQ_LO = XQ_H, XQ_SC = 2 * XQ_H, XQ_SUM = 2 * XQ_H + XQ_H / 8;
+constexpr int XQ_TOKEN_BYTES = 2 * XQ_H + XQ_H / 8 + XQ_H / 4;
+
+// Thread i of 256 consecutive threads holds columns 8 i .. 8 i + 7 of one
+// token in v and writes their part of the token's record (blocks of 32
+// columns are four consecutive lanes).  Exactly the conversion the gate/up
+// kernel did itself: the same block maxima, scale, rounding and sum order.
+__device__ __forceinline__ void xq16_store(const float (&v)[8], int i, uint8_t *rec)
+{
+    float m = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) m = fmaxf(m, fabsf(v[k]));
+    m = fmaxf(m, dpp_f<0xB1>(m));  // quad_perm [1,0,3,2]
+    m = fmaxf(m, dpp_f<0x4E>(m));  // quad_perm [2,3,0,1]
+    const float inv = m > 0.f ? 32511.0f / m : 0.f;
+    uint32_t hw[2], lw[2];
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+        hw[hf] = 0;
+        lw[hf] = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int q = __float2int_rn(v[4 * hf + k] * inv);
+            const int hi = (q + 128) >> 8;
+            const int lo = q - 256 * hi;
+            hw[hf] |= ((uint32_t)hi & 0xFFu) << (8 * k);
+            lw[hf] |= ((uint32_t)lo & 0xFFu) << (8 * k);
+        }
+    }
+    *reinterpret_cast<uint2 *>(rec + XQ_HI + 8 * i) = make_uint2(hw[0], hw[1]);
+    *reinterpret_cast<uint2 *>(rec + XQ_LO + 8 * i) = make_uint2(lw[0], lw[1]);
+    if ((i & 3) == 0) reinterpret_cast<float *>(rec + XQ_SC)[i >> 2] = m / 32511.0f;
+    const float r0 = (v[0] + v[1]) + (v[2] + v[3]), r1 = (v[4] + v[5]) + (v[6] + v[7]);
+    float r = r0 + r1;
+    r += dpp_f<0xB1>(r);
+    if ((i & 1) == 0) reinterpret_cast<float *>(rec + XQ_SUM)[i >> 1] = r;
+}

@@ -18,6 +18,7 @@
 #include <mutex>
 
 #include "bread_internal.h"
+#include "quant_dot.h"
 #include "route_dev.h"
 #include "route_seq.h"
 
@@ -126,7 +127,8 @@ __global__ __launch_bounds__(CF_THREADS, 2) void k_route_fast(const float *__res
                                                              const uint16_t *__restrict__ shg, int has_shg,
                                                              const float *__restrict__ x, float *__restrict__ logits,
                                                              float *__restrict__ radii, float *__restrict__ gsh,
-                                                             int H, int E, int T, float coef_a)
+                                                             int H, int E, int T, float coef_a,
+                                                             uint8_t *__restrict__ xq)
 {
     static_assert(L % 4 == 0 && L <= 16 && TT <= CF_TT && NR * TT <= CF_THREADS, "columns, tokens, rows");
     __shared__ float s_tot[NR][TT][CF_WAVES], s_sp[NR][TT][CF_WAVES], s_a[NR][TT][CF_WAVES];
@@ -155,6 +157,19 @@ __global__ __launch_bounds__(CF_THREADS, 2) void k_route_fast(const float *__res
         const float *xt = x + (size_t)(t0 + (t < nt ? t : nt - 1)) * H + c0;
 #pragma unroll
         for (int j = 0; j < L / 4; j++) xv[t][j] = reinterpret_cast<const float4 *>(xt)[j];
+    }
+    // with xq (H = 2048 only): workgroup b < nt also writes token t0 + b's
+    // activations in the small-batch gate/up kernel's fixed-point form
+    if constexpr (L == 8) {
+        if (xq && (int)blockIdx.x < nt) {
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+                if (t == (int)blockIdx.x) {
+                    const float v[8] = {xv[t][0].x, xv[t][0].y, xv[t][0].z, xv[t][0].w,
+                                        xv[t][1].x, xv[t][1].y, xv[t][1].z, xv[t][1].w};
+                    xq16_store(v, tid, xq + (size_t)(t0 + t) * XQ_TOKEN_BYTES);
+                }
+        }
     }
     float inc[NR][TT], a[NR][TT];
 #pragma unroll
@@ -286,8 +301,10 @@ bool bread_route_certified_ok(const bread_moe_ctx_t *c, int T)
 }
 
 int bread_launch_route_fast(bread_moe_ctx_t *c, const bread_moe_layer_t *L, const float *x, int T, float *gsh,
-                            float *radii, hipStream_t st)
+                            float *radii, uint8_t *xq, hipStream_t st)
 {
+    BREAD_REQUIRE(!xq || (c->shape.hidden == XQ_H && T <= CF_TT), BREAD_ERR_SHAPE,
+                  "fixed-point activations need hidden 2048 and at most 16 tokens");
     const bread_moe_shape_t &s = c->shape;
     const int H = s.hidden, E = s.n_experts;
     const double u = 5.9604644775390625e-8, n = (double)H;
@@ -306,7 +323,7 @@ int bread_launch_route_fast(bread_moe_ctx_t *c, const bread_moe_layer_t *L, cons
     const dim3 grid((E + 1 + nr - 1) / nr, (T + tt - 1) / tt), block(CF_THREADS);
 #define BREAD_ROUTE_FAST(LL, TTT, NRR)                                                                       \
     hipLaunchKernelGGL((k_route_fast<LL, TTT, NRR>), grid, block, 0, st, L->router, g, has_g, x, c->logits, radii, \
-                       gsh, H, E, T, coef_a)
+                       gsh, H, E, T, coef_a, xq)
     switch (L1 * 1000 + tt * 10 + nr) {
     case 4041: BREAD_ROUTE_FAST(4, 4, 1); break;
     case 4081: BREAD_ROUTE_FAST(4, 8, 1); break;
