@@ -19,6 +19,7 @@
 
 #include "bread_device.h"
 #include "bread_internal.h"
+#include "q4k_mfma.h"
 
 namespace {
 
@@ -136,10 +137,6 @@ __global__ __launch_bounds__(AM_THREADS) void k_argmax_f16(const uint16_t *__res
 // and then: a slot read right after the issuing wave's vmcnt drained and a
 // barrier did not always hold the loaded bytes yet.)
 // ---------------------------------------------------------------------------
-typedef _Float16 hd_half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 hd_half2 __attribute__((ext_vector_type(2)));
-typedef float hd_f32x4 __attribute__((ext_vector_type(4)));
-
 constexpr int HD_MAXSB = 8;           // superblocks a row (H <= 2048): one compute wave each
 constexpr int HD_MAXT = 32;           // tokens a launch (two 16-token tiles)
 constexpr int HD_NRED = 4;            // reducing waves: one thread per (token, row) of a 16 x 16 tile
@@ -148,54 +145,6 @@ constexpr int HD_THREADS = 64 * (HD_MAXSB + HD_NRED);
 // 16-token tiles (two hold twice the x fragments)
 constexpr int HD_DEPTH1 = 4, HD_DEPTH2 = 3;
 constexpr int HD_GRID = 256;          // workgroups: one a CU (12 waves of up to 168 VGPRs)
-constexpr uint32_t HD_MAGIC = 0x64646464u;  // fp16 0x64xx = 1024 + xx
-
-// Four nibbles (bytes of v, each < 16) as two packed fp16 pairs of sc * q.
-__device__ __forceinline__ void hd_scq(uint32_t v, hd_half2 sc, hd_half2 nsc, uint32_t &p0, uint32_t &p1)
-{
-    const hd_half2 a = __builtin_bit_cast(hd_half2, __builtin_amdgcn_perm(HD_MAGIC, v, 0x07010700u));
-    const hd_half2 b = __builtin_bit_cast(hd_half2, __builtin_amdgcn_perm(HD_MAGIC, v, 0x07030702u));
-    p0 = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(a, sc, nsc));  // (1024 + q) sc - 1024 sc
-    p1 = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(b, sc, nsc));
-}
-
-// Eight consecutive elements' sc * q: the low (hi = 0) or high nibbles of
-// the bytes in (a, b).
-__device__ __forceinline__ hd_half8 hd_b8(uint32_t a, uint32_t b, int hi, hd_half2 sc, hd_half2 nsc)
-{
-    uint4 r;
-    hd_scq((a >> (4 * hi)) & 0x0F0F0F0Fu, sc, nsc, r.x, r.y);
-    hd_scq((b >> (4 * hi)) & 0x0F0F0F0Fu, sc, nsc, r.z, r.w);
-    return __builtin_bit_cast(hd_half8, r);
-}
-
-// A workgroup barrier that publishes the waves' LDS writes but leaves their
-// global loads in flight (__syncthreads would wait for every outstanding
-// load, the ring's tiles ahead included).  The asm memory clobber and the
-// scheduling barrier keep LDS accesses and the ring's loads on their side.
-__device__ __forceinline__ void hd_bar()
-{
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maxima
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-}
-
-// A lane's head and qs quarters of one superblock (row c, quarter g).
-struct HdRaw {
-    uint4 head;  // d, dmin, scales
-    uint4 q0;    // qs bytes [32 g, 32 g + 16)
-    uint4 q1;    // qs bytes [32 g + 16, 32 g + 32)
-};
-
-__device__ __forceinline__ void hd_load(HdRaw &r, const uint8_t *sb, int g)
-{
-    r.head = *reinterpret_cast<const uint4 *>(sb);
-    r.q0 = *reinterpret_cast<const uint4 *>(sb + 16 + 32 * g);
-    r.q1 = *reinterpret_cast<const uint4 *>(sb + 32 + 32 * g);
-}
 
 template <int NTT, int DEPTH>
 __global__ __launch_bounds__(HD_THREADS) void k_head_q4k(const uint8_t *__restrict__ w,
@@ -212,7 +161,7 @@ __global__ __launch_bounds__(HD_THREADS) void k_head_q4k(const uint8_t *__restri
     const int niter = ((int)blockIdx.x < ntile) ? (ntile - 1 - (int)blockIdx.x) / G + 1 : 0;
     if (wv < HD_MAXSB) {
         if (wv >= NSB) {  // no superblock: keep the barrier count
-            for (int it = 0; it < niter; it++) hd_bar();
+            for (int it = 0; it < niter; it++) q4m_bar();
             return;
         }
         const int g = l >> 4, c = l & 15;
@@ -238,11 +187,11 @@ __global__ __launch_bounds__(HD_THREADS) void k_head_q4k(const uint8_t *__restri
         // (an L2 hit): loads without a condition keep the compiler's vmcnt
         // waits counted rather than draining
         const uint8_t *wcol = w + (size_t)c * row_bytes + (size_t)wv * Q4K_BYTES;  // row c of tile 0
-        auto load = [&](HdRaw &r, int it) {
+        auto load = [&](Q4mRaw &r, int it) {
             const int ti = (int)blockIdx.x + std::min(it, niter - 1) * G;
-            hd_load(r, wcol + (size_t)16 * ti * row_bytes, g);
+            q4m_load(r, wcol + (size_t)16 * ti * row_bytes, g);
         };
-        HdRaw ring[DEPTH];
+        Q4mRaw ring[DEPTH];
 #pragma unroll
         for (int k = 0; k < DEPTH - 1; k++) load(ring[k], k);
         for (int it0 = 0; it0 < niter; it0 += DEPTH) {
@@ -251,24 +200,24 @@ __global__ __launch_bounds__(HD_THREADS) void k_head_q4k(const uint8_t *__restri
                 const int it = it0 + k;
                 if (it >= niter) break;
                 load(ring[(k + DEPTH - 1) % DEPTH], it + DEPTH - 1);
-                const HdRaw &b = ring[k];
+                const Q4mRaw &b = ring[k];
                 const float d = h2f(b.head.x & 0xFFFFu), dmin = h2f(b.head.x >> 16);
                 uint32_t sc0, m0, sc1, m1;
                 scale_min_k4(2 * g, b.head.y, b.head.z, b.head.w, sc0, m0);
                 scale_min_k4(2 * g + 1, b.head.y, b.head.z, b.head.w, sc1, m1);
                 const _Float16 s0 = (_Float16)(float)sc0, s1 = (_Float16)(float)sc1;
                 const _Float16 n0 = (_Float16)(-1024.f * (float)sc0), n1 = (_Float16)(-1024.f * (float)sc1);
-                const hd_half2 S0{s0, s0}, N0{n0, n0}, S1{s1, s1}, N1{n1, n1};
-                const hd_half8 bq[8] = {hd_b8(b.q0.x, b.q0.y, 0, S0, N0), hd_b8(b.q0.z, b.q0.w, 0, S0, N0),
-                                        hd_b8(b.q1.x, b.q1.y, 0, S0, N0), hd_b8(b.q1.z, b.q1.w, 0, S0, N0),
-                                        hd_b8(b.q0.x, b.q0.y, 1, S1, N1), hd_b8(b.q0.z, b.q0.w, 1, S1, N1),
-                                        hd_b8(b.q1.x, b.q1.y, 1, S1, N1), hd_b8(b.q1.z, b.q1.w, 1, S1, N1)};
+                const q4m_half2 S0{s0, s0}, N0{n0, n0}, S1{s1, s1}, N1{n1, n1};
+                const q4m_half8 bq[8] = {q4m_b8(b.q0.x, b.q0.y, 0, S0, N0), q4m_b8(b.q0.z, b.q0.w, 0, S0, N0),
+                                        q4m_b8(b.q1.x, b.q1.y, 0, S0, N0), q4m_b8(b.q1.z, b.q1.w, 0, S0, N0),
+                                        q4m_b8(b.q0.x, b.q0.y, 1, S1, N1), q4m_b8(b.q0.z, b.q0.w, 1, S1, N1),
+                                        q4m_b8(b.q1.x, b.q1.y, 1, S1, N1), q4m_b8(b.q1.z, b.q1.w, 1, S1, N1)};
 #pragma unroll
                 for (int tt = 0; tt < NTT; tt++) {
-                    hd_f32x4 acc = {0.f, 0.f, 0.f, 0.f}, accm = {0.f, 0.f, 0.f, 0.f};
+                    q4m_f32x4 acc = {0.f, 0.f, 0.f, 0.f}, accm = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int i = 0; i < 8; i++)
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(hd_half8, xf[tt][i]), bq[i],
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(q4m_half8, xf[tt][i]), bq[i],
                                                                      acc, 0, 0, 0);
                     accm = __builtin_amdgcn_mfma_f32_16x16x4f32(xm[tt][0], (float)m0, accm, 0, 0, 0);
                     accm = __builtin_amdgcn_mfma_f32_16x16x4f32(xm[tt][1], (float)m1, accm, 0, 0, 0);
@@ -276,7 +225,7 @@ __global__ __launch_bounds__(HD_THREADS) void k_head_q4k(const uint8_t *__restri
                     for (int i = 0; i < 4; i++)
                         part[it & 1][wv][16 * tt + 4 * g + i][c] = d * acc[i] - dmin * accm[i];
                 }
-                hd_bar();
+                q4m_bar();
             }
         }
         return;
@@ -294,7 +243,7 @@ __global__ __launch_bounds__(HD_THREADS) void k_head_q4k(const uint8_t *__restri
     // the barrier after tile it's partials are in part[it & 1]; reduced
     // while the compute waves work on tile it + 1
     for (int it = 0; it < niter; it++) {
-        hd_bar();
+        q4m_bar();
         const int ti = (int)blockIdx.x + it * G;
 #pragma unroll
         for (int tt = 0; tt < NTT; tt++) {
