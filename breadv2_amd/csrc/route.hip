@@ -93,7 +93,7 @@ __global__ __launch_bounds__(RS_WAVES * WAVE) void k_route_seq(const float *__re
 //   sum over chunk i of |S_k| <= L (|S_{Li}| + A_i),
 //   |S_{Li}| <= |P_i| + gamma_{L+10} A,  |F - S_n| <= gamma_{L+10} A,
 // so R = u (L SP + c A) with SP = sum_i |P_i| (exclusive prefixes) and
-// c = 2 L + 12 + n^2 u (the gamma terms for n <= 4096, L <= 16), widened by
+// c = 2 L + 12 + n^2 u (the gamma terms for n <= 2048, L <= 8), widened by
 // 2^-10 for the fp32 evaluation and by 1e-37 for underflow.
 constexpr int CF_TT = 16;        // tokens per workgroup at most (TT)
 constexpr int CF_THREADS = 256;  // threads per router row
@@ -130,7 +130,7 @@ __global__ __launch_bounds__(CF_THREADS, 2) void k_route_fast(const float *__res
                                                              int H, int E, int T, float coef_a,
                                                              uint8_t *__restrict__ xq)
 {
-    static_assert(L % 4 == 0 && L <= 16 && TT <= CF_TT && NR * TT <= CF_THREADS, "columns, tokens, rows");
+    static_assert(L % 4 == 0 && L <= 8 && TT <= CF_TT && NR * TT <= CF_THREADS, "columns, tokens, rows");
     __shared__ float s_tot[NR][TT][CF_WAVES], s_sp[NR][TT][CF_WAVES], s_a[NR][TT][CF_WAVES];
     const int tid = (int)threadIdx.x, wv = tid / WAVE, lane = lane_id();
     const int r0 = NR * (int)blockIdx.x, t0 = (int)blockIdx.y * TT;
@@ -296,7 +296,7 @@ bool bread_route_certified_ok(const bread_moe_ctx_t *c, int T)
     const int H = s.hidden, E = s.n_experts, K = s.top_k;
     const int Imax = s.expert_inter > s.shared_inter ? s.expert_inter : s.shared_inter;
     const size_t hcap = (size_t)c->max_tokens * (K + 1) * Imax;
-    return T >= 1 && T <= CF_MAX_T && H % (4 * CF_THREADS) == 0 && H <= 4096 && E <= 16 * WAVE && K >= 1 &&
+    return T >= 1 && T <= CF_MAX_T && (H == 4 * CF_THREADS || H == 8 * CF_THREADS) && E <= 16 * WAVE && K >= 1 &&
            K <= CF_MAX_K && K <= E && (size_t)T * E <= hcap;
 }
 
@@ -313,12 +313,11 @@ int bread_launch_route_fast(bread_moe_ctx_t *c, const bread_moe_layer_t *L, cons
     // router's first row instead (and stores zeros)
     const uint16_t *g = L->shexp_gate ? L->shexp_gate : reinterpret_cast<const uint16_t *>(L->router);
     const int has_g = L->shexp_gate ? 1 : 0;
-    // tokens per workgroup: the fewest of 4, 8, 16 that hold T (8 at most
-    // for L > 8, where 16 tokens' columns would not fit the registers);
-    // beyond 16 tokens each workgroup takes 4 router rows (rows share every
-    // activation read: each row workgroup reads all of its tokens' columns)
+    // tokens per workgroup: the fewest of 4, 8, 16 that hold T; beyond 16
+    // tokens each workgroup takes 4 router rows (rows share every activation
+    // read: each row workgroup reads all of its tokens' columns)
     const int L1 = H / CF_THREADS;
-    const int tt = T <= 4 ? 4 : (T <= 8 || L1 > 8 || T > 16 ? 8 : 16);
+    const int tt = T <= 4 ? 4 : (T <= 8 || T > 16 ? 8 : 16);
     const int nr = T > 16 ? 4 : 1;
     const dim3 grid((E + 1 + nr - 1) / nr, (T + tt - 1) / tt), block(CF_THREADS);
 #define BREAD_ROUTE_FAST(LL, TTT, NRR)                                                                       \
@@ -333,14 +332,8 @@ int bread_launch_route_fast(bread_moe_ctx_t *c, const bread_moe_layer_t *L, cons
     case 8081: BREAD_ROUTE_FAST(8, 8, 1); break;
     case 8161: BREAD_ROUTE_FAST(8, 16, 1); break;
     case 8084: BREAD_ROUTE_FAST(8, 8, 4); break;
-    case 12041: BREAD_ROUTE_FAST(12, 4, 1); break;
-    case 12081: BREAD_ROUTE_FAST(12, 8, 1); break;
-    case 12084: BREAD_ROUTE_FAST(12, 8, 4); break;
-    case 16041: BREAD_ROUTE_FAST(16, 4, 1); break;
-    case 16081: BREAD_ROUTE_FAST(16, 8, 1); break;
-    case 16084: BREAD_ROUTE_FAST(16, 8, 4); break;
     default:
-        return bread_fail(BREAD_ERR_SHAPE, "bread_launch_route_fast", "hidden must be 1024, 2048, 3072 or 4096");
+        return bread_fail(BREAD_ERR_SHAPE, "bread_launch_route_fast", "hidden must be 1024 or 2048");
     }
 #undef BREAD_ROUTE_FAST
     BREAD_HIP(hipGetLastError());

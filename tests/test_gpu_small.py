@@ -108,11 +108,13 @@ def test_small_all_tokens_same_experts(full_layer):
 
 @pytest.mark.parametrize("dims", [(512, 256, 256, 16, 2, 5), (1024, 256, 512, 40, 4, 19),
                                   (768, 512, 256, 64, 8, 32), (2048, 512, 512, 300, 8, 12),
-                                  (256, 512, 256, 1024, 16, 9)])
+                                  (256, 512, 256, 1024, 16, 9), (2048, 256, 512, 1024, 16, 10),
+                                  (1024, 512, 256, 96, 12, 3)])
 def test_small_other_shapes(dims):
     """Hidden 256..2048 (lanes of superblocks beyond H idle), intermediate 256
     or 512 with the shared expert narrower or wider, E up to 1024 (the wide
-    top-k), K up to 16."""
+    top-k), K up to 16.  Hidden 1024 and 2048 route by certified fast sums
+    (1024 experts and top-16 included), the others in the reference's order."""
     H, I, Ish, E, K, T = dims
     s = api.shape(hidden=H, expert_inter=I, shared_inter=Ish, n_experts=E, top_k=K)
     t = api.synth_layer_tensors(s, seed=11 + E, layer=0)
