@@ -602,48 +602,78 @@ __device__ __forceinline__ void gu_compute(const Smem &S, const uint4 (*w)[WAVE]
 // [8t, 8t+8), t = lane%4 (the Q6_K unit of quant_dot.h), i.e. the 32 weights
 // at columns b*256 + 128n + 32s + 8t + k, s < 4, k < 8.
 //
-// Pre-decode: w[8s + k] = (d * sc) * (q - 32), the dequantised weight
-// (dequant_q4k_cpu.c:155-170, same rounding order).
-__device__ __forceinline__ void down_predecode(const Smem &S, int u, int sb, float (&w)[32])
+// Pre-decode: the lane's 32 quants q - 32 as fp16 pairs (exact: the byte
+// placed under the fp16 exponent of 1024 gives 1024 + q, and subtracting
+// 1056 leaves q - 32), q[2i] in the low half of word i, with the group
+// scale d * sc (exact in fp32: 11 x 8 bits) of each run s of 8 weights.  The
+// dot then takes sum_s (d sc_s) sum_k (q - 32) h with the fp16 operand
+// widened inside the FMA (v_fma_mix_f32): the weight is the dequantised
+// d * sc * (q - 32) of dequant_q4k_cpu.c:155-170 with the product rounded
+// once per run instead of once per weight, and the pre-decode costs one
+// permute and half a packed subtraction per weight instead of a conversion
+// and an FMA.
+typedef _Float16 dn_half2 __attribute__((ext_vector_type(2)));
+
+struct DnWeights {
+    uint32_t q[16];  // fp16 pairs (q - 32): word 4s + 2 half + j holds k = 4 half + 2j, +1 of run s
+    float ds[4];     // d * sc of run s
+};
+
+__device__ __forceinline__ uint32_t q6_pair_f16(uint32_t q, uint32_t sel)
+{
+    const uint32_t p = __builtin_amdgcn_perm(0x64646464u, q, sel);
+    const dn_half2 v = __builtin_bit_cast(dn_half2, p) - (dn_half2){(_Float16)1056.0f, (_Float16)1056.0f};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ void down_predecode(const Smem &S, int u, int sb, DnWeights &w)
 {
     const int lane = opaque(lane_id());
     const int slot = u >> 1;
     const int row = 4 * (u & 1) + (lane >> 4);
     const int b = (lane >> 3) & 1, n = (lane >> 2) & 1, t = lane & 3;
     const uint32_t *band = slot == 0 ? S.sdown[sb] : S.down + (slot - 1) * (BAND / 4);
+    // the superblock starts 2 b bytes past a word boundary (rows are 420
+    // bytes, superblocks 210), as do all of its fields the lane reads:
+    // words from one aligned base with constant offsets, then byte shifts
     const uint32_t ob = (uint32_t)(row * DN_ROW + b * Q6K_BYTES);
-    const uint2 ql0 = lds8_a2(band, ob + 64 * n + 8 * t);
-    const uint2 ql1 = lds8_a2(band, ob + 64 * n + 32 + 8 * t);
-    const uint2 qh = lds8_a2(band, ob + 128 + 32 * n + 8 * t);
-    const uint2 scw = lds8_a2(band, ob + 192 + 8 * n);
-    const float d = h2f(lds16_a2(band, ob + 208));
+    const uint32_t sh = ob & 3u;
+    const uint32_t *p = band + (ob >> 2);
+    const uint32_t *pa = p + 16 * n + 2 * t, *pb = p + 8 * n + 2 * t, *pc = p + 2 * n;
+    const uint2 ql0 = make_uint2(__builtin_amdgcn_alignbyte(pa[1], pa[0], sh), __builtin_amdgcn_alignbyte(pa[2], pa[1], sh));
+    const uint2 ql1 = make_uint2(__builtin_amdgcn_alignbyte(pa[9], pa[8], sh), __builtin_amdgcn_alignbyte(pa[10], pa[9], sh));
+    const uint2 qh = make_uint2(__builtin_amdgcn_alignbyte(pb[33], pb[32], sh), __builtin_amdgcn_alignbyte(pb[34], pb[33], sh));
+    const uint2 scw = make_uint2(__builtin_amdgcn_alignbyte(pc[49], pc[48], sh), __builtin_amdgcn_alignbyte(pc[50], pc[49], sh));
+    const float d = h2f((p[52] >> (8u * sh)) & 0xFFFFu);
     const uint32_t i2 = (uint32_t)t >> 1;
+#pragma unroll
+    for (int s = 0; s < 4; s++) w.ds[s] = d * q6k_scale(scw, i2 + 2 * s);
 #pragma unroll
     for (int half = 0; half < 2; half++) {
         uint32_t q[4];
         q6k_unpack(half ? ql0.y : ql0.x, half ? ql1.y : ql1.x, half ? qh.y : qh.x, q);
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            // fma(q, ds, -32 ds) rounds ds * (q - 32) once (-32 ds is exact):
-            // the same bits as the product, one instruction fewer
-            const float ds = d * q6k_scale(scw, i2 + 2 * s);
-            const float nds = -32.0f * ds;
-#pragma unroll
-            for (int k = 0; k < 4; k++) w[8 * s + 4 * half + k] = fmaf((float)byte_of(q[s], k), ds, nds);
+            // bytes 0, 1 and 2, 3 of q[s] under the fp16 exponent byte 0x64
+            w.q[4 * s + 2 * half] = q6_pair_f16(q[s], 0x04010400u);
+            w.q[4 * s + 2 * half + 1] = q6_pair_f16(q[s], 0x04030402u);
         }
     }
 }
 
 // Down units beyond the 16 waves (u >= 16, only for K = 8) are pre-decoded by
 // waves 1 and 2 into their own gate/up staging slot of LDS, free once their
-// gate/up is done: element 8s + k of lane i at float4 [2s + k/4][i].
-__device__ __forceinline__ void predecode_to_lds(const Smem &S, int u, int sb, float4 (*dst)[WAVE])
+// gate/up is done: the quant words of lane i at uint4 [0..3][i], the run
+// scales at [4][i].
+__device__ __forceinline__ void predecode_to_lds(const Smem &S, int u, int sb, uint4 (*dst)[WAVE])
 {
-    float w[32];
+    DnWeights w;
     down_predecode(S, u, sb, w);
     const int lane = opaque(lane_id());
 #pragma unroll
-    for (int q = 0; q < 8; q++) dst[q][lane] = make_float4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
+    for (int q = 0; q < 4; q++) dst[q][lane] = make_uint4(w.q[4 * q], w.q[4 * q + 1], w.q[4 * q + 2], w.q[4 * q + 3]);
+    dst[4][lane] = make_uint4(__builtin_bit_cast(uint32_t, w.ds[0]), __builtin_bit_cast(uint32_t, w.ds[1]),
+                              __builtin_bit_cast(uint32_t, w.ds[2]), __builtin_bit_cast(uint32_t, w.ds[3]));
 }
 
 // Position of column c of a slot's SwiGLU row in LDS.  A down lane reads its
@@ -659,7 +689,14 @@ __device__ __forceinline__ int hpos(int c)
     return 64 * (2 * s + (k >> 2)) + 32 * b + 16 * n + 4 * t + (k & 3);
 }
 
-__device__ __forceinline__ float down_acc(const Smem &S, int u, const float (&w)[32])
+// fp16 weight pair times two fp32 values, accumulated in fp32 (v_fma_mix_f32)
+__device__ __forceinline__ float dn_fma2(uint32_t wp, float x0, float x1, float a)
+{
+    const dn_half2 h = __builtin_bit_cast(dn_half2, wp);
+    return fmaf((float)h.y, x1, fmaf((float)h.x, x0, a));
+}
+
+__device__ __forceinline__ float down_acc(const Smem &S, int u, const DnWeights &w)
 {
     const int lane = opaque(lane_id());
     const int slot = u >> 1;
@@ -670,34 +707,34 @@ __device__ __forceinline__ float down_acc(const Smem &S, int u, const float (&w)
     for (int s = 0; s < 4; s++) {
         const float4 v0 = *reinterpret_cast<const float4 *>(hs + 128 * s);
         const float4 v1 = *reinterpret_cast<const float4 *>(hs + 128 * s + 64);
-        acc = fmaf(w[8 * s + 0], v0.x, acc);
-        acc = fmaf(w[8 * s + 1], v0.y, acc);
-        acc = fmaf(w[8 * s + 2], v0.z, acc);
-        acc = fmaf(w[8 * s + 3], v0.w, acc);
-        acc = fmaf(w[8 * s + 4], v1.x, acc);
-        acc = fmaf(w[8 * s + 5], v1.y, acc);
-        acc = fmaf(w[8 * s + 6], v1.z, acc);
-        acc = fmaf(w[8 * s + 7], v1.w, acc);
+        float r = dn_fma2(w.q[4 * s], v0.x, v0.y, 0.f);
+        r = dn_fma2(w.q[4 * s + 1], v0.z, v0.w, r);
+        r = dn_fma2(w.q[4 * s + 2], v1.x, v1.y, r);
+        r = dn_fma2(w.q[4 * s + 3], v1.z, v1.w, r);
+        acc = fmaf(w.ds[s], r, acc);
     }
     return sum16(acc);
 }
 
-__device__ __forceinline__ void down_dot(Smem &S, int u, const float (&w)[32])
+__device__ __forceinline__ void down_dot(Smem &S, int u, const DnWeights &w)
 {
     const int lane = opaque(lane_id());
     const float acc = down_acc(S, u, w);
     if ((lane & 15) == 0) S.dot[u >> 1][4 * (u & 1) + (lane >> 4)] = acc;
 }
 
-__device__ __forceinline__ void down_dot_lds(Smem &S, int u, const float4 (*src)[WAVE])
+__device__ __forceinline__ void down_dot_lds(Smem &S, int u, const uint4 (*src)[WAVE])
 {
     const int lane = opaque(lane_id());
-    float w[32];
+    DnWeights w;
 #pragma unroll
-    for (int q = 0; q < 8; q++) {
-        const float4 v = src[q][lane];
-        w[4 * q] = v.x; w[4 * q + 1] = v.y; w[4 * q + 2] = v.z; w[4 * q + 3] = v.w;
+    for (int q = 0; q < 4; q++) {
+        const uint4 v = src[q][lane];
+        w.q[4 * q] = v.x; w.q[4 * q + 1] = v.y; w.q[4 * q + 2] = v.z; w.q[4 * q + 3] = v.w;
     }
+    const uint4 v = src[4][lane];
+    w.ds[0] = __builtin_bit_cast(float, v.x); w.ds[1] = __builtin_bit_cast(float, v.y);
+    w.ds[2] = __builtin_bit_cast(float, v.z); w.ds[3] = __builtin_bit_cast(float, v.w);
     const float acc = down_acc(S, u, w);
     if ((lane & 15) == 0) S.dot[u >> 1][4 * (u & 1) + (lane >> 4)] = acc;
 }
@@ -1528,9 +1565,9 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
         // LDS, polled: chunk c = (workgroup w, q): float4 q of w's record
         // holds slots 2q and 2q+1 (rows 2w, 2w+1).  A polling wave issues its
         // first poll before the pre-decode, so the round trip overlaps it.
-        float w0[32];
+        DnWeights w0;
         const bool extra = wid >= W_GU && wid < W_GU + 2 && wid - W_GU + NWV < NU;
-        float4 (*xw)[WAVE] = reinterpret_cast<float4 (*)[WAVE]>(&S.gu[wid >= W_GU && wid < W_GU + 2 ? wid - W_GU : 0][0][0]);
+        uint4 (*xw)[WAVE] = &S.gu[wid >= W_GU && wid < W_GU + 2 ? wid - W_GU : 0][0];
         // (after every routed gate/up is computed: the pre-decode would
         // otherwise take VALU time from the gate/up dots)
         const bool pre = wid < NU && lds_wait(S, &S.dncnt, N_DN) && lds_wait(S, &S.gudone, K);
