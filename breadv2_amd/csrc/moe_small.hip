@@ -761,11 +761,14 @@ __global__ __launch_bounds__(SW_NT, 1) void k_sw_gateup(SbLayer L, const uint8_t
         const int cnt_s = __builtin_amdgcn_readfirstlane(S.cnt[s]);
         const bool ok = e >= -1 && e < E;
         const int cnt = ok ? (cnt_s < SB_CH ? (cnt_s > 0 ? cnt_s : 0) : SB_CH) : 0;
-        int pr[SB_CH];
+        int pr[SB_CH], tk[SB_CH];
 #pragma unroll
         for (int k = 0; k < SB_CH; k++) {
             const int p = k < cnt ? __builtin_amdgcn_readfirstlane(S.pair[(size_t)s * SB_CH + k]) : -1;
             pr[k] = p >= 0 && p < P ? p : -1;
+            // the pair's token, divided on the scalar unit (the pair index
+            // is wave-uniform; a vector division costs ~15 instructions a token)
+            tk[k] = __builtin_amdgcn_readfirstlane(pr[k] >= 0 ? pr[k] : 0) / (K + 1);
         }
         __builtin_amdgcn_s_waitcnt(0);  // this wave's staging has landed
         // the four row chunks of the lane (m = 2 mat + row: gate rows 0, 1,
@@ -803,7 +806,7 @@ __global__ __launch_bounds__(SW_NT, 1) void k_sw_gateup(SbLayer L, const uint8_t
                 for (int m = 0; m < 4; m++) v[4 * m + k] = 0.f;
                 continue;
             }
-            const int t = pr[k] >= 0 ? pr[k] / (K + 1) : 0;
+            const int t = tk[k];
             const uint4 lh = *reinterpret_cast<const uint4 *>(&M.xqh[t][base >> 2]);
             const uint4 ll = *reinterpret_cast<const uint4 *>(&M.xql[t][base >> 2]);
             const uint4 hh = *reinterpret_cast<const uint4 *>(&M.xqh[t][(base >> 2) + 8]);
@@ -814,16 +817,23 @@ __global__ __launch_bounds__(SW_NT, 1) void k_sw_gateup(SbLayer L, const uint8_t
             const uint32_t xhh[4] = {hh.x, hh.y, hh.z, hh.w}, xhl[4] = {hl.x, hl.y, hl.z, hl.w};
 #pragma unroll
             for (int m = 0; m < 4; m++) {
-                int a_lh = 0, a_ll = 0, a_hh = 0, a_hl = 0;
+                // 256 sum(q hi) + sum(q lo) in one chain per nibble half
+                // (exact: below 2^23), one zeroed accumulator each
+                int a_l = 0, a_h = 0;
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    a_lh = __builtin_amdgcn_sdot4((int)qlo[m][q], (int)xlh[q], a_lh, false);
-                    a_ll = __builtin_amdgcn_sdot4((int)qlo[m][q], (int)xll[q], a_ll, false);
-                    a_hh = __builtin_amdgcn_sdot4((int)qhi[m][q], (int)xhh[q], a_hh, false);
-                    a_hl = __builtin_amdgcn_sdot4((int)qhi[m][q], (int)xhl[q], a_hl, false);
+                    a_l = __builtin_amdgcn_sdot4((int)qlo[m][q], (int)xlh[q], a_l, false);
+                    a_h = __builtin_amdgcn_sdot4((int)qhi[m][q], (int)xhh[q], a_h, false);
                 }
-                const float al = (float)(a_lh * 256 + a_ll) * sc.x;
-                const float ah = (float)(a_hh * 256 + a_hl) * sc.y;
+                a_l *= 256;
+                a_h *= 256;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    a_l = __builtin_amdgcn_sdot4((int)qlo[m][q], (int)xll[q], a_l, false);
+                    a_h = __builtin_amdgcn_sdot4((int)qhi[m][q], (int)xhl[q], a_h, false);
+                }
+                const float al = (float)a_l * sc.x;
+                const float ah = (float)a_h * sc.y;
                 v[4 * m + k] = dsc0[m] * al - dm0[m] * sxl + dsc1[m] * ah - dm1[m] * sxh;
             }
         }

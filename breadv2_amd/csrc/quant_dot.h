@@ -239,18 +239,23 @@ __device__ __forceinline__ float q4k_chunk_dot_q16(uint4 hd, uint4 q, uint32_t j
     const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
     const uint32_t xlh[4] = {lh.x, lh.y, lh.z, lh.w}, xll[4] = {ll.x, ll.y, ll.z, ll.w};
     const uint32_t xhh[4] = {hh.x, hh.y, hh.z, hh.w}, xhl[4] = {hl.x, hl.y, hl.z, hl.w};
-    int a_lh = 0, a_ll = 0, a_hh = 0, a_hl = 0;
+    // 256 sum(q hi) + sum(q lo) in one chain per nibble half (exact: below
+    // 2^23), one zeroed accumulator each
+    int a_l = 0, a_h = 0;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-        const int lo = (int)(qw[t] & 0x0F0F0F0Fu);
-        const int hi = (int)((qw[t] >> 4) & 0x0F0F0F0Fu);
-        a_lh = __builtin_amdgcn_sdot4(lo, (int)xlh[t], a_lh, false);
-        a_ll = __builtin_amdgcn_sdot4(lo, (int)xll[t], a_ll, false);
-        a_hh = __builtin_amdgcn_sdot4(hi, (int)xhh[t], a_hh, false);
-        a_hl = __builtin_amdgcn_sdot4(hi, (int)xhl[t], a_hl, false);
+        a_l = __builtin_amdgcn_sdot4((int)(qw[t] & 0x0F0F0F0Fu), (int)xlh[t], a_l, false);
+        a_h = __builtin_amdgcn_sdot4((int)((qw[t] >> 4) & 0x0F0F0F0Fu), (int)xhh[t], a_h, false);
     }
-    const float al = (float)(a_lh * 256 + a_ll) * s_lo;
-    const float ah = (float)(a_hh * 256 + a_hl) * s_hi;
+    a_l *= 256;
+    a_h *= 256;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        a_l = __builtin_amdgcn_sdot4((int)(qw[t] & 0x0F0F0F0Fu), (int)xll[t], a_l, false);
+        a_h = __builtin_amdgcn_sdot4((int)((qw[t] >> 4) & 0x0F0F0F0Fu), (int)xhl[t], a_h, false);
+    }
+    const float al = (float)a_l * s_lo;
+    const float ah = (float)a_h * s_hi;
     return (d * (float)sc0) * al - (dmin * (float)m0) * sl + (d * (float)sc1) * ah -
            (dmin * (float)m1) * sh;
 }
