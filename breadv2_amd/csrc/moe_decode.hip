@@ -306,8 +306,11 @@ __device__ __forceinline__ void lds_expire(Smem &S)
 }
 
 // Wave-level bounded wait for an LDS flag; false if the workgroup aborts or
-// the wait runs out (lds_expire).  slow: sleep longer between looks (for
-// waits expected to last microseconds).
+// the wait runs out (lds_expire).  A look is one LDS read with no sleep
+// after it, and the abort flag is read every 16th look: measured, the
+// single-layer launch is 0.19 us shorter than with a 64-cycle sleep and the
+// abort flag read at every look (longer sleeps cost 0.2-0.4 us).  slow:
+// sleep between looks (for waits expected to last microseconds).
 __device__ __forceinline__ bool lds_wait(Smem &S, const int *p, int target, bool slow = false)
 {
     const uint32_t lim = S.spin;
@@ -316,10 +319,10 @@ __device__ __forceinline__ bool lds_wait(Smem &S, const int *p, int target, bool
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             return true;
         }
-        if (lds_get(&S.abort)) return false;
+        if ((it & 15) == 15 && lds_get(&S.abort)) return false;
         if (it >= lim) break;
         if (slow) __builtin_amdgcn_s_sleep(8);
-        else __builtin_amdgcn_s_sleep(1);
+        else __builtin_amdgcn_s_sleep(0);
     }
     lds_expire(S);
     return false;
