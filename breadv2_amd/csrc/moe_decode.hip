@@ -1541,7 +1541,9 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecArgs a)
                 __builtin_amdgcn_s_setprio(0);
                 trace_point_lane0(a, l, TP_CERT);
             }
-            bool ok = lds_wait(S, &S.nready, K);
+            // (sleeping between looks: the bands are needed microseconds later,
+            // and a spinning wave takes issue slots from the selection passes)
+            bool ok = lds_wait(S, &S.nready, K, true);
             for (int round = 0; round < 2 && ok; round++) {
 #pragma unroll
                 for (int i = 0; i < DN_LOADS; i++) {
