@@ -38,8 +38,9 @@
 // Routing is published rank by rank: wave 0 writes expert k to LDS as soon as
 // selection pass k ends, and the gate/up and down waves start that slot's
 // loads at once, so the top-k passes overlap the expert streams.  The Q6_K
-// down weights are dequantised into registers while h is in flight; after it
-// arrives only the dot products remain.
+// down weights are unpacked into registers while h is in flight (exact fp16
+// quants q - 32 and fp32 run scales d * sc); after it arrives only the dot
+// products remain.
 //
 // Three exchanges per layer cross workgroups, each carried by the data
 // itself (no counters, no atomics, no waits for store completion):
