@@ -83,8 +83,6 @@ struct bread_grouped_ws {
     int *work = nullptr;                  // per-XCD work lists of the two expert GEMMs
     int *n_work = nullptr;                // their lengths [2][8]
     float *eo = nullptr;                  // expert outputs by pair [max_tokens*(K+1)][H]
-    void *hhi = nullptr, *hlo = nullptr;  // SwiGLU outputs as hi/lo fp16 by pair [max_tokens*(K+1)][Imax]
-    int *hexp = nullptr;                  // their row scale exponents [max_tokens*(K+1)]
 };
 
 struct bread_small_ws {

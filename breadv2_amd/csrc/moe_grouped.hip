@@ -40,9 +40,8 @@
 //   k_mt_bucket   one workgroup: expert histogram, token lists by expert,
 //                 M-tiles of 32 pairs
 //   k_mt_gateup   per (M-tile, 128 rows): gate and up GEMMs, SwiGLU
-//   k_mt_hprep    one wave per pair: row scale, hi/lo fp16 in the down
-//                 operand order
-//   k_mt_down     per (M-tile, 512 rows): down GEMM
+//   k_mt_down     per (M-tile, 512 rows): the tile's SwiGLU rows split into
+//                 hi/lo fp16 with a row scale, then the down GEMM
 //   k_mt_combine  per token: shared expert, then routed experts in rank order
 // The shared expert is expert index E with every token, so both GEMMs treat
 // it like a routed expert with its own weights.
@@ -91,8 +90,6 @@ struct MtArgs {
     const int *n_work;             // [2][NXCD] items per XCD (gate/up, down)
     int slots_gu, slots_dn;        // list capacity per XCD
     float *h;                // [T*K + T][Imax] SwiGLU outputs by pair
-    const uint4 *hhi, *hlo;  // the same as hi/lo fp16 units in the down operand order
-    const int *hexp;         // [T*K + T] their row scale exponents
     float *eo;               // [T*K + T][H] expert outputs by pair
 };
 
@@ -637,44 +634,11 @@ __global__ __launch_bounds__(GU_WAVES * WAVE, 2) void k_mt_gateup(const MtArgs a
     }
 }
 
-// One wave per pair row p (rows T*K .. T*K+T-1 are the shared expert's):
-// the SwiGLU row scaled by a power of two and split into hi/lo fp16, unit
-// ((16b + t)*2 + g) of the row holding elements 256b + 128g + 8t .. +7.
-__global__ __launch_bounds__(256) void k_mt_hprep(const float *__restrict__ h, int n_rows, int n_routed, int I,
-                                                  int Ish, int Imax, uint4 *__restrict__ hhi,
-                                                  uint4 *__restrict__ hlo, int *__restrict__ hexp)
-{
-    const int p = blockIdx.x * 4 + (int)(threadIdx.x / WAVE);
-    if (p >= n_rows) return;
-    const int lane = lane_id();
-    const int n = (p < n_routed ? I : Ish) / 8;
-    const float *hr = h + (size_t)p * Imax;
-    float mx = 0.f;
-    for (int v = lane; v < n; v += WAVE) {
-        const float4 a = *reinterpret_cast<const float4 *>(hr + 8 * v);
-        const float4 b = *reinterpret_cast<const float4 *>(hr + 8 * v + 4);
-        mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
-                             fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
-    }
-    const int e = row_exp(wave_max(mx));
-    if (lane == 0) hexp[p] = e;
-    for (int v = lane; v < n; v += WAVE) {
-        const float4 a = *reinterpret_cast<const float4 *>(hr + 8 * v);
-        const float4 b = *reinterpret_cast<const float4 *>(hr + 8 * v + 4);
-        const float x8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        uint4 hi, lo;
-        split8(x8, e, hi, lo);
-        const int u = (16 * (v >> 5) + (v & 15)) * 2 + ((v >> 4) & 1);
-        hhi[(size_t)p * (Imax / 8) + u] = hi;
-        hlo[(size_t)p * (Imax / 8) + u] = lo;
-    }
-}
-
 // ---------------------------------------------------------------------------
 // Down: tile (M-tile, 512 output rows).  Wave w owns rows n0 + 64w + [0, 64)
-// as two 32-row blocks.  The tile's SwiGLU rows, already split by
-// k_mt_hprep, are staged once by LDS-direct loads (hi and lo fp16, 64 KB for
-// I = 512); each wave walks its (block, superblock) items loading the next
+// as two 32-row blocks.  The tile's fp32 SwiGLU rows are read once, scaled
+// by a power of two per row and split into hi and lo fp16 parts in LDS (64 KB
+// for I = 512); each wave walks its (block, superblock) items loading the next
 // item's raw Q6_K bytes into registers while dequantising the current one.
 // ---------------------------------------------------------------------------
 
@@ -688,7 +652,7 @@ __global__ __launch_bounds__(DN_WAVES * WAVE, 2) void k_mt_down(const MtArgs a)
     const bool sh = tl.e == a.E;
     const int I = sh ? a.Ish : a.I;
     const int n0 = chunk * DN_ROWS;
-    const int tid = threadIdx.x, w = wave_id(), lane = lane_id();
+    const int w = wave_id(), lane = lane_id();
     const int g = lane >> 5, r = lane & 31;
     const int nb = I / QK;
     const uint64_t rbd = (uint64_t)nb * Q6K_BYTES;
@@ -705,18 +669,47 @@ __global__ __launch_bounds__(DN_WAVES * WAVE, 2) void k_mt_down(const MtArgs a)
     if (items > 0) q6k_load(item_ptr(0), g, R0);
 
     {
-        // the tile's activation units: LDS unit ((16b + t)*2 + g)*32 + n
-        // holds unit (16b + t)*2 + g of pair row p0 + n; wave w loads LDS
-        // units 64q + lane for q = w, w + DN_WAVES, ...
-        const int n = lane & 31, hu = a.Imax / 8;
-        const size_t prow = (size_t)(tl.p0 + min(n, tl.nr - 1)) * hu + (lane >> 5);
-        for (int q = w; q < I / 16; q += DN_WAVES) {
-            lds_load16(a.hhi + prow + 2 * q, &sA[0][64 * q]);
-            lds_load16(a.hlo + prow + 2 * q, &sA[1][64 * q]);
+        // the tile's SwiGLU rows (fp32, by pair) scaled by a power of two per
+        // row and split into hi/lo fp16 in LDS: element group v (8 floats)
+        // of pair row p0 + n is LDS unit 64 (16 (v / 32) + v % 16) + 32 ((v /
+        // 16) % 2) + n.  Wave w takes rows 4w .. 4w+3, 16 lanes a row, groups
+        // gl + 16 k of the row.
+        const int rw = 4 * w + (lane >> 4), gl = lane & 15;
+        const int ng = I / 8;
+        const float *hr = a.h + (size_t)(tl.p0 + min(rw, tl.nr - 1)) * a.Imax;
+        float4 va[4], vb[4];
+        float mx = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int v = gl + 16 * k;
+            va[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+            vb[k] = va[k];
+            if (v < ng) {
+                va[k] = *reinterpret_cast<const float4 *>(hr + 8 * v);
+                vb[k] = *reinterpret_cast<const float4 *>(hr + 8 * v + 4);
+            }
+            mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(va[k].x), fabsf(va[k].y)), fmaxf(fabsf(va[k].z), fabsf(va[k].w))),
+                                 fmaxf(fmaxf(fabsf(vb[k].x), fabsf(vb[k].y)), fmaxf(fabsf(vb[k].z), fabsf(vb[k].w)))));
         }
-        if (tid < MT) sexp[tid] = a.hexp[tl.p0 + min(tid, tl.nr - 1)];
+        mx = fmaxf(mx, dpp_f<0xB1>(mx));   // the 16 lanes of the row
+        mx = fmaxf(mx, dpp_f<0x4E>(mx));
+        mx = fmaxf(mx, dpp_f<0x141>(mx));
+        mx = fmaxf(mx, dpp_f<0x140>(mx));
+        const int e = row_exp(mx);
+        if (gl == 0) sexp[rw] = e;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int v = gl + 16 * k;
+            if (v < ng) {
+                const float x8[8] = {va[k].x, va[k].y, va[k].z, va[k].w, vb[k].x, vb[k].y, vb[k].z, vb[k].w};
+                uint4 hi, lo;
+                split8(x8, e, hi, lo);
+                const int u = 64 * (16 * (v >> 5) + (v & 15)) + 32 * ((v >> 4) & 1) + rw;
+                sA[0][u] = hi;
+                sA[1][u] = lo;
+            }
+        }
     }
-    wait_vmcnt<0>();
     __syncthreads();
 
     f32x16 acc;
@@ -874,10 +867,6 @@ int bread_grouped_alloc(bread_moe_ctx_t *c)
     if (e == hipSuccess) e = hipMalloc((void **)&g.work, NXCD * xt * (chunks_gu(s) + chunks_dn(s)) * sizeof(int));
     if (e == hipSuccess) e = hipMalloc((void **)&g.n_work, 2 * NXCD * sizeof(int));
     if (e == hipSuccess) e = hipMalloc((void **)&g.eo, P * H * sizeof(float));
-    const size_t Imax = (size_t)(s.expert_inter > s.shared_inter ? s.expert_inter : s.shared_inter);
-    if (e == hipSuccess) e = hipMalloc(&g.hhi, P * Imax * 2);
-    if (e == hipSuccess) e = hipMalloc(&g.hlo, P * Imax * 2);
-    if (e == hipSuccess) e = hipMalloc((void **)&g.hexp, P * sizeof(int));
     return e == hipSuccess ? BREAD_OK : (e == hipErrorOutOfMemory ? BREAD_ERR_NOMEM : BREAD_ERR_HIP);
 }
 
@@ -894,9 +883,6 @@ void bread_grouped_free(bread_moe_ctx_t *c)
     (void)hipFree(g.work);
     (void)hipFree(g.n_work);
     (void)hipFree(g.eo);
-    (void)hipFree(g.hhi);
-    (void)hipFree(g.hlo);
-    (void)hipFree(g.hexp);
     g = bread_grouped_ws{};
 }
 
@@ -960,15 +946,8 @@ int bread_launch_moe_grouped(bread_moe_ctx_t *c, const bread_moe_layer_t *L, con
     a.slots_gu = slots_gu;
     a.slots_dn = slots_dn;
     a.h = c->h;
-    a.hhi = (const uint4 *)g.hhi;
-    a.hlo = (const uint4 *)g.hlo;
-    a.hexp = g.hexp;
     a.eo = g.eo;
     hipLaunchKernelGGL(k_mt_gateup, dim3(NXCD * slots_gu), dim3(GU_WAVES * WAVE), 0, st, a);
-    BREAD_HIP(hipGetLastError());
-    const int rows = T * (K + 1);
-    hipLaunchKernelGGL(k_mt_hprep, dim3((rows + 3) / 4), dim3(256), 0, st, c->h, rows, T * K, s.expert_inter,
-                       s.shared_inter, Imax, (uint4 *)g.hhi, (uint4 *)g.hlo, g.hexp);
     BREAD_HIP(hipGetLastError());
     hipLaunchKernelGGL(k_mt_down, dim3(NXCD * slots_dn), dim3(DN_WAVES * WAVE), 0, st, a);
     BREAD_HIP(hipGetLastError());
