@@ -268,3 +268,14 @@ __device__ __forceinline__ T *uniform_ptr(T *p)
 {
     return reinterpret_cast<T *>(uniform64(reinterpret_cast<uint64_t>(p)));
 }
+
+constexpr uint32_t BUF_WORD3 = 0x00020000u;  // raw buffer descriptor word 3 (gfx9)
+
+// Raw buffer descriptor over [base, base + bytes): loads beyond the range
+// return zeros.  The base is made wave-uniform explicitly: a descriptor the
+// compiler keeps in vector registers costs a waterfall loop around every load.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(const_cast<void *>(base)), (short)0,
+                                             uniform((int)bytes), (int)BUF_WORD3);
+}

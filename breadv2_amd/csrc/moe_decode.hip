@@ -116,7 +116,6 @@ constexpr uint32_t SPIN_DEFAULT = 1u << 18;  // sleeps a bounded wait allows aft
 // and its tau and spread taken with this bound on |c - 1|; the recomputations
 // rebuild the reference's own x (ref_x).
 constexpr float CERT_KAPPA = 1.220703125e-4f;  // 2^-13 >= |c - 1|
-constexpr uint32_t BUF_WORD3 = 0x00020000u;  // raw buffer descriptor word 3 (gfx9)
 constexpr int AUX_COHERENT = 16;             // sc1: device-coherent access
 constexpr uint32_t SENTINEL = 0x7FA5A5A5u;   // signalling NaN: "not written yet"
 // Exchange layouts: every workgroup publishes into lines of its own, so a
@@ -241,14 +240,6 @@ struct Smem {
 static_assert(sizeof(Smem) > 80 * 1024 && sizeof(Smem) <= 160 * 1024, "LDS footprint");
 
 // ---------------------------------------------------------------- memory helpers
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_t bytes)
-{
-    // the base is made wave-uniform explicitly: a descriptor the compiler
-    // keeps in vector registers costs a waterfall loop around every load
-    return __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(const_cast<void *>(base)), (short)0,
-                                             uniform((int)bytes), (int)BUF_WORD3);
-}
 
 // An empty asm hides v's value from the optimiser, so per-lane address math
 // that depends on it is recomputed where it is used instead of being hoisted

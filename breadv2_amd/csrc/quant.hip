@@ -144,6 +144,105 @@ __global__ __launch_bounds__(256) void k_matvec_xr(const uint8_t *__restrict__ w
     }
 }
 
+// ---- Long Q4_K matvecs with fp16 x (the lm_head at fp16 I/O).  Four lanes
+// a superblock, lane j owning its 32 quant bytes 32j .. 32j+31: low nibbles
+// are elements 64j + [0, 32), high nibbles 64j + 32 + [0, 32), so each lane
+// decodes one scale pair per superblock for 64 weights.  One wave covers
+// 2 / NBL rows a slot (cols = 2048 NBL), four slots an iteration.  Every
+// nibble q becomes the fp16 1 + q/64 (bytes 0x3C and q << 4, placed by
+// v_perm_b32) and v_dot2_f32_f16 sums (1 + q/64) x against the lane's x pairs,
+// each product exact in fp32; sum q x = 64 (a - sum x).  Row offsets are
+// wave-uniform (scalar), the lane's offset in the slot fixed; raw buffer loads
+// return zeros past the matrix, so the last slots need no clamping (their
+// rows are not stored).
+template <typename YT, int NBL>
+__global__ __launch_bounds__(256) void k_matvec_q4h(const uint8_t *__restrict__ w, const uint16_t *__restrict__ x,
+                                                    YT *__restrict__ y, int rows, uint32_t row_bytes)
+{
+    constexpr int RS = 2 / NBL;  // rows a slot
+    constexpr int NS = 4;        // slots an iteration
+    constexpr int RPI = RS * NS;
+    const int lane = lane_id();
+    const int j = lane & 3;
+    const int b = (lane >> 2) & (8 * NBL - 1);
+    const int h = lane / (32 * NBL);
+    const int wv = uniform((int)((blockIdx.x * blockDim.x + threadIdx.x) / WAVE));
+    const int nw = (int)(gridDim.x * blockDim.x / WAVE);
+    uint32_t xl[16], xh[16];
+    float sl = 0.f, sh = 0.f;
+    {
+        const uint4 *xp = reinterpret_cast<const uint4 *>(x + QK * b + 64 * j);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint4 a = xp[i], c = xp[4 + i];
+            xl[4 * i] = a.x; xl[4 * i + 1] = a.y; xl[4 * i + 2] = a.z; xl[4 * i + 3] = a.w;
+            xh[4 * i] = c.x; xh[4 * i + 1] = c.y; xh[4 * i + 2] = c.z; xh[4 * i + 3] = c.w;
+        }
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            sl += h2f(xl[k]) + h2f(xl[k] >> 16);
+            sh += h2f(xh[k]) + h2f(xh[k] >> 16);
+        }
+    }
+    const auto wr = rsrc(w, (uint32_t)rows * row_bytes);
+    const int voff = (int)((uint32_t)h * row_bytes + (uint32_t)b * Q4K_BYTES);
+    // scale bytes of sub-blocks 2j, 2j + 1 (get_scale_min_k4): for j < 2 the
+    // low six bits of bytes 2j, 2j+1 (scales) and 2j+4, 2j+5 (mins); for
+    // j >= 2 the nibbles of bytes 2j+4, 2j+5 with the top two bits of bytes
+    // 2j-4, 2j-3 (scales) and 2j, 2j+1 (mins)
+    const bool jlo = j < 2;
+    const uint32_t sel_lo = 0x05040100u + 0x02020202u * (uint32_t)j;               // y[2j, 2j+1], z[2j, 2j+1]
+    const uint32_t sel_nb = 0x01000100u;
+    const uint32_t sel_hi = 0x01000100u + 0x02020202u * (uint32_t)(jlo ? 0 : j - 2) + 0x04040000u;  // y[2j-4, 2j-3], z[2j-4, 2j-3]
+    const int wsh = jlo ? 0 : 16 * (j - 2);
+    for (int r0 = wv * RPI; r0 < rows; r0 += nw * RPI) {
+        uint4 hd[NS], q0[NS], q1[NS];
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            // the whole offset in the vector operand: the range check covers it
+            const int o = voff + (int)((uint32_t)(r0 + RS * s) * row_bytes);
+            hd[s] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, o, 0, 0));
+            q0[s] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, o + 16 + 32 * j, 0, 0));
+            q1[s] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, o + 32 + 32 * j, 0, 0));
+        }
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            // [sc0, sc1, m0, m1], one byte each
+            uint32_t sm;
+            if (jlo) {
+                sm = __builtin_amdgcn_perm(hd[s].z, hd[s].y, sel_lo) & 0x3F3F3F3Fu;
+            } else {
+                const uint32_t n2 = (hd[s].w >> wsh) & 0xFFFFu;                     // bytes 2j+4, 2j+5
+                const uint32_t nb = __builtin_amdgcn_perm(0u, n2, sel_nb);          // [b0, b1, b0, b1]
+                const uint32_t lo4 = (nb & 0x00000F0Fu) | ((nb >> 4) & 0x0F0F0000u);
+                const uint32_t top = __builtin_amdgcn_perm(hd[s].z, hd[s].y, sel_hi);  // [2j-4, 2j-3, 2j, 2j+1]
+                sm = lo4 | ((top >> 2) & 0x30303030u);
+            }
+            const float d = h2f(hd[s].x), dmin = h2f(hd[s].x >> 16);
+            const uint32_t qw[8] = {q0[s].x, q0[s].y, q0[s].z, q0[s].w, q1[s].x, q1[s].y, q1[s].z, q1[s].w};
+            float al = 0.f, ah = 0.f;
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const uint32_t lo = (qw[t] << 4) & 0xF0F0F0F0u;
+                const uint32_t hi = qw[t] & 0xF0F0F0F0u;
+                al = __builtin_amdgcn_fdot2(__builtin_bit_cast(qd_half2, __builtin_amdgcn_perm(0x3C3C3C3Cu, lo, 0x04010400u)),
+                                            __builtin_bit_cast(qd_half2, xl[2 * t]), al, false);
+                al = __builtin_amdgcn_fdot2(__builtin_bit_cast(qd_half2, __builtin_amdgcn_perm(0x3C3C3C3Cu, lo, 0x04030402u)),
+                                            __builtin_bit_cast(qd_half2, xl[2 * t + 1]), al, false);
+                ah = __builtin_amdgcn_fdot2(__builtin_bit_cast(qd_half2, __builtin_amdgcn_perm(0x3C3C3C3Cu, hi, 0x04010400u)),
+                                            __builtin_bit_cast(qd_half2, xh[2 * t]), ah, false);
+                ah = __builtin_amdgcn_fdot2(__builtin_bit_cast(qd_half2, __builtin_amdgcn_perm(0x3C3C3C3Cu, hi, 0x04030402u)),
+                                            __builtin_bit_cast(qd_half2, xh[2 * t + 1]), ah, false);
+            }
+            float p = (d * (float)(sm & 0xFFu)) * (64.f * (al - sl)) - (dmin * (float)((sm >> 16) & 0xFFu)) * sl +
+                      (d * (float)((sm >> 8) & 0xFFu)) * (64.f * (ah - sh)) - (dmin * (float)(sm >> 24)) * sh;
+            p = NBL == 1 ? sum32(p) : wave_sum(p);
+            const int r = r0 + RS * s + h;
+            if ((lane & (32 * NBL - 1)) == 0 && r < rows) store_y(y, r, p);
+        }
+    }
+}
+
 // ---- bit-exact dequant: one thread per 8 consecutive output elements.
 // Operation order and roundings of dequant_q4k_cpu.c:111-121 / :155-165;
 // contraction is off so d1*q - m1 is a multiply then a subtract.
@@ -260,6 +359,18 @@ int launch_matvec(const void *w, const XT *x, YT *y, int rows, int cols, int qty
     // long matvecs with 2048 or 4096 columns: x held in registers, >= 4 rows
     // per wave (16 waves per CU)
     constexpr int XR_WAVES = 256 * 16;
+    if constexpr (std::is_same<XT, uint16_t>::value) {
+        // fp16 x, Q4_K: the dot2 kernel (32-bit buffer offsets: the matrix
+        // and the last iteration's rows past it below 4 GB)
+        if (rows >= 4 * XR_WAVES && (cols == 2048 || cols == 4096) && qtype == BREAD_QTYPE_Q4_K &&
+            ((uint64_t)rows + 16) * rb < (1ull << 32)) {
+            const dim3 g(XR_WAVES / 4), b(256);
+            if (cols == 2048) hipLaunchKernelGGL((k_matvec_q4h<YT, 1>), g, b, 0, st, wb, x, y, rows, (uint32_t)rb);
+            else hipLaunchKernelGGL((k_matvec_q4h<YT, 2>), g, b, 0, st, wb, x, y, rows, (uint32_t)rb);
+            BREAD_HIP(hipGetLastError());
+            return BREAD_OK;
+        }
+    }
     if (rows >= 4 * XR_WAVES && (cols == 2048 || cols == 4096) && qtype != BREAD_QTYPE_Q8_0) {
         const dim3 g(XR_WAVES / 4), b(256);
         if (qtype == BREAD_QTYPE_Q4_K) {

@@ -286,6 +286,8 @@ __device__ __forceinline__ float q4k_chunk_dot_sx(uint4 hd, uint4 q, uint32_t j,
            (dmin * (float)m1) * sh;
 }
 
+typedef _Float16 qd_half2 __attribute__((ext_vector_type(2)));
+
 // Activations in 16-bit block fixed point for the small-batch gate/up
 // kernel (H = 2048): per 32-column block s = max|x| / 32511 and x ~= s (256
 // hi + lo) with hi, lo signed bytes, plus fp32 sums of 16-column runs (the
