@@ -243,6 +243,101 @@ __global__ __launch_bounds__(256) void k_matvec_q4h(const uint8_t *__restrict__ 
     }
 }
 
+// ---- Long Q6_K matvecs with fp16 x.  Four lanes a superblock: lane j takes
+// half n = j / 2 and positions l = 16 (j % 2) + [0, 16) of it, i.e. the four
+// 16-element runs 128 n + 32 s + l (s = 0..3) with scales sc[8 n + j % 2 +
+// 2 s].  The 6-bit q of each weight becomes the fp16 1024 + q (bytes q, 0x64
+// by v_perm_b32), exact; v_dot2_f32_f16 sums (1024 + q) x per run and
+// sum (q - 32) x = a - 1056 sum x.  Superblocks are 210 bytes, so a lane's
+// ranges sit 2 bytes past a dword boundary for odd superblocks: each range is
+// loaded as aligned dwords plus one and realigned by v_alignbyte.  Slots,
+// scalar row offsets and range-checked buffer loads as k_matvec_q4h.
+template <typename YT, int NBL, int NS>
+__global__ __launch_bounds__(256) void k_matvec_q6h(const uint8_t *__restrict__ w, const uint16_t *__restrict__ x,
+                                                    YT *__restrict__ y, int rows, uint32_t row_bytes)
+{
+    constexpr int RS = 2 / NBL;  // rows a slot
+    constexpr int RPI = RS * NS;
+    const int lane = lane_id();
+    const int j = lane & 3, n = j >> 1, hf = j & 1;
+    const int b = (lane >> 2) & (8 * NBL - 1);
+    const int h = lane / (32 * NBL);
+    const int wv = uniform((int)((blockIdx.x * blockDim.x + threadIdx.x) / WAVE));
+    const int nw = (int)(gridDim.x * blockDim.x / WAVE);
+    uint32_t xs[4][8];
+    float X[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const uint4 *xp = reinterpret_cast<const uint4 *>(x + QK * b + 128 * n + 32 * r + 16 * hf);
+        const uint4 a = xp[0], c = xp[1];
+        xs[r][0] = a.x; xs[r][1] = a.y; xs[r][2] = a.z; xs[r][3] = a.w;
+        xs[r][4] = c.x; xs[r][5] = c.y; xs[r][6] = c.z; xs[r][7] = c.w;
+        X[r] = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) X[r] += h2f(xs[r][k]) + h2f(xs[r][k] >> 16);
+    }
+    const auto wr = rsrc(w, (uint32_t)rows * row_bytes);
+    const uint32_t sbo = (uint32_t)h * row_bytes + (uint32_t)b * Q6K_BYTES;
+    const uint32_t sh = sbo & 3u;  // realignment, bytes (0 or 2)
+    const int voff = (int)(sbo & ~3u);
+    auto ld5 = [&](int o, uint32_t (&v)[4]) {
+        const uint4 a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, o, 0, 0));
+        const uint32_t e = __builtin_amdgcn_raw_buffer_load_b32(wr, o + 16, 0, 0);
+        v[0] = __builtin_amdgcn_alignbyte(a.y, a.x, sh);
+        v[1] = __builtin_amdgcn_alignbyte(a.z, a.y, sh);
+        v[2] = __builtin_amdgcn_alignbyte(a.w, a.z, sh);
+        v[3] = __builtin_amdgcn_alignbyte(e, a.w, sh);
+    };
+    for (int r0 = wv * RPI; r0 < rows; r0 += nw * RPI) {
+        uint32_t qa[NS][4], qb[NS][4], qh[NS][4], sc[NS][2], dw[NS];
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            const int o = voff + (int)((uint32_t)(r0 + RS * s) * row_bytes);
+            ld5(o + 64 * n + 16 * hf, qa[s]);
+            ld5(o + 64 * n + 32 + 16 * hf, qb[s]);
+            ld5(o + 128 + 32 * n + 16 * hf, qh[s]);
+            const uint2 c2 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wr, o + 192 + 8 * n, 0, 0));
+            const uint32_t c3 = __builtin_amdgcn_raw_buffer_load_b32(wr, o + 200 + 8 * n, 0, 0);
+            sc[s][0] = __builtin_amdgcn_alignbyte(c2.y, c2.x, sh);
+            sc[s][1] = __builtin_amdgcn_alignbyte(c3, c2.y, sh);
+            dw[s] = __builtin_amdgcn_raw_buffer_load_b32(wr, o + 208, 0, 0) >> (8 * sh);
+        }
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const uint32_t a = qa[s][t], bq = qb[s][t], hq = qh[s][t];
+                const uint32_t q[4] = {(a & 0x0F0F0F0Fu) | ((hq << 4) & 0x30303030u),
+                                       (bq & 0x0F0F0F0Fu) | ((hq << 2) & 0x30303030u),
+                                       ((a >> 4) & 0x0F0F0F0Fu) | (hq & 0x30303030u),
+                                       ((bq >> 4) & 0x0F0F0F0Fu) | ((hq >> 2) & 0x30303030u)};
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    acc[r] = __builtin_amdgcn_fdot2(
+                        __builtin_bit_cast(qd_half2, __builtin_amdgcn_perm(0x64646464u, q[r], 0x04010400u)),
+                        __builtin_bit_cast(qd_half2, xs[r][2 * t]), acc[r], false);
+                    acc[r] = __builtin_amdgcn_fdot2(
+                        __builtin_bit_cast(qd_half2, __builtin_amdgcn_perm(0x64646464u, q[r], 0x04030402u)),
+                        __builtin_bit_cast(qd_half2, xs[r][2 * t + 1]), acc[r], false);
+                }
+            }
+            float p = 0.f;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                // scale byte hf + 2 r of the half's eight: bytes hf, hf+2 of
+                // the first word, then of the second
+                const int scv = (int)(int8_t)(sc[s][r >> 1] >> (8 * (hf + 2 * (r & 1))));
+                p = fmaf((float)scv, fmaf(-1056.f, X[r], acc[r]), p);
+            }
+            p *= h2f(dw[s]);
+            p = NBL == 1 ? sum32(p) : wave_sum(p);
+            const int rr = r0 + RS * s + h;
+            if ((lane & (32 * NBL - 1)) == 0 && rr < rows) store_y(y, rr, p);
+        }
+    }
+}
+
 // ---- bit-exact dequant: one thread per 8 consecutive output elements.
 // Operation order and roundings of dequant_q4k_cpu.c:111-121 / :155-165;
 // contraction is off so d1*q - m1 is a multiply then a subtract.
@@ -367,6 +462,14 @@ int launch_matvec(const void *w, const XT *x, YT *y, int rows, int cols, int qty
             const dim3 g(XR_WAVES / 4), b(256);
             if (cols == 2048) hipLaunchKernelGGL((k_matvec_q4h<YT, 1>), g, b, 0, st, wb, x, y, rows, (uint32_t)rb);
             else hipLaunchKernelGGL((k_matvec_q4h<YT, 2>), g, b, 0, st, wb, x, y, rows, (uint32_t)rb);
+            BREAD_HIP(hipGetLastError());
+            return BREAD_OK;
+        }
+        if (rows >= 4 * XR_WAVES && (cols == 2048 || cols == 4096) && qtype == BREAD_QTYPE_Q6_K &&
+            ((uint64_t)rows + 16) * rb < (1ull << 32)) {
+            const dim3 g(XR_WAVES / 4), b(256);
+            if (cols == 2048) hipLaunchKernelGGL((k_matvec_q6h<YT, 1, 2>), g, b, 0, st, wb, x, y, rows, (uint32_t)rb);
+            else hipLaunchKernelGGL((k_matvec_q6h<YT, 2, 2>), g, b, 0, st, wb, x, y, rows, (uint32_t)rb);
             BREAD_HIP(hipGetLastError());
             return BREAD_OK;
         }

@@ -156,7 +156,7 @@ def test_matvec_f32_parity(qtype, rows, cols):
 
 @pytest.mark.parametrize("qtype,rows,cols", [(Q4K, 512, 2048), (Q6K, 2048, 512), (Q80, 64, 2048), (Q4K, 9, 768),
                                              (Q4K, 20001, 2048), (Q4K, 16385, 4096), (Q4K, 16384, 2048),
-                                             (Q6K, 16385, 4096)])
+                                             (Q6K, 16385, 4096), (Q6K, 20001, 2048)])
 def test_matvec_f16_io(qtype, rows, cols):
     """bread_matvec fp16 I/O: equal to the oracle's fp16-rounded result up to
     one ulp plus the fp32 summation-order bound of test_matvec_f32_parity
