@@ -484,6 +484,18 @@ def verify(arena, s, rounds: int, stream):
     return out
 
 
+def calib_copy():
+    """One 512 MiB device copy: known bytes for scaling rocprofv3's FETCH_SIZE
+    and WRITE_SIZE."""
+    import torch
+
+    src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -502,6 +514,8 @@ def main() -> int:
                     help="profiling aid: run only the configs 4/5 cases and print their JSON")
     ap.add_argument("--only-head", action="store_true",
                     help="profiling aid: run only the batched greedy head timings and print their JSON")
+    ap.add_argument("--only-lm-head", action="store_true",
+                    help="profiling aid: run only the lm_head matvec timings (Q4_K, Q6_K) and print their JSON")
     ap.add_argument("--only-verify", action="store_true",
                     help="profiling aid: run only the speculative-verify rounds and print their JSON")
     ap.add_argument("--calib-copy", action="store_true",
@@ -522,6 +536,11 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.only_head:
         print(json.dumps({"greedy_head": greedy_head(20)}), flush=True)
+        return 0
+    if args.only_lm_head:
+        print(json.dumps({"lm_head": lm_head(20)}), flush=True)
+        if args.calib_copy:
+            calib_copy()
         return 0
     s = api.shape()
     L = args.layers
@@ -604,11 +623,7 @@ def main() -> int:
         raise RuntimeError("decode kernel flagged a device error")
     rstat = ctx.route_stats()
     if args.calib_copy:
-        src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda:0")
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        calib_copy()
     avg_us = sum(kern_us) / len(kern_us)
     med_us = kern_us[len(kern_us) // 2]
     log(f"moe kernel: avg {avg_us:.2f} us, median {med_us:.2f} us")
