@@ -175,6 +175,34 @@ def test_matvec_f16_io(qtype, rows, cols):
     assert np.max(np.abs(g32 - r32)) < 0.05 * max(1.0, float(np.max(np.abs(r32))))
 
 
+@pytest.mark.parametrize("qtype", [Q4K, Q6K])
+def test_lm_head_full_size_f16_io(qtype):
+    """The lm_head at its benchmark shape (248,320 x 2048, fp16 I/O, the
+    long-matvec kernels): every row computed on the device; the first and
+    last 1,024 rows (the kernel's first and last slots, the range-checked
+    loads past the matrix) and 4,096 random ones checked against the oracle
+    to the bound of test_matvec_f16_io."""
+    rows, cols = 248_320, 2048
+    rb = cols // 256 * (144 if qtype == Q4K else 210)
+    wd = torch.empty(rows * rb, dtype=torch.uint8, device=DEV)
+    (api.synth_q4k if qtype == Q4K else api.synth_q6k)(wd, rows * cols // 256, 77 + qtype)
+    x16 = np.random.default_rng(78).standard_normal(cols).astype(np.float16)
+    y = torch.empty(rows, dtype=torch.float16, device=DEV)
+    api.bread_matvec(wd, dev(x16), y, rows, cols, qtype)
+    got = y.cpu().numpy().astype(np.float32)
+    w = wd.cpu().numpy()
+    pick = np.unique(np.concatenate([np.arange(1024), np.arange(rows - 1024, rows),
+                                     np.random.default_rng(79).integers(0, rows, 4096)]))
+    wsel = w.reshape(rows, rb)[pick].reshape(-1)
+    n = pick.size
+    ref = O.matvec_f16io(wsel, qtype, x16.view(np.uint16), n, cols).view(np.float16).astype(np.float32)
+    ulp = np.spacing(np.abs(ref.astype(np.float16))).astype(np.float32)
+    order = 2 * cols * 2.0**-24 * abs_bound(wsel, qtype, x16.astype(np.float32), n, cols)
+    err = np.abs(got[pick] - ref)
+    assert np.all(err <= ulp + order + 1e-6), f"max excess {float(np.max(err - ulp - order))}"
+    assert np.all(np.isfinite(got))
+
+
 def test_matvec_zero_rows_is_noop():
     w = torch.zeros(144, dtype=torch.uint8, device=DEV)
     x = torch.zeros(256, dtype=torch.float32, device=DEV)
