@@ -254,24 +254,31 @@ __global__ __launch_bounds__(HD_THREADS) void k_head_q4k(const uint8_t *__restri
             const uint16_t h = f2h(v);
             logits[(size_t)t * vocab + 16 * ti + row] = h;
             // greedy_sample's order: the largest non-NaN value, the lowest
-            // index among equals
+            // index among equals; the lane's rows come in increasing order,
+            // so a strictly larger value replaces its best
             const float vf = h2f(h);
-            float bv = vf;
-            int bi = vf == vf ? 16 * ti + row : -1;
-#pragma unroll
-            for (int off = 8; off > 0; off >>= 1) {
-                const float ov = __shfl_xor(bv, off, 16);
-                const int oi = __shfl_xor(bi, off, 16);
-                if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
-                    bv = ov;
-                    bi = oi;
-                }
-            }
-            if (bi >= 0 && (besti[tt] < 0 || bv > best[tt])) {
-                best[tt] = bv;
-                besti[tt] = bi;
+            if (vf == vf && (besti[tt] < 0 || vf > best[tt])) {
+                best[tt] = vf;
+                besti[tt] = 16 * ti + row;
             }
         }
+    }
+#pragma unroll
+    for (int tt = 0; tt < NTT; tt++) {
+        // the 16 lanes of the token's row group: larger value, then lower index
+        float bv = best[tt];
+        int bi = besti[tt];
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off, 16);
+            const int oi = __shfl_xor(bi, off, 16);
+            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        best[tt] = bv;
+        besti[tt] = bi;
     }
 #pragma unroll
     for (int tt = 0; tt < NTT; tt++) {
