@@ -148,6 +148,27 @@ __device__ __forceinline__ float dpp_f(float v)
                                                                  0xF, 0xF, true));
 }
 
+// Inclusive prefix sum over the wave in lane order, all on DPP: row_shr 1,
+// 2, 4, 8 inside the 16-lane rows (lanes without a source add 0), then each
+// row's total into the rows after it (row_bcast 15 into rows 1 and 3,
+// row_bcast 31 into rows 2 and 3).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int dpp_i(int v)
+{
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWS, 0xF, true);
+}
+
+__device__ __forceinline__ int wave_scan_incl(int v)
+{
+    v += dpp_i<0x111, 0xF>(v);
+    v += dpp_i<0x112, 0xF>(v);
+    v += dpp_i<0x114, 0xF>(v);
+    v += dpp_i<0x118, 0xF>(v);
+    v += dpp_i<0x142, 0xA>(v);
+    v += dpp_i<0x143, 0xC>(v);
+    return v;
+}
+
 // Sum over aligned groups of 8 lanes; the result is in every lane of the group.
 __device__ __forceinline__ float sum8(float v)
 {

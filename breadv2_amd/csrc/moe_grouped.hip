@@ -344,15 +344,7 @@ __global__ __launch_bounds__(256) void k_mt_topk_xprep(const float *__restrict__
 __device__ __forceinline__ void block_scan2(int a, int b, int *wsa, int *wsb, int &xa, int &xb, int &ta, int &tb)
 {
     const int lane = lane_id(), w = threadIdx.x / WAVE, nw = blockDim.x / WAVE;
-    int ia = a, ib = b;
-#pragma unroll
-    for (int d = 1; d < WAVE; d <<= 1) {
-        const int oa = __shfl_up(ia, d), ob = __shfl_up(ib, d);
-        if (lane >= d) {
-            ia += oa;
-            ib += ob;
-        }
-    }
+    const int ia = wave_scan_incl(a), ib = wave_scan_incl(b);
     if (lane == WAVE - 1) {
         wsa[w] = ia;
         wsb[w] = ib;

@@ -117,11 +117,7 @@ __device__ void sb_number_slots(const int *sidx, int E, int K, int T, int32_t *_
     const int nsh = (T + SB_CH - 1) / SB_CH;
     const int ncnt = tid < E ? __popc(mask[tid]) : 0;
     const int nch = (ncnt + SB_CH - 1) / SB_CH;
-    int incl = nch;  // inclusive scan of the chunk counts over the experts
-    for (int off = 1; off < WAVE; off <<= 1) {
-        const int v = __shfl_up(incl, off);
-        if (lane >= off) incl += v;
-    }
+    const int incl = wave_scan_incl(nch);  // inclusive scan of the chunk counts over the experts
     if (lane == WAVE - 1) wave_tot[wv] = incl;
     __syncthreads();
     int before = 0;
