@@ -80,7 +80,8 @@ void bread_set_exit_on_error(int enable);
 /* y[r] = sum_c dequant(W[r,c]) * x[c] for r < rows.  x and y are fp16 bits
  * (the reference's `half`), accumulation is fp32, y is rounded to nearest
  * fp16.  qtype is 12 (Q4_K), 14 (Q6_K) or 8 (Q8_0); cols must be a multiple
- * of 256 (K-quants) or 32 (Q8_0).  w must be 4-byte aligned.
+ * of 256 (K-quants) or 32 (Q8_0).  w must be 4-byte aligned and x 16-byte
+ * aligned (BREAD_ERR_ALIGN otherwise).
  * Replaces kernels.cu:289-308 `void bread_matvec(void *w, half *x, half *y,
  * int rows, int cols, int qtype, cudaStream_t stream)`. */
 int bread_matvec(const void *w, const uint16_t *x, uint16_t *y, int rows, int cols,
