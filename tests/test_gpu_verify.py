@@ -237,6 +237,41 @@ def test_greedy_head_batched_q4k(T):
         assert int(t1.cpu().numpy()[0]) == tok[t]
 
 
+@pytest.mark.parametrize("T", [1, 17])
+def test_greedy_head_full_vocab_q4k(T):
+    """The batched head at the lm_head's real size (248,320 x 2048 Q4_K, about
+    60 tiles a workgroup): every token's argmax is greedy_sample over its
+    returned logits, and the first and last 512 rows plus 4,096 random ones
+    are within one fp16 ulp plus the fp32 order bound of the oracle's (h =
+    +-1 and fp16-exact norm weights give device and oracle the same x16)."""
+    s = api.shape()
+    H, vocab = s.hidden, 248_320
+    rng = np.random.default_rng(700 + T)
+    h = rng.choice([-1.0, 1.0], size=(T, H)).astype(np.float32)
+    nw = rng.choice([0.5, 0.75, 1.0, 1.25, 1.5], size=H).astype(np.float32)
+    rb = H // 256 * 144
+    wd = torch.empty(vocab * rb, dtype=torch.uint8, device=DEV)
+    api.synth_q4k(wd, vocab * H // 256, 710 + T)
+    ctx = B.MoeContext(s, max_tokens=T)
+    print(f"full-vocab head T={T}", flush=True)
+    tok, lg = ctx.greedy_head(dev(h), dev(nw), wd, Q4K, vocab, T)
+    torch.cuda.synchronize()
+    tok, lg = tok.cpu().numpy(), lg.cpu().numpy()
+    assert ctx.check_device() == 0
+    w = wd.cpu().numpy()
+    x16 = (h * nw[None]).astype(np.float16)
+    pick = np.unique(np.concatenate([np.arange(512), np.arange(vocab - 512, vocab),
+                                     rng.integers(0, vocab, 4096)]))
+    wsel = w.reshape(vocab, rb)[pick].reshape(-1)
+    for t in range(T):
+        assert tok[t] == O.greedy_f16(lg[t])
+        ref = O.matvec_f16io(wsel, Q4K, x16[t].view(np.uint16), pick.size, H).view(np.float16).astype(np.float64)
+        order = 2 * H * 2.0 ** -24 * abs_bound(wsel, Q4K, x16[t].astype(np.float32), pick.size, H)
+        err = np.abs(lg[t][pick].astype(np.float64) - ref)
+        assert np.all(err <= np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) + order + 1e-6), \
+            f"token {t}: max excess {float(np.max(err - order))}"
+
+
 def test_greedy_head_batched_nan_row():
     """greedy_sample keeps index 0 when logits[0] is NaN: a NaN input token
     gives an all-NaN row and token 0; the other tokens are unaffected."""
