@@ -32,16 +32,41 @@ __global__ __launch_bounds__(256) void k_norm_rows(const float *__restrict__ x, 
     __shared__ float part[4];
     const float *xt = x + (size_t)blockIdx.x * n;
     OT *ot = out + (size_t)blockIdx.x * n;
+    const int tid = (int)threadIdx.x;
+    // rows up to NRK * 256 elements stay in registers between the two
+    // passes (x and w requested together, one memory round trip); the
+    // arithmetic and its order are the same either way
+    constexpr int NRK = 8;
+    const bool held = n <= NRK * 256;
+    float xv[NRK], wv[NRK];
     float ss = 0.f;
-    for (int i = threadIdx.x; i < n; i += 256) ss = fmaf(xt[i], xt[i], ss);
+    if (held) {
+#pragma unroll
+        for (int k = 0; k < NRK; k++) {
+            const int i = tid + 256 * k;
+            xv[k] = i < n ? xt[i] : 0.f;
+            wv[k] = i < n && w ? w[i] : 1.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < NRK; k++)
+            if (tid + 256 * k < n) ss = fmaf(xv[k], xv[k], ss);
+    } else {
+        for (int i = tid; i < n; i += 256) ss = fmaf(xt[i], xt[i], ss);
+    }
     ss = wave_sum(ss);
-    if (lane_id() == 0) part[threadIdx.x / WAVE] = ss;
+    if (lane_id() == 0) part[tid / WAVE] = ss;
     __syncthreads();
     const float inv = 1.0f / sqrtf((part[0] + part[1] + part[2] + part[3]) / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += 256) {
-        const float v = xt[i] * inv * (w ? w[i] : 1.0f);
+    auto put = [&](int i, float v) {
         if constexpr (sizeof(OT) == 2) ot[i] = f2h(v);
         else ot[i] = v;
+    };
+    if (held) {
+#pragma unroll
+        for (int k = 0; k < NRK; k++)
+            if (tid + 256 * k < n) put(tid + 256 * k, xv[k] * inv * wv[k]);
+    } else {
+        for (int i = tid; i < n; i += 256) put(i, xt[i] * inv * (w ? w[i] : 1.0f));
     }
 }
 
